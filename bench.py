@@ -1,0 +1,356 @@
+"""Benchmark of the MI355X attention path on one GPU.
+
+Default workload: the Llama-3.2-3B-shaped configuration BASELINE.json quotes
+its targets on --
+  5b  decode: batch 64, 24 query / 8 KV heads, d 128, cache 16384, lengths
+      U[4096, 16383]; one step = RoPE + KV append + split-K attention;
+  5a  prefill: batch 1, 24 / 8 heads, d 128, seq 8192, causal.
+``value`` is the decode step's algorithmic HBM throughput (GB/s); the prefill
+figure (TFLOP/s) is reported in the ``prefill`` object.  Each carries a
+``roofline`` (events on the library stream around the attention kernels) and a
+``cpu_baseline`` (the NumPy oracle of the same attention on a bounded sample,
+timed on this host's cores).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 5|all|1|2|3|4|5a|5b]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "triton-llm_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "decode attn HBM GB/s + prefill attn TFLOP/s (% MI355X roofline), 1 GPU"
+HBM_PEAK_GBS = 8000.0
+PEAK_TFLOPS = {"bfloat16": 2516.6, "float16": 2516.6, "float32": 157.3}
+DT_SHORT = {"bfloat16": "bf16", "float16": "fp16", "float32": "fp32"}
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class Events:
+    """HIP event pairs on the library stream (via the C ABI)."""
+
+    def __init__(self, lib, n):
+        import ctypes
+
+        self.lib = lib
+        self.ev = []
+        for _ in range(n):
+            p = ctypes.c_void_p()
+            assert lib.tl_event_create(ctypes.byref(p)) == 0
+            self.ev.append(p)
+
+    def record(self, i):
+        assert self.lib.tl_event_record(self.ev[i], None) == 0
+
+    def ms(self, i, j):
+        import ctypes
+
+        out = ctypes.c_float()
+        assert self.lib.tl_event_synchronize(self.ev[j]) == 0
+        assert self.lib.tl_event_elapsed_ms(ctypes.byref(out), self.ev[i], self.ev[j]) == 0
+        return float(out.value)
+
+    def close(self):
+        for e in self.ev:
+            self.lib.tl_event_destroy(e)
+
+
+def cpu_threads():
+    n = os.environ.get("OMP_NUM_THREADS") or os.environ.get("OPENBLAS_NUM_THREADS")
+    try:
+        return int(n) if n else len(os.sched_getaffinity(0))
+    except Exception:
+        return os.cpu_count() or 1
+
+
+# ---------------------------------------------------------------------------
+# decode
+# ---------------------------------------------------------------------------
+
+def bench_decode(cfg, steps, warmup, replicas=1, cpu=True):
+    from oracle import attention as oa
+    from oracle import inputs as oi
+    from oracle import numerics as on
+    from triton_llm import gpu
+    from triton_llm.kernels import attention_decode, rope_kv_append
+    from triton_llm.kernels.decode import decode_workspace_bytes
+
+    dt = cfg.dtype
+    gdt = {"bfloat16": gpu.bfloat16, "float16": np.float16, "float32": np.float32}[dt]
+    t0 = time.perf_counter()
+    data = oi.make_decode(cfg, fill="zero")
+    log(f"{cfg.name}: inputs generated in {time.perf_counter() - t0:.1f}s")
+    lens = data["lens"]
+    B, Hq, Hkv, D = cfg.batch, cfg.n_head, cfg.n_kv_head, cfg.d_k
+    cos, sin = oi.rope_tables(cfg)
+    caches = []
+    for _ in range(replicas):  # rotate replicas so small caches are not served from MALL
+        caches.append((gpu.to_device(data["k_cache"], gdt), gpu.to_device(data["v_cache"], gdt)))
+    q = gpu.to_device(data["q"], gdt)
+    kn = gpu.to_device(data["k_new"], gdt)
+    vn = gpu.to_device(data["v_new"], gdt)
+    lens_d = gpu.to_device(lens)
+    cos_d = gpu.to_device(cos) if cos is not None else None
+    sin_d = gpu.to_device(sin) if sin is not None else None
+    out = gpu.allocate((B, Hq, D), gdt)
+    ws_bytes, split = decode_workspace_bytes(B, Hq, Hkv, cfg.max_ctx, D)
+    ws = gpu.allocate((ws_bytes,), np.uint8)
+    lib = gpu.runtime()
+
+    def step(i):
+        kc, vc = caches[i % replicas]
+        rope_kv_append(q, kn, vn, kc, vc, lens_d, cos_d, sin_d)
+        ev.record(3 * i + 1)
+        attention_decode(q, kc, vc, lens_d, Hq, Hkv, sm_scale=cfg.scale, len_add=1, out=out,
+                         workspace=ws, split=split)
+
+    ev = Events(lib, 3 * max(steps, warmup) + 3)
+    for i in range(warmup):
+        ev.record(3 * i)
+        step(i)
+        ev.record(3 * i + 2)
+    gpu.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev.record(3 * i)
+        step(i)
+        ev.record(3 * i + 2)
+    gpu.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    step_ms = [ev.ms(3 * i, 3 * i + 2) for i in range(steps)]
+    attn_ms = [ev.ms(3 * i + 1, 3 * i + 2) for i in range(steps)]
+    ev.close()
+
+    e = 4 if dt == "float32" else 2
+    step_bytes = oi.decode_bytes(cfg, lens)
+    attn_bytes = int(np.sum(2 * Hkv * (lens.astype(np.int64) + 1) * D * e)) + B * Hq * D * 2 * e
+    step_med = float(np.median(step_ms))
+    attn_med = float(np.median(attn_ms))
+    res = {
+        "value": step_bytes / (step_med * 1e-3) / 1e9,
+        "unit": "GB/s",
+        "ms_per_step": step_med,
+        "wall_ms_per_step": wall_ms,
+        "split": split,
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "decode_split_kernel + decode_combine_kernel (tl_attention_decode)",
+            "achieved": attn_bytes / (attn_med * 1e-3) / 1e9,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": attn_bytes / (attn_med * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "traffic": None,
+            "algorithmic_bytes": attn_bytes,
+            "kernel_ms": attn_med,
+        },
+    }
+    if cpu:
+        res["cpu_baseline"] = cpu_decode_baseline(cfg, data, oa, on)
+    return res
+
+
+def cpu_decode_baseline(cfg, data, oa, on, budget_s=15.0):
+    """NumPy fp32 decode attention on a bounded sample of sequences."""
+    dt = cfg.dtype
+    lens = data["lens"] + 1
+    B, Hkv, D = cfg.batch, cfg.n_kv_head, cfg.d_k
+    order = list(range(B))
+    # fp32 copies of the sampled sequences (conversion not timed)
+    done, t_total, nbytes = [], 0.0, 0
+    for b in order:
+        L = int(lens[b])
+        kf = on.from_storage(data["k_cache"][b:b + 1, :, :L], dt)
+        vf = on.from_storage(data["v_cache"][b:b + 1, :, :L], dt)
+        qf = on.from_storage(data["q"][b:b + 1], dt)
+        t0 = time.perf_counter()
+        oa.decode_ref(qf, kf, vf, np.array([L]), sm_scale=cfg.scale)
+        t_total += time.perf_counter() - t0
+        nbytes += 2 * Hkv * L * D * (4 if dt == "float32" else 2) + 2 * cfg.n_head * D * 2
+        done.append(b)
+        if t_total > budget_s:
+            break
+    return {
+        "value": nbytes / t_total / 1e9,
+        "unit": "GB/s",
+        "cores": cpu_threads(),
+        "kind": "port",
+        "sample": f"{len(done)} of {B} sequences ({int(np.sum(lens[done]))} positions), "
+                  f"NumPy fp32 oracle decode, {t_total:.2f}s; bytes counted as the GPU's "
+                  f"{DT_SHORT[dt]} K/V reads",
+    }
+
+
+# ---------------------------------------------------------------------------
+# prefill
+# ---------------------------------------------------------------------------
+
+def bench_prefill(cfg, steps, warmup, cpu=True):
+    from oracle import attention as oa
+    from oracle import inputs as oi
+    from oracle import numerics as on
+    from triton_llm import gpu
+    from triton_llm.kernels import apply_rope, flash_attention, precompute_cos_sin
+    from triton_llm.kernels.flash import flash_workspace_bytes
+
+    dt = cfg.dtype
+    gdt = {"bfloat16": gpu.bfloat16, "float16": np.float16, "float32": np.float32}[dt]
+    raw = oi.make_prefill_raw(cfg)
+    B, Hq, Hkv, S, D = cfg.batch, cfg.n_head, cfg.n_kv_head, cfg.seq, cfg.d_k
+    q = gpu.to_device(raw["q"], gdt)
+    k = gpu.to_device(raw["k"], gdt)
+    v = gpu.to_device(raw["v"], gdt)
+    if cfg.rope_theta is not None:
+        cos, sin = precompute_cos_sin(S, D, cfg.rope_theta)
+        cd, sd = gpu.to_device(cos), gpu.to_device(sin)
+        apply_rope(gpu.view(q, (B * Hq * S, D)), cd, sd, seq_len=S)
+        apply_rope(gpu.view(k, (B * Hkv * S, D)), cd, sd, seq_len=S)
+    out = gpu.allocate(q.shape, gdt)
+    wsb = flash_workspace_bytes(B, Hkv, S, D, gdt)
+    ws = gpu.allocate((max(wsb, 1),), np.uint8)
+    lib = gpu.runtime()
+    ev = Events(lib, 2 * max(steps, warmup) + 2)
+    for i in range(warmup):
+        flash_attention(q, k, v, causal=True, sm_scale=cfg.scale, out=out, workspace=ws)
+    gpu.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev.record(2 * i)
+        flash_attention(q, k, v, causal=True, sm_scale=cfg.scale, out=out, workspace=ws)
+        ev.record(2 * i + 1)
+    gpu.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    ms = float(np.median([ev.ms(2 * i, 2 * i + 1) for i in range(steps)]))
+    ev.close()
+    flops = oi.prefill_flops(cfg)
+    tf = flops / (ms * 1e-3) / 1e12
+    peak = PEAK_TFLOPS[dt]
+    res = {
+        "value": tf,
+        "unit": "TFLOP/s",
+        "ms_per_step": ms,
+        "wall_ms_per_step": wall_ms,
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "flash_fwd (+ V^T staging for 16-bit) (tl_attention_fwd)",
+            "achieved": tf,
+            "peak": peak,
+            "unit": "TFLOP/s",
+            "frac": tf / peak,
+            "traffic": None,
+            "algorithmic_flops": flops,
+            "kernel_ms": ms,
+        },
+    }
+    if cpu:
+        res["cpu_baseline"] = cpu_prefill_baseline(cfg, raw, oa, on)
+    return res
+
+
+def cpu_prefill_baseline(cfg, raw, oa, on, budget_s=15.0):
+    """NumPy fp32 causal attention on a bounded sample: one KV group, query
+    tiles of 512 rows taken from the end of the sequence (the longest rows)."""
+    dt = cfg.dtype
+    B, Hq, Hkv, S, D = cfg.batch, cfg.n_head, cfg.n_kv_head, cfg.seq, cfg.d_k
+    g = Hq // Hkv
+    q = on.from_storage(raw["q"][:1, :g], dt)
+    k = on.from_storage(raw["k"][:1, :1], dt)
+    v = on.from_storage(raw["v"][:1, :1], dt)
+    t_total, flops, tiles = 0.0, 0, 0
+    for start in range(max(0, S - 512), -1, -512):
+        rows = np.arange(start, min(S, start + 512))
+        t0 = time.perf_counter()
+        oa.attention_bhsd(q, k, v, causal=True, sm_scale=cfg.scale, rows=rows)
+        t_total += time.perf_counter() - t0
+        flops += int(np.sum(4 * g * D * (rows + 1)))
+        tiles += 1
+        if t_total > budget_s:
+            break
+    return {
+        "value": flops / t_total / 1e12,
+        "unit": "TFLOP/s",
+        "cores": cpu_threads(),
+        "kind": "port",
+        "sample": f"{tiles} x 512-row query tiles of 1 KV group ({g} heads), NumPy fp32 oracle, {t_total:.2f}s",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="5")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build measures one GPU only; the attention path does not "
+                                   "shard across GPUs (see DESIGN.md for how it would)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    from oracle import inputs as oi
+    from triton_llm import gpu
+
+    gpu.synchronize()  # initialise
+    cpu = not args.no_cpu
+    sel = {"5": ["5a", "5b"], "all": ["1", "2", "3", "4", "5a", "5b"]}.get(args.config, [args.config])
+    results = {}
+    for name in sel:
+        cfg = oi.CONFIGS[name]
+        log(f"config {name}: {cfg.name}")
+        if cfg.kind == "decode":
+            cache_mb = 2 * cfg.batch * cfg.n_kv_head * cfg.max_ctx * cfg.d_k * (4 if cfg.dtype == "float32" else 2) / 1e6
+            replicas = max(1, int(np.ceil(1024 / cache_mb))) if cache_mb < 1024 else 1
+            results[name] = bench_decode(cfg, args.steps, args.warmup, replicas=replicas, cpu=cpu)
+        else:
+            results[name] = bench_prefill(cfg, args.steps, args.warmup, cpu=cpu)
+        log(f"config {name}: {results[name]['value']:.1f} {results[name]['unit']} "
+            f"({results[name]['roofline']['frac'] * 100:.1f}% of roofline)")
+
+    head = "5b" if "5b" in results else sel[0]
+    r = results[head]
+    cfg = oi.CONFIGS[head]
+    line = {
+        "metric": METRIC,
+        "value": r["value"],
+        "unit": r["unit"],
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": r["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": DT_SHORT[cfg.dtype],
+        "data": "synthetic (seeded N(0,1) inputs, BASELINE.md recipe)",
+        "config": {
+            "workload": f"{cfg.name} (config {head})" + (" + llama3.2-3b-prefill-bf16 (config 5a)" if "5a" in results and head == "5b" else ""),
+            "batch": cfg.batch, "n_head": cfg.n_head, "n_kv_head": cfg.n_kv_head, "d_k": cfg.d_k,
+            "max_ctx": cfg.max_ctx or None, "seq": cfg.seq or None,
+        },
+        "roofline": r["roofline"],
+    }
+    if "cpu_baseline" in r:
+        line["cpu_baseline"] = r["cpu_baseline"]
+    if "5a" in results and head != "5a":
+        line["prefill"] = results["5a"]
+    if len(results) > 2 or (len(results) == 2 and "5a" not in results):
+        line["configs"] = results
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,156 @@
+/*
+ * triton_llm_hip.h -- C ABI of libtriton_llm_hip.so, the gfx950 (MI355X)
+ * attention path behind triton_llm's Python entry points.
+ *
+ * Every function returns an int status: 0 on success, otherwise a hipError_t
+ * value (argument errors use TL_ERR_INVALID = hipErrorInvalidValue, shapes the
+ * kernels do not cover use TL_ERR_UNSUPPORTED = hipErrorNotSupported).
+ * tl_error_string() turns a status into text.
+ *
+ * Conventions
+ *   - Pointers are device pointers unless named host_*.
+ *   - Strides are in ELEMENTS, as in the reference kernels
+ *     (triton_llm/kernels/attention.py:48-49 "Row strides in elements").
+ *     The head dimension is always contiguous (stride 1).
+ *   - `stream` NULL means the library's own stream (created by tl_init);
+ *     all launches and copies the Python layer issues go to that stream, so
+ *     stream order replaces the reference's per-call device synchronize.
+ *   - The library never allocates device memory on its own.  Scratch
+ *     ("workspace") is passed in by the caller, sized by the *_workspace_bytes
+ *     query functions.
+ *   - dtype codes: TL_DTYPE_F32, TL_DTYPE_F16, TL_DTYPE_BF16.  Softmax and
+ *     accumulation always run in fp32.
+ */
+#ifndef TRITON_LLM_HIP_H
+#define TRITON_LLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TL_DTYPE_F32 0
+#define TL_DTYPE_F16 1
+#define TL_DTYPE_BF16 2
+
+#define TL_ERR_INVALID 1       /* hipErrorInvalidValue */
+#define TL_ERR_UNSUPPORTED 801 /* hipErrorNotSupported */
+
+/* ---------------------------------------------------------------------------
+ * Runtime / allocator.  Replaces the ctypes bindings the reference's
+ * triton_llm/gpu.py makes directly on libamdhip64 / libcudart:
+ *   hipMalloc      gpu.py:120-121, :230-236   -> tl_malloc
+ *   hipFree        gpu.py:123-124, :194-200   -> tl_free
+ *   hipMemcpy H2D  gpu.py:215-224             -> tl_memcpy_htod (async on the
+ *                                                library stream + stream sync)
+ *   hipMemcpy D2H  gpu.py:202-213             -> tl_memcpy_dtoh (idem)
+ *   hipDeviceSynchronize gpu.py:252-263       -> tl_synchronize
+ *   backend probe  gpu.py:47-86               -> tl_device_count / tl_init
+ * ------------------------------------------------------------------------- */
+int tl_device_count(int* count);
+int tl_init(int device);
+void* tl_default_stream(void);
+int tl_malloc(void** ptr, size_t nbytes);
+int tl_free(void* ptr);
+int tl_memcpy_htod(void* dst, const void* host_src, size_t nbytes);
+int tl_memcpy_dtoh(void* host_dst, const void* src, size_t nbytes);
+int tl_memcpy_dtod(void* dst, const void* src, size_t nbytes);
+int tl_memset(void* dst, int value, size_t nbytes);
+int tl_synchronize(void);
+const char* tl_error_string(int status);
+
+/* Event timing (no counterpart in the reference, which times nothing below
+ * the Python wall clock; used by bench.py for per-kernel durations). */
+int tl_event_create(void** event);
+int tl_event_destroy(void* event);
+int tl_event_record(void* event, void* stream);
+int tl_event_synchronize(void* event);
+int tl_event_elapsed_ms(float* ms, void* start, void* stop);
+
+/* ---------------------------------------------------------------------------
+ * RoPE, in place.  Replaces apply_rope (triton_llm/kernels/rope.py:153-222)
+ * and its _rope_kernel (rope.py:25-70): half-split pairing (i, i + d_k/2),
+ * position = (row % seq_len) + position_offset, cos/sin tables half-packed
+ * fp32 (max_seq, d_k/2).  The rotation is evaluated as separately rounded
+ * fp32 multiplies and adds (no FMA contraction) and rounded once to the
+ * storage type, so results are bit-identical to the NumPy restatement.
+ * ------------------------------------------------------------------------- */
+int tl_rope_inplace(void* x, const float* cos_table, const float* sin_table,
+                    int64_t n_rows, int64_t row_stride, int d_k, int seq_len,
+                    int position_offset, int dtype, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Attention forward (prefill / general Sq x Sk).  Replaces
+ *   attention_gqa + _gqa_attention_kernel (attention_gqa.py:149-269, :21-146)
+ *   attention     + _attention_kernel     (attention.py:141-216, :18-138)
+ * Q: (batch, n_head, seq_q, d_k), K/V: (batch, n_kv_head, seq_k, d_k), O like Q,
+ * each given by {batch, head, seq} element strides.  Query head h reads KV head
+ * h / (n_head / n_kv_head) (attention_gqa.py:76).  causal != 0 masks key j for
+ * query i when j > i + (seq_k - seq_q) (bottom-right alignment,
+ * attention_gqa.py:97; equal to attention.py's top-left mask when
+ * seq_q == seq_k).  Scores are (q . k) * sm_scale.
+ * Requires seq_q >= 1, seq_k >= 1 (the Python layer returns the reference's
+ * empty/zero results itself).  Workspace: see tl_attention_fwd_workspace_bytes
+ * (it holds a key-major copy of V for the 16-bit MFMA path).
+ * ------------------------------------------------------------------------- */
+size_t tl_attention_fwd_workspace_bytes(int batch, int n_kv_head, int seq_k,
+                                        int d_k, int dtype);
+int tl_attention_fwd(const void* q, const void* k, const void* v, void* o,
+                     void* workspace, size_t workspace_bytes, int batch,
+                     int n_head, int n_kv_head, int seq_q, int seq_k, int d_k,
+                     const int64_t* q_strides, const int64_t* k_strides,
+                     const int64_t* v_strides, const int64_t* o_strides,
+                     float sm_scale, int causal, int dtype, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Single-token decode over a preallocated KV cache (split-K + log-sum-exp
+ * combine).  The reference does this with attention_gqa(q, K[:L], V[:L],
+ * causal=False) after re-uploading the cache prefix every step
+ * (smollm2_triton/model.py:299-314; gpt2_triton/model.py:332-349); here the
+ * cache stays resident and is read in place.
+ * Q/O: (batch, n_head, d_k) with {batch, head} strides.  Caches:
+ * (batch, n_kv_head, max_ctx, d_k) with {batch, head, seq} strides.
+ * Sequence b attends to positions [0, min(cache_lens[b] + len_add, max_ctx)).
+ * split_size: positions per split (multiple of 16); 0 picks a default.
+ * ------------------------------------------------------------------------- */
+int tl_decode_split_size(int batch, int n_kv_head, int max_ctx);
+size_t tl_attention_decode_workspace_bytes(int batch, int n_head, int max_ctx,
+                                           int d_k, int split_size);
+int tl_attention_decode(const void* q, const void* k_cache, const void* v_cache,
+                        const int32_t* cache_lens, int len_add, void* o,
+                        void* workspace, size_t workspace_bytes, int batch,
+                        int n_head, int n_kv_head, int max_ctx, int d_k,
+                        const int64_t* q_strides, const int64_t* k_strides,
+                        const int64_t* v_strides, const int64_t* o_strides,
+                        float sm_scale, int split_size, int dtype,
+                        void* stream);
+
+/* ---------------------------------------------------------------------------
+ * RoPE + KV-cache append, fused into the Q/K write.  Replaces the model's
+ * host-side sequence  apply_rope(q) ; apply_rope(k) ; k/v -> host ;
+ * cache[:, len] = k/v  (smollm2_triton/model.py:296-308 decode,
+ * :332-339 prefill; gpt2_triton/model.py:339-341 without RoPE).
+ * q: (batch, n_new, n_head, d_k) rotated in place (may be NULL);
+ * k_new / v_new: (batch, n_new, n_kv_head, d_k), read only;
+ * token s of sequence b is written to cache position cache_lens[b] + s, after
+ * RoPE at that position for q and k.  cos/sin NULL disables RoPE (GPT-2).
+ * Positions >= max_ctx (or >= rope_rows when RoPE is on) are not written.
+ * Strides: q/k_new/v_new {batch, seq, head}; caches {batch, head, seq}.
+ * ------------------------------------------------------------------------- */
+int tl_rope_kv_append(void* q, const void* k_new, const void* v_new,
+                      void* k_cache, void* v_cache, const int32_t* cache_lens,
+                      const float* cos_table, const float* sin_table,
+                      int rope_rows, int batch, int n_new, int n_head,
+                      int n_kv_head, int max_ctx, int d_k,
+                      const int64_t* q_strides, const int64_t* k_new_strides,
+                      const int64_t* v_new_strides,
+                      const int64_t* k_cache_strides,
+                      const int64_t* v_cache_strides, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TRITON_LLM_HIP_H */

@@ -1,0 +1,77 @@
+"""The C-ABI library: it loads, exports every function include/triton_llm_hip.h
+declares, and its host-only entry points (workspace sizing, argument checks)
+behave -- no kernel launch, no GPU needed."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from triton_llm import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "triton_llm_hip.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tl_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    declared = header_functions()
+    assert len(declared) >= 20
+    assert sorted(_lib.SIGNATURES) == declared
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in header_functions():
+        assert hasattr(lib, name), name
+
+
+def test_workspace_queries():
+    lib = _lib.load()
+    # fp32 needs no V^T copy; 16-bit needs B * Hkv * D * round_up(Sk, 64) * 2 bytes.
+    assert lib.tl_attention_fwd_workspace_bytes(1, 8, 8192, 128, _lib.DTYPE_F32) == 0
+    assert lib.tl_attention_fwd_workspace_bytes(1, 8, 8192, 128, _lib.DTYPE_BF16) == 8 * 128 * 8192 * 2
+    assert lib.tl_attention_fwd_workspace_bytes(2, 3, 100, 64, _lib.DTYPE_F16) == 2 * 3 * 64 * 128 * 2
+    split = lib.tl_decode_split_size(64, 8, 16384)
+    assert split % 16 == 0 and 64 <= split <= 2048
+    ws = lib.tl_attention_decode_workspace_bytes(64, 24, 16384, 128, split)
+    rows = 64 * 24 * ((16384 + split - 1) // split)
+    assert ws >= rows * (128 + 2) * 4
+    assert lib.tl_attention_decode_workspace_bytes(0, 24, 16384, 128, split) == 0
+
+
+def test_argument_errors_return_invalid_without_launching():
+    lib = _lib.load()
+    null = ctypes.c_void_p(None)
+    s3 = _lib.strides(0, 0, 0)
+    # NULL tensors -> TL_ERR_INVALID (1) before any HIP call.
+    st = lib.tl_attention_fwd(null, null, null, null, null, 0, 1, 2, 1, 4, 4, 64,
+                              s3, s3, s3, s3, 0.125, 1, _lib.DTYPE_BF16, None)
+    assert st == 1
+    # n_head not a multiple of n_kv_head.
+    st = lib.tl_attention_decode(null, null, null, null, 0, null, null, 0, 1, 3, 2, 16, 64,
+                                 s3, s3, s3, s3, 0.125, 0, _lib.DTYPE_BF16, None)
+    assert st == 1
+    # Empty work is a successful no-op.
+    assert lib.tl_rope_inplace(null, null, null, 0, 64, 64, 1, 0, _lib.DTYPE_F32, None) == 0
+    assert lib.tl_rope_inplace(null, null, null, 4, 64, 63, 1, 0, _lib.DTYPE_F32, None) == 1
+    assert lib.tl_rope_kv_append(null, null, null, null, null, null, null, null, 0, 0, 1, 1, 1, 8, 64,
+                                 s3, s3, s3, s3, s3, _lib.DTYPE_F32, None) == 0
+
+
+def test_error_string():
+    assert _lib.error_string(0) == "success"
+    assert isinstance(_lib.error_string(1), str)
+
+
+def test_missing_library_fails_loudly(monkeypatch):
+    monkeypatch.setenv("TRITON_LLM_HIP_LIB", "/nonexistent/libtriton_llm_hip.so")
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(RuntimeError, match="no CPU fallback|There is no CPU fallback"):
+        _lib.load()

@@ -1,0 +1,117 @@
+"""Decode over the resident KV cache (configs 2, 4, 5b and edge cases) against
+the oracle.  Positions past each sequence's length hold NaN, so any read of
+them would poison the output.  Tolerance: 2e-2 max-abs for 16-bit, 2e-3 fp32.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import attention as oa
+from oracle import inputs as oi
+from oracle import numerics as on
+from oracle import rope as orope
+from tests import _helpers as H
+from triton_llm import gpu
+from triton_llm.kernels import attention_decode, decode_step, precompute_cos_sin
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"float32": 2e-3, "float16": 2e-2, "bfloat16": 2e-2}
+
+
+def run_decode_step(cfg, data, batches=None, split=0):
+    """GPU: append (+RoPE) then attend over len + 1.  Oracle on the same inputs.
+
+    Returns (gpu_out_f32, oracle_out, appended caches from the GPU)."""
+    dt = cfg.dtype
+    B, Hq, Hkv, D = cfg.batch, cfg.n_head, cfg.n_kv_head, cfg.d_k
+    lens = data["lens"]
+    cos, sin = oi.rope_tables(cfg)
+    q_d = H.upload(data["q"], dt)
+    kc_d, vc_d = H.upload(data["k_cache"], dt), H.upload(data["v_cache"], dt)
+    lens_d = gpu.to_device(lens)
+    cos_d = gpu.to_device(cos) if cos is not None else None
+    sin_d = gpu.to_device(sin) if sin is not None else None
+    print(f"[case] {cfg.name} B={B} Hq={Hq} Hkv={Hkv} D={D} max_ctx={cfg.max_ctx} "
+          f"lens=[{lens.min()},{lens.max()}] split={split}", flush=True)
+    out_d = decode_step(q_d, H.upload(data["k_new"], dt), H.upload(data["v_new"], dt), kc_d, vc_d,
+                        lens_d, Hq, Hkv, cos_d, sin_d, sm_scale=cfg.scale, split=split)
+    got = on.from_storage(H.download(out_d), dt)
+
+    # Oracle: the same append on host storage, then attention over len + 1.
+    q = data["q"].copy()
+    kc, vc = data["k_cache"], data["v_cache"]
+    for b in range(B):
+        p = int(lens[b])
+        if cos is not None:
+            q[b] = orope.apply_rope_storage(data["q"][b], cos, sin, p, dt)
+            kc[b, :, p] = orope.apply_rope_storage(data["k_new"][b], cos, sin, p, dt)
+        else:
+            kc[b, :, p] = data["k_new"][b]
+        vc[b, :, p] = data["v_new"][b]
+    exp = oa.decode_ref(q, kc, vc, lens + 1, sm_scale=cfg.scale, dtype=dt, batches=batches)
+    return got, exp, kc_d, vc_d
+
+
+def compare(name, got, exp, tol, batches=None):
+    sel = slice(None) if batches is None else list(batches)
+    g, e = got[sel], exp[sel]
+    assert np.all(np.isfinite(got)), f"{name}: non-finite output"
+    err = H.max_abs(g, e)
+    H.report(name, err, tol)
+    assert err <= tol
+
+
+@pytest.mark.parametrize("name", ["2", "4"])
+def test_decode_config_full(name):
+    cfg = oi.CONFIGS[name]
+    data = oi.make_decode(cfg, fill="nan")
+    got, exp, kc_d, _ = run_decode_step(cfg, data)
+    compare(f"config{name}", got, exp, TOL[cfg.dtype])
+    # the GPU cache after the append equals the oracle's, bitwise, everywhere
+    np.testing.assert_array_equal(H.download(kc_d).view(np.uint16), data["k_cache"].view(np.uint16))
+
+
+def test_decode_config_5b_full_size_sampled():
+    cfg = oi.CONFIGS["5b"]
+    data = oi.make_decode(cfg, fill="nan")
+    lens = data["lens"]
+    batches = sorted(set(list(range(0, cfg.batch, 8)) + [int(np.argmax(lens)), int(np.argmin(lens))]))
+    got, exp, _, _ = run_decode_step(cfg, data, batches=batches)
+    compare("config5b", got, exp, TOL[cfg.dtype], batches)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+@pytest.mark.parametrize("group,d_k", [(1, 64), (3, 128), (4, 64), (8, 128), (12, 64)])
+def test_decode_shapes_and_dtypes(dtype, group, d_k):
+    Hkv = 2
+    cfg = oi.Config("decode-edge", "decode", dtype, 5, Hkv * group, Hkv, d_k, 11, 0.3,
+                    max_ctx=300, lo=0, hi=299, rope_theta=1e4)
+    lens = oi.draw_lens(cfg)
+    lens[:3] = [0, 299, 15]  # empty prefix, full cache, short
+    data = oi.make_decode(cfg, fill="nan", lens=lens)
+    got, exp, _, _ = run_decode_step(cfg, data, split=32)
+    compare(f"edge {dtype} g{group} d{d_k}", got, exp, TOL[dtype])
+
+
+def test_decode_without_append_and_len_zero_gives_zeros():
+    dt = "bfloat16"
+    cfg = oi.Config("decode-noappend", "decode", dt, 4, 6, 2, 64, 5, 0.125, max_ctx=128, lo=1, hi=127)
+    lens = oi.draw_lens(cfg)
+    lens[0] = 0
+    data = oi.make_decode(cfg, fill="nan", lens=lens)
+    lens_d = gpu.to_device(data["lens"])
+    out = attention_decode(H.upload(data["q"], dt), H.upload(data["k_cache"], dt), H.upload(data["v_cache"], dt),
+                           lens_d, 6, 2, sm_scale=0.125, len_add=0)
+    got = on.from_storage(H.download(out), dt)
+    exp = oa.decode_ref(data["q"], data["k_cache"], data["v_cache"], data["lens"], sm_scale=0.125, dtype=dt)
+    assert np.all(got[0] == 0)
+    compare("no-append", got, exp, TOL[dt])
+
+
+@pytest.mark.parametrize("split", [16, 64, 256, 2048])
+def test_decode_split_sizes_agree(split):
+    cfg = oi.scaled(oi.CONFIGS["4"], batch=6, max_ctx=2048, lo=1, hi=2047)
+    data = oi.make_decode(cfg, fill="nan")
+    got, exp, _, _ = run_decode_step(cfg, data, split=split)
+    compare(f"split{split}", got, exp, TOL[cfg.dtype])

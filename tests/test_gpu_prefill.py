@@ -1,0 +1,130 @@
+"""Flash prefill (configs 1, 3, 5a and edge shapes) against the oracle.
+
+Config 3 and 5a apply RoPE on the GPU (bit-exact, tested separately) to the
+raw rounded inputs, exactly as the oracle's input recipe does on the host.
+Tolerances: 2e-3 max-abs for fp32, 2e-2 for bf16/fp16.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import attention as oa
+from oracle import inputs as oi
+from oracle import numerics as on
+from tests import _helpers as H
+from triton_llm import gpu
+from triton_llm.kernels import apply_rope, flash_attention, flash_attention_strided, precompute_cos_sin
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"float32": 2e-3, "float16": 2e-2, "bfloat16": 2e-2}
+
+
+def gpu_prefill(cfg, raw, causal=True):
+    dt = cfg.dtype
+    B, Hq, Hkv, S, D = cfg.batch, cfg.n_head, cfg.n_kv_head, cfg.seq, cfg.d_k
+    print(f"[case] {cfg.name} B={B} Hq={Hq} Hkv={Hkv} S={S} D={D} {dt} causal={causal}", flush=True)
+    q_d, k_d, v_d = H.upload(raw["q"], dt), H.upload(raw["k"], dt), H.upload(raw["v"], dt)
+    if cfg.rope_theta is not None:
+        cos, sin = precompute_cos_sin(S, D, cfg.rope_theta)
+        cos_d, sin_d = gpu.to_device(cos), gpu.to_device(sin)
+        apply_rope(gpu.view(q_d, (B * Hq * S, D)), cos_d, sin_d, seq_len=S)
+        apply_rope(gpu.view(k_d, (B * Hkv * S, D)), cos_d, sin_d, seq_len=S)
+    o_d = flash_attention(q_d, k_d, v_d, causal=causal, sm_scale=cfg.scale)
+    return on.from_storage(H.download(o_d), dt)
+
+
+def compare(name, got, exp, tol):
+    err = H.max_abs(got, exp)
+    H.report(name, err, tol)
+    assert err <= tol
+
+
+@pytest.mark.parametrize("name", ["1", "3"])
+def test_prefill_config_full(name):
+    cfg = oi.CONFIGS[name]
+    got = gpu_prefill(cfg, oi.make_prefill_raw(cfg))
+    ref = oi.make_prefill(cfg)
+    exp = oa.attention_bhsd(ref["q"], ref["k"], ref["v"], causal=True, sm_scale=cfg.scale, dtype=cfg.dtype)
+    assert np.all(np.isfinite(got))
+    compare(f"config{name}", got, exp, TOL[cfg.dtype])
+
+
+def test_prefill_config_5a_full_size_sampled_rows():
+    cfg = oi.CONFIGS["5a"]
+    got = gpu_prefill(cfg, oi.make_prefill_raw(cfg))
+    assert np.all(np.isfinite(got))
+    ref = oi.make_prefill(cfg)
+    rows = np.unique(np.concatenate([np.arange(0, 8), np.arange(127, 136),
+                                     np.linspace(0, cfg.seq - 1, 48).astype(int),
+                                     np.arange(cfg.seq - 8, cfg.seq)]))
+    exp = oa.attention_bhsd(ref["q"], ref["k"], ref["v"], causal=True, sm_scale=cfg.scale,
+                            rows=rows, dtype=cfg.dtype)
+    compare("config5a(rows)", got[:, :, rows], exp[:, :, rows], TOL[cfg.dtype])
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+@pytest.mark.parametrize("d_k", [64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_ragged_shapes(dtype, d_k, causal):
+    # seq not a multiple of either tile size; GQA group 3; batch 2.
+    cfg = oi.Config("ragged", "prefill", dtype, 2, 6, 2, d_k, 21, 1 / np.sqrt(d_k), seq=200)
+    raw = oi.make_prefill_raw(cfg)
+    got = gpu_prefill(cfg, raw, causal=causal)
+    exp = oa.attention_bhsd(raw["q"], raw["k"], raw["v"], causal=causal, sm_scale=cfg.scale, dtype=dtype)
+    compare(f"ragged {dtype} d{d_k} causal={causal}", got, exp, TOL[dtype])
+
+
+@pytest.mark.parametrize("sq,sk", [(1, 1), (1, 300), (37, 300), (130, 129), (64, 64), (5, 3)])
+def test_prefill_seq_q_ne_seq_k(sq, sk):
+    """Bottom-right causal alignment; sq > sk leaves the first rows fully masked (NaN)."""
+    dt = "bfloat16"
+    rng = np.random.default_rng(sq * 1000 + sk)
+    B, Hq, Hkv, D = 1, 4, 2, 64
+    q = on.to_storage(rng.standard_normal((B, Hq, sq, D), dtype=np.float32), dt)
+    k = on.to_storage(rng.standard_normal((B, Hkv, sk, D), dtype=np.float32), dt)
+    v = on.to_storage(rng.standard_normal((B, Hkv, sk, D), dtype=np.float32), dt)
+    o = flash_attention(H.upload(q, dt), H.upload(k, dt), H.upload(v, dt), causal=True)
+    got = on.from_storage(H.download(o), dt)
+    exp = oa.attention_bhsd(q, k, v, causal=True, dtype=dt)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(exp))
+    compare(f"sq{sq} sk{sk}", np.nan_to_num(got), np.nan_to_num(exp), TOL[dt])
+
+
+@pytest.mark.parametrize("d_k", [16, 32, 256])
+def test_prefill_generic_head_sizes(d_k):
+    dt = "float32"
+    cfg = oi.Config("generic", "prefill", dt, 1, 4, 2, d_k, 5, 1 / np.sqrt(d_k), seq=70)
+    raw = oi.make_prefill_raw(cfg)
+    got = gpu_prefill(cfg, raw)
+    exp = oa.attention_bhsd(raw["q"], raw["k"], raw["v"], causal=True, sm_scale=cfg.scale)
+    compare(f"generic d{d_k}", got, exp, TOL[dt])
+
+
+@pytest.mark.parametrize("group", [1, 2, 3, 4, 8])
+def test_prefill_gqa_groups(group):
+    dt = "bfloat16"
+    cfg = oi.Config("groups", "prefill", dt, 1, 2 * group, 2, 128, 30 + group, 0.088, seq=256)
+    raw = oi.make_prefill_raw(cfg)
+    got = gpu_prefill(cfg, raw)
+    exp = oa.attention_bhsd(raw["q"], raw["k"], raw["v"], causal=True, sm_scale=cfg.scale, dtype=dt)
+    compare(f"group{group}", got, exp, TOL[dt])
+
+
+def test_prefill_reads_cache_layout_and_seq_major_rows():
+    """K/V straight from a (B, Hkv, max_ctx, D) cache; Q and O as (B, S, Hq*D) rows."""
+    dt = "bfloat16"
+    rng = np.random.default_rng(3)
+    B, Hq, Hkv, S, D, C = 2, 6, 2, 150, 64, 512
+    q_rows = on.to_storage(rng.standard_normal((B, S, Hq, D), dtype=np.float32), dt)
+    kc = on.to_storage(rng.standard_normal((B, Hkv, C, D), dtype=np.float32), dt)
+    vc = on.to_storage(rng.standard_normal((B, Hkv, C, D), dtype=np.float32), dt)
+    q_d, kc_d, vc_d = H.upload(q_rows, dt), H.upload(kc, dt), H.upload(vc, dt)
+    o_d = gpu.allocate((B, S, Hq, D), gpu.bfloat16)
+    flash_attention_strided(
+        q_d, kc_d, vc_d, o_d, batch=B, n_head=Hq, n_kv_head=Hkv, seq_q=S, seq_k=S, d_k=D,
+        q_strides=(S * Hq * D, D, Hq * D), k_strides=(Hkv * C * D, C * D, D),
+        v_strides=(Hkv * C * D, C * D, D), o_strides=(S * Hq * D, D, Hq * D), causal=True)
+    got = on.from_storage(H.download(o_d), dt).transpose(0, 2, 1, 3)
+    exp = oa.attention_bhsd(q_rows.transpose(0, 2, 1, 3), kc[:, :, :S], vc[:, :, :S], causal=True, dtype=dt)
+    compare("cache-layout", got, exp, TOL[dt])

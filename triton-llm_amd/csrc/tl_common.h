@@ -1,0 +1,122 @@
+// Shared device/host helpers for the gfx950 attention library.
+//
+// Element types are tagged by the same integer codes the C ABI uses
+// (TL_DTYPE_F32 / TL_DTYPE_F16 / TL_DTYPE_BF16).  All arithmetic that feeds
+// softmax or accumulation runs in fp32; 16-bit types are storage formats.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/triton_llm_hip.h"
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Storage type tags.  `bits` is the raw 16/32-bit pattern type.
+struct F32 {
+  using bits = uint32_t;
+  static constexpr int code = TL_DTYPE_F32;
+  static constexpr int size = 4;
+};
+struct F16 {
+  using bits = uint16_t;
+  static constexpr int code = TL_DTYPE_F16;
+  static constexpr int size = 2;
+};
+struct BF16 {
+  using bits = uint16_t;
+  static constexpr int code = TL_DTYPE_BF16;
+  static constexpr int size = 2;
+};
+
+// ---- scalar conversions -------------------------------------------------
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
+  return __uint_as_float(b << 16);
+}
+
+// fp32 -> bf16 with round-to-nearest-even on the bit pattern.  NaN maps to a
+// quiet NaN that keeps the sign (0x7FC0 | sign), the convention the host
+// oracle uses, so stores of rounded values are bit-exact against it.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return ((u >> 16) & 0x8000u) | 0x7FC0u;
+  uint32_t bias = 0x7FFFu + ((u >> 16) & 1u);
+  return (u + bias) >> 16;
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t b) {
+  _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)b);
+  return (float)h;
+}
+
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  _Float16 h = (_Float16)f;  // v_cvt_f16_f32, round-to-nearest-even
+  return (uint32_t)__builtin_bit_cast(uint16_t, h);
+}
+
+template <typename T>
+__device__ __forceinline__ float to_f32(typename T::bits b);
+template <>
+__device__ __forceinline__ float to_f32<F32>(uint32_t b) { return __uint_as_float(b); }
+template <>
+__device__ __forceinline__ float to_f32<F16>(uint16_t b) { return f16_bits_to_f32(b); }
+template <>
+__device__ __forceinline__ float to_f32<BF16>(uint16_t b) { return bf16_bits_to_f32(b); }
+
+template <typename T>
+__device__ __forceinline__ typename T::bits from_f32(float f);
+template <>
+__device__ __forceinline__ uint32_t from_f32<F32>(float f) { return __float_as_uint(f); }
+template <>
+__device__ __forceinline__ uint16_t from_f32<F16>(float f) { return (uint16_t)f32_to_f16_bits(f); }
+template <>
+__device__ __forceinline__ uint16_t from_f32<BF16>(float f) { return (uint16_t)f32_to_bf16_bits_rne(f); }
+
+// Unpack a 32-bit word holding two 16-bit values (low half first).
+template <typename T>
+__device__ __forceinline__ void unpack2(uint32_t w, float& lo, float& hi);
+template <>
+__device__ __forceinline__ void unpack2<BF16>(uint32_t w, float& lo, float& hi) {
+  lo = __uint_as_float(w << 16);
+  hi = __uint_as_float(w & 0xFFFF0000u);
+}
+template <>
+__device__ __forceinline__ void unpack2<F16>(uint32_t w, float& lo, float& hi) {
+  lo = f16_bits_to_f32(w & 0xFFFFu);
+  hi = f16_bits_to_f32(w >> 16);
+}
+
+// ---- DPP cross-lane helpers (rows of 16 lanes) --------------------------
+// dpp_ctrl encodings (GCN/CDNA DPP): row_ror:n = 0x120 + n.
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 16 lanes of a DPP row; every lane of the row receives the sum.
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_mov<0x128>(x);  // row_ror:8
+  x += dpp_mov<0x124>(x);  // row_ror:4
+  x += dpp_mov<0x122>(x);  // row_ror:2
+  x += dpp_mov<0x121>(x);  // row_ror:1
+  return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Status returned by launch wrappers: the HIP error of the launch (0 = ok).
+static inline int tl_launch_status() { return (int)hipGetLastError(); }
+
+// Resolve the stream argument of an entry point: NULL means the library stream.
+hipStream_t tl_resolve_stream(void* stream);

@@ -1,0 +1,711 @@
+// Attention forward for prefill (any seq_q x seq_k, MHA and GQA, causal or
+// not) on gfx950 matrix cores.
+//
+// Reference semantics (triton_llm/kernels/attention_gqa.py:21-146): query row
+// i of head h attends to keys j of KV head h / group with j <= i + (Sk - Sq)
+// when causal; scores are (q . k) * sm_scale; online softmax over key tiles;
+// output = acc / row_sum.  The reference runs one program per (row, head)
+// with vector multiply-reduce; this kernel is a flash-style tiled kernel on
+// MFMA:
+//
+//   workgroup = 4 waves = BM = 128 query rows of one query head;
+//   each wave owns 32 query rows; key tiles of BN = 64 staged through LDS.
+//
+// It computes the TRANSPOSED products  S^T = K . Q^T  and  O^T = V^T . P^T
+// with 32x32 MFMA tiles.  In the 32x32 accumulator layout lane l holds
+// column n = l % 32 and 16 rows; with the transposed products column n is a
+// query row, so every lane owns exactly one query row: the row max needs one
+// exchange between lane l and l ^ 32, the row sum is kept per lane and merged
+// once at the end, and the O rescale is a per-lane scalar.
+//
+// MFMA operand layouts used (gfx950, wave64):
+//   32x32x16 (f16/bf16): A lane l = A[l%32][8*(l/32) + 0..7],
+//                        B lane l = B[8*(l/32) + 0..7][l%32],
+//                        C lane l, reg r = C[8*(r/4) + 4*(l/32) + r%4][l%32].
+//   32x32x2  (f32):      A lane l = A[l%32][l/32], B lane l = B[l/32][l%32],
+//                        same C layout.
+// The reduction index of one MFMA may be any permutation as long as A and B
+// agree; the P^T operand is taken straight from the S^T accumulator
+// registers and the V^T operand is read with the matching key permutation.
+//
+// 16-bit inputs read V through a key-major copy V^T [b][kv][d][Sk_pad]
+// (written by vt_transpose_kernel into the caller's workspace) so that a
+// lane's 8 consecutive keys for one d are two 8-byte LDS reads.  fp32 reads
+// V in its natural layout (one element per lane per MFMA).
+#include "tl_common.h"
+
+#include <math.h>
+
+namespace {
+
+constexpr int BM = 128;  // query rows per workgroup
+constexpr int BN = 64;   // keys per tile
+constexpr int kThreads = 256;
+
+struct FlashParams {
+  const void* q;
+  const void* k;
+  const void* v;   // natural V (fp32 path)
+  const void* vt;  // key-major V^T (16-bit path)
+  void* o;
+  int batch, n_head, n_kv, group, seq_q, seq_k, sk_pad, n_qt;
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_sh, o_ss;
+  float scale_log2;
+};
+
+template <typename T>
+struct Mfma;
+
+template <>
+struct Mfma<BF16> {
+  typedef bf16x8 frag;
+  static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ frag pack(const float* x) {
+    frag r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = (__bf16)x[i];
+    return r;
+  }
+};
+
+template <>
+struct Mfma<F16> {
+  typedef f16x8 frag;
+  static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ frag pack(const float* x) {
+    frag r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = (_Float16)x[i];
+    return r;
+  }
+};
+
+__device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32); }
+
+// Map the linear block id so that each XCD (blocks are dealt round-robin to
+// the 8 XCDs) receives a contiguous range of work items, i.e. the same KV
+// head, and inside it the longest causal rows first.
+__device__ __forceinline__ void decode_block(const FlashParams& p, int& b, int& hq, int& qt) {
+  const int L = blockIdx.x;
+  const int N = gridDim.x;
+  const int w = (N % 8 == 0) ? (L % 8) * (N / 8) + L / 8 : L;
+  // w = ((b * n_kv + hkv) * n_qt + (n_qt - 1 - qt)) * group + g
+  const int g = w % p.group;
+  int rest = w / p.group;
+  const int qt_rev = rest % p.n_qt;
+  rest /= p.n_qt;
+  const int hkv = rest % p.n_kv;
+  b = rest / p.n_kv;
+  qt = p.n_qt - 1 - qt_rev;
+  hq = hkv * p.group + g;
+}
+
+// ---------------------------------------------------------------------------
+// 16-bit (f16 / bf16) kernel.
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(kThreads, 2) void flash_fwd_16(FlashParams p) {
+  using M = Mfma<T>;
+  using frag = typename M::frag;
+  using Bits = typename T::bits;
+  constexpr int KROW = D * 2 + 16;   // bytes per K row in LDS (16 B pad)
+  constexpr int VROW = BN * 2 + 8;   // bytes per V^T row in LDS (8 B pad)
+  constexpr int K_CPR = D * 2 / 16;  // 16-byte chunks per K row
+  constexpr int K_CHUNKS = BN * K_CPR / kThreads;
+  constexpr int V_CPR = BN * 2 / 16;  // 16-byte chunks per V^T row (= 8)
+  constexpr int V_CHUNKS = D * V_CPR / kThreads;
+  constexpr int NDB = D / 32;  // 32-row blocks of O^T
+  constexpr int NKS = D / 16;  // k-steps of S^T
+  static_assert(K_CHUNKS * kThreads == BN * K_CPR, "K tile split");
+  static_assert(V_CHUNKS * kThreads == D * V_CPR, "V tile split");
+
+  __shared__ __attribute__((aligned(16))) char smem[BN * KROW + D * VROW];
+  char* Ks = smem;
+  char* Vs = smem + BN * KROW;
+
+  int b, hq, qt;
+  decode_block(p, b, hq, qt);
+  const int hkv = hq / p.group;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int lq = lane & 31;
+  const int h = lane >> 5;
+  const int off = p.seq_k - p.seq_q;  // bottom-right causal offset
+
+  const int q_first = qt * BM;
+  const int q_last = min(p.seq_q, q_first + BM) - 1;
+  int k_end = p.seq_k;
+  if (CAUSAL) k_end = max(0, min(p.seq_k, q_last + off + 1));
+  const int n_kt = (k_end + BN - 1) / BN;
+
+  const int q0 = q_first + wave * 32;  // first row of this wave
+  const int qi = q0 + lq;              // this lane's query row
+  int wave_k_end = p.seq_k;
+  if (CAUSAL) wave_k_end = max(0, min(p.seq_k, min(q0 + 31, p.seq_q - 1) + off + 1));
+
+  // Q^T operand: lane holds Q[qi][16ks + 8h .. +7] for every k-step.
+  frag qf[NKS];
+  {
+    const Bits* qrow = (const Bits*)p.q + b * p.q_sb + hq * p.q_sh + (int64_t)qi * p.q_ss;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      u32x4 raw = {0u, 0u, 0u, 0u};
+      if (qi < p.seq_q) raw = *(const u32x4*)(qrow + 16 * ks + 8 * h);
+      qf[ks] = __builtin_bit_cast(frag, raw);
+    }
+  }
+
+  f32x16 o_acc[NDB];
+#pragma unroll
+  for (int i = 0; i < NDB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o_acc[i][r] = 0.f;
+  float m_run = -INFINITY;
+  float l_run = 0.f;  // this lane's half of the row sum
+
+  const Bits* kbase = (const Bits*)p.k + b * p.k_sb + hkv * p.k_sh;
+  const Bits* vtbase = (const Bits*)p.vt + ((int64_t)b * p.n_kv + hkv) * D * p.sk_pad;
+  u32x4 kreg[K_CHUNKS], vreg[V_CHUNKS];
+
+  auto load_tile = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < K_CHUNKS; ++i) {
+      const int c = tid + kThreads * i;
+      const int row = c / K_CPR;
+      const int col = c % K_CPR;
+      const int key = kt * BN + row;
+      u32x4 z = {0u, 0u, 0u, 0u};
+      kreg[i] = key < p.seq_k ? *(const u32x4*)(kbase + (int64_t)key * p.k_ss + col * 8) : z;
+    }
+#pragma unroll
+    for (int i = 0; i < V_CHUNKS; ++i) {
+      const int c = tid + kThreads * i;
+      const int d = c / V_CPR;
+      const int col = c % V_CPR;
+      vreg[i] = *(const u32x4*)(vtbase + (int64_t)d * p.sk_pad + kt * BN + col * 8);
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int i = 0; i < K_CHUNKS; ++i) {
+      const int c = tid + kThreads * i;
+      const int row = c / K_CPR;
+      const int col = c % K_CPR;
+      *(u32x4*)(Ks + row * KROW + col * 16) = kreg[i];
+    }
+#pragma unroll
+    for (int i = 0; i < V_CHUNKS; ++i) {
+      const int c = tid + kThreads * i;
+      const int d = c / V_CPR;
+      const int col = c % V_CPR;
+      u32x2* dst = (u32x2*)(Vs + d * VROW + col * 16);
+      dst[0] = u32x2{vreg[i].x, vreg[i].y};
+      dst[1] = u32x2{vreg[i].z, vreg[i].w};
+    }
+  };
+
+  const float c = p.scale_log2;
+  if (n_kt > 0) load_tile(0);
+  for (int kt = 0; kt < n_kt; ++kt) {
+    if (kt > 0) __syncthreads();
+    store_tile();
+    __syncthreads();
+    if (kt + 1 < n_kt) load_tile(kt + 1);
+
+    const int kb = kt * BN;
+    if (kb >= wave_k_end) continue;  // whole tile masked for this wave
+
+    // S^T = K . Q^T for two 32-key blocks.
+    f32x16 s[2];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[mb][r] = 0.f;
+      const char* krow = Ks + (32 * mb + lq) * KROW + 16 * h;
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        frag a = __builtin_bit_cast(frag, *(const u32x4*)(krow + 32 * ks));
+        s[mb] = M::mma(a, qf[ks], s[mb]);
+      }
+    }
+
+    const bool need_mask = (kb + BN > p.seq_k) || (CAUSAL && kb + BN - 1 > q0 + off);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = s[mb][r] * c;
+        if (need_mask) {
+          const int key = kb + 32 * mb + 8 * (r >> 2) + 4 * h + (r & 3);
+          const bool ok = key < p.seq_k && (!CAUSAL || key <= qi + off);
+          x = ok ? x : -INFINITY;
+        }
+        s[mb][r] = x;
+        mx = fmaxf(mx, x);
+      }
+    }
+    mx = fmaxf(mx, xor32(mx));
+    const float m_new = fmaxf(m_run, mx);
+    const float base = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = fast_exp2(m_run - base);
+    m_run = m_new;
+    if (__any(alpha != 1.f)) {
+      l_run *= alpha;
+#pragma unroll
+      for (int i = 0; i < NDB; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o_acc[i][r] *= alpha;
+    }
+    float psum = 0.f;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float e = fast_exp2(s[mb][r] - base);
+        s[mb][r] = e;
+        psum += e;
+      }
+    l_run += psum;
+
+    // O^T += V^T . P^T, 16 keys per MFMA.
+#pragma unroll
+    for (int t = 0; t < BN / 16; ++t) {
+      const int mb = t >> 1;
+      const int tp = t & 1;
+      float pv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pv[j] = s[mb][8 * tp + j];
+      const frag pb = M::pack(pv);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const char* vrow = Vs + (32 * db + lq) * VROW + (16 * t + 4 * h) * 2;
+        const u32x2 lo = *(const u32x2*)vrow;
+        const u32x2 hi = *(const u32x2*)(vrow + 16);
+        const u32x4 raw = {lo.x, lo.y, hi.x, hi.y};
+        o_acc[db] = M::mma(__builtin_bit_cast(frag, raw), pb, o_acc[db]);
+      }
+    }
+  }
+
+  // Epilogue: O[qi][d] = O^T[d][qi] / l.
+  const float l_tot = l_run + xor32(l_run);
+  const float inv = 1.f / l_tot;
+  if (qi < p.seq_q) {
+    Bits* orow = (Bits*)p.o + b * p.o_sb + hq * p.o_sh + (int64_t)qi * p.o_ss;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d0 = 32 * db + 8 * rq + 4 * h;
+        uint32_t w0 = (uint32_t)from_f32<T>(o_acc[db][4 * rq + 0] * inv) |
+                      ((uint32_t)from_f32<T>(o_acc[db][4 * rq + 1] * inv) << 16);
+        uint32_t w1 = (uint32_t)from_f32<T>(o_acc[db][4 * rq + 2] * inv) |
+                      ((uint32_t)from_f32<T>(o_acc[db][4 * rq + 3] * inv) << 16);
+        *(u32x2*)(orow + d0) = u32x2{w0, w1};
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// fp32 kernel (v_mfma_f32_32x32x2_f32).  K-step mapping for S^T: lane half h
+// covers d = h*D/2 + 4c + i for step (c, i), so both K (LDS) and Q (global)
+// are read as 16-byte chunks.
+// ---------------------------------------------------------------------------
+// d_k = 128 keeps 64 fp32 Q values per lane, so it runs at one wave per SIMD.
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(kThreads, D == 128 ? 1 : 2) void flash_fwd_f32(FlashParams p) {
+  constexpr int KROW = D * 4 + 16;
+  constexpr int VROW = D * 4 + 32;
+  constexpr int CPR = D * 4 / 16;
+  constexpr int CHUNKS = BN * CPR / kThreads;
+  constexpr int NDB = D / 32;
+  constexpr int NC = D / 8;  // 16-byte chunks per lane half
+  static_assert(CHUNKS * kThreads == BN * CPR, "tile split");
+
+  __shared__ __attribute__((aligned(16))) char smem[BN * KROW + BN * VROW];
+  char* Ks = smem;
+  char* Vs = smem + BN * KROW;
+
+  int b, hq, qt;
+  decode_block(p, b, hq, qt);
+  const int hkv = hq / p.group;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int lq = lane & 31;
+  const int h = lane >> 5;
+  const int off = p.seq_k - p.seq_q;
+
+  const int q_first = qt * BM;
+  const int q_last = min(p.seq_q, q_first + BM) - 1;
+  int k_end = p.seq_k;
+  if (CAUSAL) k_end = max(0, min(p.seq_k, q_last + off + 1));
+  const int n_kt = (k_end + BN - 1) / BN;
+  const int q0 = q_first + wave * 32;
+  const int qi = q0 + lq;
+  int wave_k_end = p.seq_k;
+  if (CAUSAL) wave_k_end = max(0, min(p.seq_k, min(q0 + 31, p.seq_q - 1) + off + 1));
+
+  f32x4 qf[NC];
+  {
+    const float* qrow = (const float*)p.q + b * p.q_sb + hq * p.q_sh + (int64_t)qi * p.q_ss;
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc) {
+      f32x4 z = {0.f, 0.f, 0.f, 0.f};
+      qf[cc] = qi < p.seq_q ? *(const f32x4*)(qrow + h * (D / 2) + 4 * cc) : z;
+    }
+  }
+
+  f32x16 o_acc[NDB];
+#pragma unroll
+  for (int i = 0; i < NDB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o_acc[i][r] = 0.f;
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+
+  const float* kbase = (const float*)p.k + b * p.k_sb + hkv * p.k_sh;
+  const float* vbase = (const float*)p.v + b * p.v_sb + hkv * p.v_sh;
+  f32x4 kreg[CHUNKS], vreg[CHUNKS];
+
+  auto load_tile = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < CHUNKS; ++i) {
+      const int cidx = tid + kThreads * i;
+      const int row = cidx / CPR;
+      const int col = cidx % CPR;
+      const int key = kt * BN + row;
+      f32x4 z = {0.f, 0.f, 0.f, 0.f};
+      const bool ok = key < p.seq_k;
+      kreg[i] = ok ? *(const f32x4*)(kbase + (int64_t)key * p.k_ss + col * 4) : z;
+      vreg[i] = ok ? *(const f32x4*)(vbase + (int64_t)key * p.v_ss + col * 4) : z;
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int i = 0; i < CHUNKS; ++i) {
+      const int cidx = tid + kThreads * i;
+      const int row = cidx / CPR;
+      const int col = cidx % CPR;
+      *(f32x4*)(Ks + row * KROW + col * 16) = kreg[i];
+      *(f32x4*)(Vs + row * VROW + col * 16) = vreg[i];
+    }
+  };
+
+  const float c = p.scale_log2;
+  if (n_kt > 0) load_tile(0);
+  for (int kt = 0; kt < n_kt; ++kt) {
+    if (kt > 0) __syncthreads();
+    store_tile();
+    __syncthreads();
+    if (kt + 1 < n_kt) load_tile(kt + 1);
+
+    const int kb = kt * BN;
+    if (kb >= wave_k_end) continue;
+
+    f32x16 s[2];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[mb][r] = 0.f;
+      const char* krow = Ks + (32 * mb + lq) * KROW + h * (D / 2) * 4;
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) {
+        const f32x4 a = *(const f32x4*)(krow + 16 * cc);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          s[mb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], qf[cc][i], s[mb], 0, 0, 0);
+      }
+    }
+
+    const bool need_mask = (kb + BN > p.seq_k) || (CAUSAL && kb + BN - 1 > q0 + off);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = s[mb][r] * c;
+        if (need_mask) {
+          const int key = kb + 32 * mb + 8 * (r >> 2) + 4 * h + (r & 3);
+          const bool ok = key < p.seq_k && (!CAUSAL || key <= qi + off);
+          x = ok ? x : -INFINITY;
+        }
+        s[mb][r] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = fmaxf(mx, xor32(mx));
+    const float m_new = fmaxf(m_run, mx);
+    const float base = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = fast_exp2(m_run - base);
+    m_run = m_new;
+    if (__any(alpha != 1.f)) {
+      l_run *= alpha;
+#pragma unroll
+      for (int i = 0; i < NDB; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o_acc[i][r] *= alpha;
+    }
+    float psum = 0.f;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float e = fast_exp2(s[mb][r] - base);
+        s[mb][r] = e;
+        psum += e;
+      }
+    l_run += psum;
+
+    // O^T += V^T . P^T: step (mb, r) uses key 32mb + 8(r/4) + 4h + r%4 in
+    // lane half h, i.e. MFMA k = h.
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = 32 * mb + 8 * (r >> 2) + 4 * h + (r & 3);
+        const char* vrow = Vs + key * VROW + lq * 4;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const float a = *(const float*)(vrow + 128 * db);
+          o_acc[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, s[mb][r], o_acc[db], 0, 0, 0);
+        }
+      }
+  }
+
+  const float l_tot = l_run + xor32(l_run);
+  const float inv = 1.f / l_tot;
+  if (qi < p.seq_q) {
+    float* orow = (float*)p.o + b * p.o_sb + hq * p.o_sh + (int64_t)qi * p.o_ss;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d0 = 32 * db + 8 * rq + 4 * h;
+        f32x4 v = {o_acc[db][4 * rq] * inv, o_acc[db][4 * rq + 1] * inv,
+                   o_acc[db][4 * rq + 2] * inv, o_acc[db][4 * rq + 3] * inv};
+        *(f32x4*)(orow + d0) = v;
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// V (b, kv, s, d) -> V^T (b, kv, d, s_pad), zero-filled for s >= seq_k.
+// One workgroup per (64-key tile, kv head, batch).
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void vt_transpose_kernel(const uint16_t* __restrict__ v,
+                                                           uint16_t* __restrict__ vt,
+                                                           int seq_k, int sk_pad, int n_kv,
+                                                           int64_t v_sb, int64_t v_sh,
+                                                           int64_t v_ss) {
+  __shared__ uint16_t tile[64][D + 2];
+  const int kt = blockIdx.x;
+  const int hkv = blockIdx.y;
+  const int b = blockIdx.z;
+  const uint16_t* src = v + b * v_sb + hkv * v_sh;
+  for (int idx = threadIdx.x; idx < 64 * D; idx += 256) {
+    const int r = idx / D;
+    const int d = idx - r * D;
+    const int key = kt * 64 + r;
+    tile[r][d] = key < seq_k ? src[(int64_t)key * v_ss + d] : (uint16_t)0;
+  }
+  __syncthreads();
+  uint16_t* dst = vt + ((int64_t)b * n_kv + hkv) * D * sk_pad + kt * 64;
+  for (int idx = threadIdx.x; idx < 64 * D; idx += 256) {
+    const int d = idx / 64;
+    const int r = idx - d * 64;
+    dst[(int64_t)d * sk_pad + r] = tile[r][d];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Generic fallback for head sizes the MFMA kernels do not cover (any d_k up
+// to 256): one wave per (query row, head), keys in tiles of 64 with the
+// reference's online softmax.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(64) void attn_generic_kernel(FlashParams p, int D, int causal) {
+  using Bits = typename T::bits;
+  __shared__ float qs[256];
+  __shared__ float ps[64];
+  const int qi = blockIdx.x;
+  const int hq = blockIdx.y;
+  const int b = blockIdx.z;
+  const int hkv = hq / p.group;
+  const int lane = threadIdx.x;
+  const Bits* qrow = (const Bits*)p.q + b * p.q_sb + hq * p.q_sh + (int64_t)qi * p.q_ss;
+  for (int d = lane; d < D; d += 64) qs[d] = to_f32<T>(qrow[d]);
+  __syncthreads();
+  const Bits* kb = (const Bits*)p.k + b * p.k_sb + hkv * p.k_sh;
+  const Bits* vb = (const Bits*)p.v + b * p.v_sb + hkv * p.v_sh;
+  const int limit = causal ? min(p.seq_k, qi + (p.seq_k - p.seq_q) + 1) : p.seq_k;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+  const float c = p.scale_log2;
+  for (int k0 = 0; k0 < p.seq_k; k0 += 64) {
+    const int key = k0 + lane;
+    float s = -INFINITY;
+    if (key < limit) {
+      const Bits* kr = kb + (int64_t)key * p.k_ss;
+      float d = 0.f;
+      for (int e = 0; e < D; ++e) d = fmaf(qs[e], to_f32<T>(kr[e]), d);
+      s = d * c;
+    }
+    float mx = s;
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    const float m_new = fmaxf(m_run, mx);
+    const float base = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = fast_exp2(m_run - base);
+    const float pk = fast_exp2(s - base);
+    float sum = pk;
+    for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o);
+    l_run = l_run * alpha + sum;
+    m_run = m_new;
+    __syncthreads();
+    ps[lane] = pk;
+    __syncthreads();
+    const int n = min(64, p.seq_k - k0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = lane + 64 * j;
+      if (d < D) {
+        float a = acc[j] * alpha;
+        for (int kk = 0; kk < n; ++kk) {
+          const float pw = ps[kk];
+          if (pw != 0.f) a = fmaf(pw, to_f32<T>(vb[(int64_t)(k0 + kk) * p.v_ss + d]), a);
+        }
+        acc[j] = a;
+      }
+    }
+  }
+  Bits* orow = (Bits*)p.o + b * p.o_sb + hq * p.o_sh + (int64_t)qi * p.o_ss;
+  const float inv = 1.f / l_run;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int d = lane + 64 * j;
+    if (d < D) orow[d] = from_f32<T>(acc[j] * inv);
+  }
+}
+
+inline bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+
+template <typename T, int D>
+int launch_flash_16(FlashParams& p, void* ws, bool causal, hipStream_t st) {
+  // Key-major V^T into the workspace.
+  p.vt = ws;
+  dim3 tg(p.sk_pad / 64, p.n_kv, p.batch);
+  hipLaunchKernelGGL(vt_transpose_kernel<D>, tg, dim3(256), 0, st, (const uint16_t*)p.v,
+                     (uint16_t*)ws, p.seq_k, p.sk_pad, p.n_kv, p.v_sb, p.v_sh, p.v_ss);
+  int e = tl_launch_status();
+  if (e) return e;
+  dim3 grid((unsigned)(p.n_qt * p.n_head * p.batch));
+  if (causal)
+    hipLaunchKernelGGL((flash_fwd_16<T, D, true>), grid, dim3(kThreads), 0, st, p);
+  else
+    hipLaunchKernelGGL((flash_fwd_16<T, D, false>), grid, dim3(kThreads), 0, st, p);
+  return tl_launch_status();
+}
+
+template <int D>
+int launch_flash_f32(FlashParams& p, bool causal, hipStream_t st) {
+  dim3 grid((unsigned)(p.n_qt * p.n_head * p.batch));
+  if (causal)
+    hipLaunchKernelGGL((flash_fwd_f32<D, true>), grid, dim3(kThreads), 0, st, p);
+  else
+    hipLaunchKernelGGL((flash_fwd_f32<D, false>), grid, dim3(kThreads), 0, st, p);
+  return tl_launch_status();
+}
+
+template <typename T>
+int launch_generic(FlashParams& p, int d_k, bool causal, hipStream_t st) {
+  dim3 grid(p.seq_q, p.n_head, p.batch);
+  hipLaunchKernelGGL(attn_generic_kernel<T>, grid, dim3(64), 0, st, p, d_k, causal ? 1 : 0);
+  return tl_launch_status();
+}
+
+bool mfma_shape_ok(const FlashParams& p, int d_k, int dtype) {
+  if (d_k != 64 && d_k != 128) return false;
+  const int64_t vec = dtype == TL_DTYPE_F32 ? 4 : 8;  // elements per 16 bytes
+  const int64_t s[] = {p.q_sb, p.q_sh, p.q_ss, p.k_sb, p.k_sh, p.k_ss,
+                       p.v_sb, p.v_sh, p.v_ss, p.o_sb, p.o_sh, p.o_ss};
+  for (int64_t x : s)
+    if (x % vec) return false;
+  return aligned16(p.q) && aligned16(p.k) && aligned16(p.v) && aligned16(p.o);
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t tl_attention_fwd_workspace_bytes(int batch, int n_kv_head, int seq_k, int d_k,
+                                        int dtype) {
+  if (dtype == TL_DTYPE_F32 || batch <= 0 || n_kv_head <= 0 || seq_k <= 0 || d_k <= 0) return 0;
+  const size_t sk_pad = (size_t)((seq_k + 63) / 64) * 64;
+  return (size_t)batch * n_kv_head * d_k * sk_pad * 2;
+}
+
+int tl_attention_fwd(const void* q, const void* k, const void* v, void* o, void* workspace,
+                     size_t workspace_bytes, int batch, int n_head, int n_kv_head,
+                     int seq_q, int seq_k, int d_k, const int64_t* q_strides,
+                     const int64_t* k_strides, const int64_t* v_strides,
+                     const int64_t* o_strides, float sm_scale, int causal, int dtype,
+                     void* stream) {
+  if (batch == 0 || n_head == 0 || seq_q == 0) return 0;
+  if (!q || !k || !v || !o || batch < 0 || n_head < 0 || n_kv_head < 1 ||
+      n_head % n_kv_head != 0 || seq_q < 0 || seq_k < 1 || d_k < 1 || d_k > 256 ||
+      !q_strides || !k_strides || !v_strides || !o_strides)
+    return TL_ERR_INVALID;
+  FlashParams p{};
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.o = o;
+  p.batch = batch;
+  p.n_head = n_head;
+  p.n_kv = n_kv_head;
+  p.group = n_head / n_kv_head;
+  p.seq_q = seq_q;
+  p.seq_k = seq_k;
+  p.sk_pad = (seq_k + 63) / 64 * 64;
+  p.n_qt = (seq_q + BM - 1) / BM;
+  p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.q_ss = q_strides[2];
+  p.k_sb = k_strides[0]; p.k_sh = k_strides[1]; p.k_ss = k_strides[2];
+  p.v_sb = v_strides[0]; p.v_sh = v_strides[1]; p.v_ss = v_strides[2];
+  p.o_sb = o_strides[0]; p.o_sh = o_strides[1]; p.o_ss = o_strides[2];
+  p.scale_log2 = sm_scale * 1.4426950408889634f;
+  hipStream_t st = tl_resolve_stream(stream);
+  const bool cz = causal != 0;
+  if (mfma_shape_ok(p, d_k, dtype)) {
+    if (dtype == TL_DTYPE_F32) {
+      return d_k == 64 ? launch_flash_f32<64>(p, cz, st) : launch_flash_f32<128>(p, cz, st);
+    }
+    if (!workspace ||
+        workspace_bytes < tl_attention_fwd_workspace_bytes(batch, n_kv_head, seq_k, d_k, dtype) ||
+        !aligned16(workspace))
+      return TL_ERR_INVALID;
+    if (dtype == TL_DTYPE_BF16)
+      return d_k == 64 ? launch_flash_16<BF16, 64>(p, workspace, cz, st)
+                       : launch_flash_16<BF16, 128>(p, workspace, cz, st);
+    if (dtype == TL_DTYPE_F16)
+      return d_k == 64 ? launch_flash_16<F16, 64>(p, workspace, cz, st)
+                       : launch_flash_16<F16, 128>(p, workspace, cz, st);
+    return TL_ERR_INVALID;
+  }
+  switch (dtype) {
+    case TL_DTYPE_F32: return launch_generic<F32>(p, d_k, cz, st);
+    case TL_DTYPE_F16: return launch_generic<F16>(p, d_k, cz, st);
+    case TL_DTYPE_BF16: return launch_generic<BF16>(p, d_k, cz, st);
+    default: return TL_ERR_INVALID;
+  }
+}
+
+}  // extern "C"

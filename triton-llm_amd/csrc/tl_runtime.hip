@@ -1,0 +1,114 @@
+// Runtime half of the C ABI: device selection, the library stream, the
+// allocator and copies.  The Python allocator (triton_llm/gpu.py) binds these
+// instead of binding libamdhip64 symbols directly, so every copy and every
+// kernel launch shares one in-order HIP stream.
+#include "tl_common.h"
+
+namespace {
+hipStream_t g_stream = nullptr;
+int g_device = -1;
+}  // namespace
+
+hipStream_t tl_resolve_stream(void* stream) {
+  return stream ? (hipStream_t)stream : g_stream;
+}
+
+extern "C" {
+
+int tl_device_count(int* count) {
+  if (!count) return TL_ERR_INVALID;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  *count = (e == hipSuccess) ? n : 0;
+  return (int)e;
+}
+
+int tl_init(int device) {
+  if (g_stream && g_device == device) return 0;
+  hipError_t e = hipSetDevice(device);
+  if (e != hipSuccess) return (int)e;
+  if (g_stream) {
+    // Re-initialising on another device: drop the old stream first.
+    (void)hipStreamDestroy(g_stream);
+    g_stream = nullptr;
+  }
+  // Default priority, non-blocking with respect to the legacy null stream.
+  e = hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking);
+  if (e != hipSuccess) return (int)e;
+  g_device = device;
+  return 0;
+}
+
+void* tl_default_stream(void) { return (void*)g_stream; }
+
+int tl_malloc(void** ptr, size_t nbytes) {
+  if (!ptr) return TL_ERR_INVALID;
+  *ptr = nullptr;
+  if (nbytes == 0) return 0;  // zero-byte tensors carry a NULL pointer
+  return (int)hipMalloc(ptr, nbytes);
+}
+
+int tl_free(void* ptr) {
+  if (!ptr) return 0;
+  return (int)hipFree(ptr);
+}
+
+int tl_memcpy_htod(void* dst, const void* host_src, size_t nbytes) {
+  if (nbytes == 0) return 0;
+  if (!dst || !host_src) return TL_ERR_INVALID;
+  hipError_t e = hipMemcpyAsync(dst, host_src, nbytes, hipMemcpyHostToDevice, g_stream);
+  if (e != hipSuccess) return (int)e;
+  // The host buffer may be released by the caller right after return.
+  return (int)hipStreamSynchronize(g_stream);
+}
+
+int tl_memcpy_dtoh(void* host_dst, const void* src, size_t nbytes) {
+  if (nbytes == 0) return 0;
+  if (!host_dst || !src) return TL_ERR_INVALID;
+  hipError_t e = hipMemcpyAsync(host_dst, src, nbytes, hipMemcpyDeviceToHost, g_stream);
+  if (e != hipSuccess) return (int)e;
+  return (int)hipStreamSynchronize(g_stream);
+}
+
+int tl_memcpy_dtod(void* dst, const void* src, size_t nbytes) {
+  if (nbytes == 0) return 0;
+  if (!dst || !src) return TL_ERR_INVALID;
+  return (int)hipMemcpyAsync(dst, src, nbytes, hipMemcpyDeviceToDevice, g_stream);
+}
+
+int tl_memset(void* dst, int value, size_t nbytes) {
+  if (nbytes == 0) return 0;
+  if (!dst) return TL_ERR_INVALID;
+  return (int)hipMemsetAsync(dst, value, nbytes, g_stream);
+}
+
+int tl_synchronize(void) {
+  hipError_t e = g_stream ? hipStreamSynchronize(g_stream) : hipSuccess;
+  if (e != hipSuccess) return (int)e;
+  return (int)hipDeviceSynchronize();
+}
+
+const char* tl_error_string(int status) {
+  if (status == 0) return "success";
+  return hipGetErrorString((hipError_t)status);
+}
+
+int tl_event_create(void** event) {
+  if (!event) return TL_ERR_INVALID;
+  return (int)hipEventCreate((hipEvent_t*)event);
+}
+
+int tl_event_destroy(void* event) { return (int)hipEventDestroy((hipEvent_t)event); }
+
+int tl_event_record(void* event, void* stream) {
+  return (int)hipEventRecord((hipEvent_t)event, tl_resolve_stream(stream));
+}
+
+int tl_event_synchronize(void* event) { return (int)hipEventSynchronize((hipEvent_t)event); }
+
+int tl_event_elapsed_ms(float* ms, void* start, void* stop) {
+  if (!ms) return TL_ERR_INVALID;
+  return (int)hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop);
+}
+
+}  // extern "C"

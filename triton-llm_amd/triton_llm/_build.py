@@ -1,0 +1,92 @@
+"""Build libtriton_llm_hip.so (gfx950) from triton-llm_amd/csrc.
+
+Each ``.hip`` source is compiled to an object in parallel with hipcc, then the
+objects are linked into ``triton_llm/_lib/libtriton_llm_hip.so`` in-tree, so
+the built library travels with the source tree.
+
+Run as ``python -m triton_llm._build`` (with ``triton-llm_amd`` on sys.path) or
+call :func:`build`.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures
+import os
+import shutil
+import subprocess
+import sys
+import tempfile
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+ROOT_DIR = os.path.dirname(PKG_DIR)  # triton-llm_amd/
+CSRC_DIR = os.path.join(ROOT_DIR, "csrc")
+LIB_DIR = os.path.join(PKG_DIR, "_lib")
+LIB_NAME = "libtriton_llm_hip.so"
+LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
+
+OFFLOAD_ARCH = "gfx950"
+
+# -packed-fp32-ops is disabled for every device compile: packed fp32 forms
+# have produced silently wrong results on the target boxes.  The host pass
+# warns that it does not know the feature; that warning is harmless.
+HIPCC_FLAGS = [
+    f"--offload-arch={OFFLOAD_ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-function",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(path):
+        raise RuntimeError("hipcc not found; ROCm is required to build the HIP library")
+    return path
+
+
+def sources() -> list[str]:
+    return sorted(
+        os.path.join(CSRC_DIR, f) for f in os.listdir(CSRC_DIR) if f.endswith(".hip")
+    )
+
+
+def _compile_one(src: str, obj: str) -> None:
+    cmd = [_hipcc(), *HIPCC_FLAGS, "-c", src, "-o", obj]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {os.path.basename(src)}:\n{err}")
+    if err.strip():
+        print(err, file=sys.stderr)
+
+
+def build(verbose: bool = True, jobs: int | None = None) -> str:
+    """Compile every csrc/*.hip for gfx950 and link the shared library."""
+    os.makedirs(LIB_DIR, exist_ok=True)
+    srcs = sources()
+    if not srcs:
+        raise RuntimeError(f"no HIP sources under {CSRC_DIR}")
+    jobs = jobs or min(len(srcs), int(os.environ.get("MAX_JOBS", "8")))
+    with tempfile.TemporaryDirectory(prefix="tl_build_") as tmp:
+        objs = [os.path.join(tmp, os.path.basename(s) + ".o") for s in srcs]
+        with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
+            futs = [ex.submit(_compile_one, s, o) for s, o in zip(srcs, objs)]
+            for f in futs:
+                f.result()
+        tmp_lib = LIB_PATH + ".tmp"
+        cmd = [_hipcc(), f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC", *objs, "-o", tmp_lib]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"link failed:\n{res.stderr}")
+        os.replace(tmp_lib, LIB_PATH)
+    if verbose:
+        print(f"built {LIB_PATH}")
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    build()
