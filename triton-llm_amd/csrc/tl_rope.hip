@@ -4,19 +4,22 @@
 // (triton_llm/kernels/rope.py:49-66): element i pairs with i + d_k/2,
 //   out[i]        = x[i] * cos[pos, i] - x[i + h] * sin[pos, i]
 //   out[i + h]    = x[i] * sin[pos, i] + x[i + h] * cos[pos, i]
-// Each product and the sum/difference are rounded separately in fp32
-// (__fmul_rn / __fadd_rn / __fsub_rn never contract into an FMA), which is
-// exactly how NumPy evaluates the same expression, so the fp32 result is
+// Each product and the sum/difference are rounded separately in fp32, which
+// is exactly how NumPy evaluates the same expression, so the fp32 result is
 // bit-identical to the host restatement; 16-bit outputs are then rounded once
-// (RNE) to the storage type.
+// (RNE) to the storage type.  hipcc contracts a*b - c*d into an FMA by default
+// (even when written with __fmul_rn / __fsub_rn), so the rotation helper
+// switches contraction off for its own expressions.
 #include "tl_common.h"
 
 namespace {
 
 __device__ __forceinline__ void rotate_pair(float xe, float xo, float c, float s,
                                             float& oe, float& oo) {
-  oe = __fsub_rn(__fmul_rn(xe, c), __fmul_rn(xo, s));
-  oo = __fadd_rn(__fmul_rn(xe, s), __fmul_rn(xo, c));
+#pragma clang fp contract(off)
+  const float a = xe * c, b = xo * s, d = xe * s, e = xo * c;
+  oe = a - b;
+  oo = d + e;
 }
 
 // One thread per (row, pair index).  Rows are flattened (..., seq) so the
