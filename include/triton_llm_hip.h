@@ -92,8 +92,8 @@ int tl_rope_inplace(void* x, const float* cos_table, const float* sin_table,
  * attention_gqa.py:97; equal to attention.py's top-left mask when
  * seq_q == seq_k).  Scores are (q . k) * sm_scale.
  * Requires seq_q >= 1, seq_k >= 1 (the Python layer returns the reference's
- * empty/zero results itself).  Workspace: see tl_attention_fwd_workspace_bytes
- * (it holds a key-major copy of V for the 16-bit MFMA path).
+ * empty/zero results itself).  Workspace: tl_attention_fwd_workspace_bytes
+ * (the 16-bit MFMA path stages a key-major copy of V there; 0 for fp32).
  * ------------------------------------------------------------------------- */
 size_t tl_attention_fwd_workspace_bytes(int batch, int n_kv_head, int seq_k,
                                         int d_k, int dtype);

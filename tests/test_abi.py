@@ -34,10 +34,11 @@ def test_library_exports_every_declared_symbol():
 
 def test_workspace_queries():
     lib = _lib.load()
-    # fp32 needs no V^T copy; 16-bit needs B * Hkv * D * round_up(Sk, 64) * 2 bytes.
+    # fp32 reads V in place; the 16-bit MFMA path stages V^T: B * Hkv * D * round_up(Sk, 64) * 2.
     assert lib.tl_attention_fwd_workspace_bytes(1, 8, 8192, 128, _lib.DTYPE_F32) == 0
     assert lib.tl_attention_fwd_workspace_bytes(1, 8, 8192, 128, _lib.DTYPE_BF16) == 8 * 128 * 8192 * 2
     assert lib.tl_attention_fwd_workspace_bytes(2, 3, 100, 64, _lib.DTYPE_F16) == 2 * 3 * 64 * 128 * 2
+    assert lib.tl_attention_fwd_workspace_bytes(1, 1, 100, 32, _lib.DTYPE_BF16) == 0  # generic path
     split = lib.tl_decode_split_size(64, 8, 16384)
     assert split % 16 == 0 and 64 <= split <= 2048
     ws = lib.tl_attention_decode_workspace_bytes(64, 24, 16384, 128, split)

@@ -26,12 +26,11 @@
 //                        same C layout.
 // The reduction index of one MFMA may be any permutation as long as A and B
 // agree; the P^T operand is taken straight from the S^T accumulator
-// registers and the V^T operand is read with the matching key permutation.
+// registers (lane half h holds keys 8a + 4h + b, b < 4, of each 32-key
+// block) and the V^T operand is read with the matching key permutation.
 //
-// 16-bit inputs read V through a key-major copy V^T [b][kv][d][Sk_pad]
-// (written by vt_transpose_kernel into the caller's workspace) so that a
-// lane's 8 consecutive keys for one d are two 8-byte LDS reads.  fp32 reads
-// V in its natural layout (one element per lane per MFMA).
+// Kernels: vt_pack_kernel + flash_fwd_pp (f16 / bf16, d_k 64 / 128), flash_fwd_f32
+// (fp32, d_k 64 / 128), attn_generic_kernel (any d_k <= 256).
 #include "tl_common.h"
 
 #include <math.h>
@@ -45,10 +44,10 @@ constexpr int kThreads = 256;
 struct FlashParams {
   const void* q;
   const void* k;
-  const void* v;   // natural V (fp32 path)
-  const void* vt;  // key-major V^T (16-bit path)
+  const void* v;
+  const void* vt;  // key-major V^T copy (16-bit path), see vt_pack_kernel
   void* o;
-  int batch, n_head, n_kv, group, seq_q, seq_k, sk_pad, n_qt;
+  int batch, n_head, n_kv, group, seq_q, seq_k, n_qt, sk_pad;
   int64_t q_sb, q_sh, q_ss;
   int64_t k_sb, k_sh, k_ss;
   int64_t v_sb, v_sh, v_ss;
@@ -108,27 +107,120 @@ __device__ __forceinline__ void decode_block(const FlashParams& p, int& b, int& 
 }
 
 // ---------------------------------------------------------------------------
-// 16-bit (f16 / bf16) kernel.
+// 16-bit (f16 / bf16) kernel: two wave groups in ping-pong.
+//
+// Workgroup = 8 waves = 2 groups of 4; each wave owns 32 query rows, group g
+// the rows [128 g, 128 g + 128) of the workgroup's 256.  Both groups walk the
+// same 64-key K / V tiles.  Per tile a group runs
+//     G0(t): S^T = K_t . Q^T        (MFMA)
+//     A(t):  masked online softmax  (VALU: max, exp2, pack, row sum)
+//     G1(t): O^T += V_t^T . P_t^T   (MFMA)
+// and the work is cut into phases separated by workgroup barriers:
+//     phase 2t   : group 0 runs {G1(t-1), G0(t)}   group 1 runs A(t-1)
+//     phase 2t+1 : group 0 runs A(t)               group 1 runs {G1(t-1), G0(t)}
+// so on every SIMD (one wave of each group) one wave issues MFMAs while the
+// other does the softmax.  K_{t+1} and V^T_t are loaded into registers at
+// the start of phase 2t and written to LDS at the start of phase 2t+1, into
+// the buffers freed at the end of phase 2t-1; two buffers each.
+//
+// V is read from a key-major copy V^T [b][kv][d][Sk_pad] written once per
+// call by vt_pack_kernel, with each 16-key group stored in the order the
+// MFMA's k-index permutation wants (see vt_pack_kernel), so the 8 keys a lane
+// feeds into one PV MFMA are one contiguous 16 bytes: ds_read_b128, the same
+// fast LDS path as the K operand.  (A transposing LDS read of natural V,
+// ds_read_b64_tr_b16, measured ~3x lower LDS throughput per byte on gfx950
+// and bounded the kernel.)
+//
+// LDS rows are unpadded; the 16-byte chunk c of row r lives in slot
+// c ^ swz(r) (lds_swz for K rows, vt_swz for V^T rows), which makes every
+// operand read conflict-free.
+//
+// Softmax per score: one max (amortised over max3), one FMA applying the
+// scale and subtracting the running max, one exp2, half a convert; the row
+// sum is a v_dot2 over the packed 16-bit P the PV product consumes.  The
+// running max is raised (and O rescaled) only when a tile's max exceeds it by
+// more than kRescaleLog2 (log2 units), which bounds P by 2^kRescaleLog2.
 // ---------------------------------------------------------------------------
+constexpr float kRescaleLog2 = 8.0f;
+constexpr int PP_THREADS = 512;
+constexpr int PP_BM = 256;  // query rows per workgroup
+constexpr int PP_BN = 64;   // keys per tile
+
+// V^T rows in LDS are 64 keys x 2 B = 128 B; 16 consecutive rows read the
+// same chunk, so the slot is XORed with (row / 2) % 8 (rows of one parity
+// share a bank half).
+__device__ __forceinline__ int vt_swz(int r) { return (r >> 1) & 7; }
+
+template <int D>
+__device__ __forceinline__ int lds_swz(int r) {
+  if constexpr (D == 128) return 4 * (r & 3) + ((r >> 2) & 3);
+  else return 4 * ((r >> 1) & 1) + ((r >> 2) & 3);
+}
+
+template <typename T>
+__device__ __forceinline__ float dot2_sum(typename Mfma<T>::frag pf, float acc);
+
+template <>
+__device__ __forceinline__ float dot2_sum<BF16>(bf16x8 pf, float acc) {
+  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    bf16x2 pr = {pf[2 * i], pf[2 * i + 1]};
+    acc = __builtin_amdgcn_fdot2_f32_bf16(pr, one, acc, false);
+  }
+  return acc;
+}
+
+template <>
+__device__ __forceinline__ float dot2_sum<F16>(f16x8 pf, float acc) {
+  const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f16x2 pr = {pf[2 * i], pf[2 * i + 1]};
+    acc = __builtin_amdgcn_fdot2(pr, one, acc, false);
+  }
+  return acc;
+}
+
+// Max of lane l and lane l ^ 32 (both lanes receive it).
+__device__ __forceinline__ float max_xor32(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float sum_xor32(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Workgroup barrier that orders LDS only (global prefetches stay in flight).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
 template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(kThreads, 2) void flash_fwd_16(FlashParams p) {
+__global__ __launch_bounds__(PP_THREADS, 2) void flash_fwd_pp(FlashParams p) {
   using M = Mfma<T>;
   using frag = typename M::frag;
   using Bits = typename T::bits;
-  constexpr int KROW = D * 2 + 16;   // bytes per K row in LDS (16 B pad)
-  constexpr int VROW = BN * 2 + 8;   // bytes per V^T row in LDS (8 B pad)
-  constexpr int K_CPR = D * 2 / 16;  // 16-byte chunks per K row
-  constexpr int K_CHUNKS = BN * K_CPR / kThreads;
-  constexpr int V_CPR = BN * 2 / 16;  // 16-byte chunks per V^T row (= 8)
-  constexpr int V_CHUNKS = D * V_CPR / kThreads;
-  constexpr int NDB = D / 32;  // 32-row blocks of O^T
-  constexpr int NKS = D / 16;  // k-steps of S^T
-  static_assert(K_CHUNKS * kThreads == BN * K_CPR, "K tile split");
-  static_assert(V_CHUNKS * kThreads == D * V_CPR, "V tile split");
+  constexpr int BN = PP_BN;
+  constexpr int ROWB = D * 2;         // bytes per K / V row in LDS
+  constexpr int TILEB = BN * ROWB;    // bytes per K or V tile
+  constexpr int NSL = ROWB / 16;      // 16-byte slots per row
+  constexpr int RPR = 1024 / ROWB;    // rows per 1 KiB region
+  constexpr int NREG = TILEB / 1024;  // 1 KiB regions per tile
+  constexpr int RPW = NREG / 8;       // regions per wave per tile
+  constexpr int NDB = D / 32;         // 32-row blocks of O^T
+  constexpr int NKS = D / 16;         // k-steps of S^T
+  static_assert(RPW * 8 == NREG, "tile must split into 1 KiB regions per wave");
 
-  __shared__ __attribute__((aligned(16))) char smem[BN * KROW + D * VROW];
-  char* Ks = smem;
-  char* Vs = smem + BN * KROW;
+  __shared__ __attribute__((aligned(1024))) char smem[4 * TILEB];  // K0 K1 V0 V1
 
   int b, hq, qt;
   decode_block(p, b, hq, qt);
@@ -136,22 +228,23 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_16(FlashParams p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int group = wave >> 2;
   const int lq = lane & 31;
   const int h = lane >> 5;
   const int off = p.seq_k - p.seq_q;  // bottom-right causal offset
 
-  const int q_first = qt * BM;
-  const int q_last = min(p.seq_q, q_first + BM) - 1;
+  const int q_first = qt * PP_BM;
+  const int q_last = min(p.seq_q, q_first + PP_BM) - 1;
   int k_end = p.seq_k;
   if (CAUSAL) k_end = max(0, min(p.seq_k, q_last + off + 1));
   const int n_kt = (k_end + BN - 1) / BN;
 
-  const int q0 = q_first + wave * 32;  // first row of this wave
-  const int qi = q0 + lq;              // this lane's query row
+  const int q0 = q_first + 128 * group + 32 * (wave & 3);  // first row of this wave
+  const int qi = q0 + lq;                                  // this lane's query row
   int wave_k_end = p.seq_k;
   if (CAUSAL) wave_k_end = max(0, min(p.seq_k, min(q0 + 31, p.seq_q - 1) + off + 1));
+  if (q0 >= p.seq_q) wave_k_end = 0;  // no rows: skip all compute
 
-  // Q^T operand: lane holds Q[qi][16ks + 8h .. +7] for every k-step.
   frag qf[NKS];
   {
     const Bits* qrow = (const Bits*)p.q + b * p.q_sb + hq * p.q_sh + (int64_t)qi * p.q_ss;
@@ -168,137 +261,214 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_16(FlashParams p) {
   for (int i = 0; i < NDB; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o_acc[i][r] = 0.f;
-  float m_run = -INFINITY;
-  float l_run = 0.f;  // this lane's half of the row sum
+  float m_run = -INFINITY;  // running max of scaled scores (log2 domain)
+  float l_run = 0.f;        // this lane's half of the row sum
+  f32x16 s[2];
+  frag pfr[BN / 16];
 
+  // Direct global -> LDS tile loads.  Wave w fills 1 KiB regions w + 8 i; lane
+  // l of a region holds row R * RPR + l / NSL, slot l % NSL, i.e. the chunk
+  // (l % NSL) ^ swz(row) of that row.
   const Bits* kbase = (const Bits*)p.k + b * p.k_sb + hkv * p.k_sh;
   const Bits* vtbase = (const Bits*)p.vt + ((int64_t)b * p.n_kv + hkv) * D * p.sk_pad;
-  u32x4 kreg[K_CHUNKS], vreg[V_CHUNKS];
-
-  auto load_tile = [&](int kt) {
+  // K tile: 64 key rows of ROWB bytes.  V^T tile: D rows of 64 keys (128 B).
+  constexpr int VT_RPR = 1024 / (BN * 2);  // V^T rows per 1 KiB region (8)
+  int ld_row[RPW], ld_col[RPW], vt_off[RPW];
 #pragma unroll
-    for (int i = 0; i < K_CHUNKS; ++i) {
-      const int c = tid + kThreads * i;
-      const int row = c / K_CPR;
-      const int col = c % K_CPR;
-      const int key = kt * BN + row;
-      u32x4 z = {0u, 0u, 0u, 0u};
-      kreg[i] = key < p.seq_k ? *(const u32x4*)(kbase + (int64_t)key * p.k_ss + col * 8) : z;
-    }
+  for (int i = 0; i < RPW; ++i) {
+    const int row = (wave + 8 * i) * RPR + lane / NSL;
+    ld_row[i] = row;
+    ld_col[i] = ((lane % NSL) ^ lds_swz<D>(row)) * 8;
+    const int vrow = (wave + 8 * i) * VT_RPR + lane / 8;
+    vt_off[i] = vrow * p.sk_pad + ((lane % 8) ^ vt_swz(vrow)) * 8;
+  }
+  // Tiles are staged through registers: global loads are issued at the start
+  // of phase 2t and written to LDS at the start of phase 2t+1 (the target
+  // buffers are already free then), so their latency overlaps a whole phase.
+  // (Direct global -> LDS loads were tried; with them in the loop the
+  // compiler's wait insertion only ever waits for all LDS reads, which
+  // serialises the operand prefetch.)
+  u32x4 kst[RPW], vst[RPW];
+  auto load_k = [&](int kb) {
 #pragma unroll
-    for (int i = 0; i < V_CHUNKS; ++i) {
-      const int c = tid + kThreads * i;
-      const int d = c / V_CPR;
-      const int col = c % V_CPR;
-      vreg[i] = *(const u32x4*)(vtbase + (int64_t)d * p.sk_pad + kt * BN + col * 8);
-    }
-  };
-  auto store_tile = [&]() {
-#pragma unroll
-    for (int i = 0; i < K_CHUNKS; ++i) {
-      const int c = tid + kThreads * i;
-      const int row = c / K_CPR;
-      const int col = c % K_CPR;
-      *(u32x4*)(Ks + row * KROW + col * 16) = kreg[i];
-    }
-#pragma unroll
-    for (int i = 0; i < V_CHUNKS; ++i) {
-      const int c = tid + kThreads * i;
-      const int d = c / V_CPR;
-      const int col = c % V_CPR;
-      u32x2* dst = (u32x2*)(Vs + d * VROW + col * 16);
-      dst[0] = u32x2{vreg[i].x, vreg[i].y};
-      dst[1] = u32x2{vreg[i].z, vreg[i].w};
+    for (int i = 0; i < RPW; ++i) {
+      const int key = min(kb + ld_row[i], p.seq_k - 1);  // rows past the end: any valid row
+      kst[i] = *(const u32x4*)(kbase + (int64_t)key * p.k_ss + ld_col[i]);
     }
   };
+  auto load_v = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) vst[i] = *(const u32x4*)(vtbase + kb + vt_off[i]);
+  };
+  auto store_k = [&](char* buf) {
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) *(u32x4*)(buf + (wave + 8 * i) * 1024 + lane * 16) = kst[i];
+  };
+  auto store_v = [&](char* buf) {
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) *(u32x4*)(buf + (wave + 8 * i) * 1024 + lane * 16) = vst[i];
+  };
+  char* kbuf = smem;
+  char* vbuf = smem + 2 * TILEB;
 
   const float c = p.scale_log2;
-  if (n_kt > 0) load_tile(0);
-  for (int kt = 0; kt < n_kt; ++kt) {
-    if (kt > 0) __syncthreads();
-    store_tile();
-    __syncthreads();
-    if (kt + 1 < n_kt) load_tile(kt + 1);
+  auto tile_active = [&](int t) { return t >= 0 && t < n_kt && t * BN < wave_k_end; };
 
-    const int kb = kt * BN;
-    if (kb >= wave_k_end) continue;  // whole tile masked for this wave
-
-    // S^T = K . Q^T for two 32-key blocks.
-    f32x16 s[2];
+  // G0(t): S^T = K_t . Q^T
+  auto gemm0 = [&](int t) {
+    const char* Kb = kbuf + (t & 1) * TILEB;
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[mb][r] = 0.f;
-      const char* krow = Ks + (32 * mb + lq) * KROW + 16 * h;
+      const int row = 32 * mb + lq;
+      const char* krow = Kb + row * ROWB;
+      const int sw = lds_swz<D>(row);
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
-        frag a = __builtin_bit_cast(frag, *(const u32x4*)(krow + 32 * ks));
+        frag a = __builtin_bit_cast(frag, *(const u32x4*)(krow + (((2 * ks + h) ^ sw) << 4)));
         s[mb] = M::mma(a, qf[ks], s[mb]);
       }
     }
-
-    const bool need_mask = (kb + BN > p.seq_k) || (CAUSAL && kb + BN - 1 > q0 + off);
-    float mx = -INFINITY;
+  };
+  // G1(t): O^T += V_t^T . P_t^T.  Lane (d = 32 db + lq, half h) reads the 8
+  // keys 16 tt + 8 h .. +7 of the permuted V^T row d: one 16-byte chunk.
+  auto gemm1 = [&](int t) {
+    const char* Vb = vbuf + (t & 1) * TILEB;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
+    for (int tt = 0; tt < BN / 16; ++tt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = s[mb][r] * c;
-        if (need_mask) {
-          const int key = kb + 32 * mb + 8 * (r >> 2) + 4 * h + (r & 3);
-          const bool ok = key < p.seq_k && (!CAUSAL || key <= qi + off);
-          x = ok ? x : -INFINITY;
-        }
-        s[mb][r] = x;
-        mx = fmaxf(mx, x);
+      for (int db = 0; db < NDB; ++db) {
+        const int row = 32 * db + lq;
+        const u32x4 raw = *(const u32x4*)(Vb + row * (BN * 2) + (((2 * tt + h) ^ vt_swz(row)) << 4));
+        o_acc[db] = M::mma(__builtin_bit_cast(frag, raw), pfr[tt], o_acc[db]);
       }
+  };
+  // {G1(t-1), G0(t)} as one stream: PV and S MFMAs alternate (NDB + 2
+  // independent accumulator chains), and the LDS operand reads run kPrefetch
+  // jobs ahead of their MFMA so no MFMA waits on LDS latency.
+  //
+  // Operand addresses: the swizzle term of K row 32 mb + lq does not depend on
+  // mb, and that of V^T row 32 db + lq does not depend on db, so one lane
+  // constant per k-step (K) and per 16-key step (V^T) covers every read; mb
+  // and db become immediate offsets.
+  int k_addr[NKS], v_addr[BN / 16];
+  {
+    const int swk = lds_swz<D>(lq);
+    const int swv = vt_swz(lq);  // == vt_swz(32 db + lq) for every db
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) k_addr[ks] = lq * ROWB + (((2 * ks + h) ^ swk) << 4);
+#pragma unroll
+    for (int tt = 0; tt < BN / 16; ++tt) v_addr[tt] = lq * (BN * 2) + (((2 * tt + h) ^ swv) << 4);
+  }
+  auto gemm10 = [&](int t) {
+    constexpr int NG = BN / 16 * NDB;  // jobs per GEMM (== 2 * NKS)
+    static_assert(NG == 2 * NKS, "S and PV job counts must match");
+    constexpr int kPrefetch = 2;
+    const char* Kb = kbuf + (t & 1) * TILEB;
+    const char* Vb = vbuf + ((t - 1) & 1) * TILEB;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[mb][r] = 0.f;
+    u32x4 kfr[NG], vfr[NG];
+    auto fetch = [&](int g) {
+      const int tt = g / NDB, db = g % NDB;  // PV job: keys 16 tt.., d-block db
+      vfr[g] = *(const u32x4*)(Vb + v_addr[tt] + 32 * db * (BN * 2));
+      const int ks = g >> 1, mb = g & 1;  // S job: k-step ks, key block mb
+      kfr[g] = *(const u32x4*)(Kb + k_addr[ks] + 32 * mb * ROWB);
+    };
+#pragma unroll
+    for (int g = 0; g < kPrefetch; ++g) fetch(g);
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      if (g + kPrefetch < NG) fetch(g + kPrefetch);
+      const int tt = g / NDB, db = g % NDB;
+      o_acc[db] = M::mma(__builtin_bit_cast(frag, vfr[g]), pfr[tt], o_acc[db]);
+      s[g & 1] = M::mma(__builtin_bit_cast(frag, kfr[g]), qf[g >> 1], s[g & 1]);
+      __builtin_amdgcn_sched_barrier(0);  // keep reads kPrefetch jobs ahead
     }
-    mx = fmaxf(mx, xor32(mx));
-    const float m_new = fmaxf(m_run, mx);
-    const float base = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = fast_exp2(m_run - base);
-    m_run = m_new;
-    if (__any(alpha != 1.f)) {
+  };
+  // A(t): masked online softmax of S_t -> P_t
+  auto softmax = [&](int t) {
+    const int kb = t * BN;
+    const bool need_mask = (kb + BN > p.seq_k) || (CAUSAL && kb + BN - 1 > q0 + off);
+    if (need_mask) {
+      // key = kb + 32mb + 8(r/4) + 4h + r%4 must be < seq_k and <= qi + off.
+      int lim = p.seq_k - 1 - kb - 4 * h;
+      if (CAUSAL) lim = min(lim, qi + off - kb - 4 * h);
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kl = 32 * mb + 8 * (r >> 2) + (r & 3);
+          s[mb][r] = kl <= lim ? s[mb][r] : -INFINITY;
+        }
+    }
+    float mx = s[0][0];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int r = (mb == 0 ? 1 : 0); r < 16; ++r) mx = fmaxf(mx, s[mb][r]);
+    mx = max_xor32(mx) * c;  // c > 0: scaling preserves the order
+    if (__any(mx > m_run + kRescaleLog2)) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2(m_run - m_new);
+      m_run = m_new;
       l_run *= alpha;
 #pragma unroll
       for (int i = 0; i < NDB; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o_acc[i][r] *= alpha;
     }
-    float psum = 0.f;
+    const float nb = (m_run == -INFINITY) ? 0.f : -m_run;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float e = fast_exp2(s[mb][r] - base);
-        s[mb][r] = e;
-        psum += e;
-      }
-    l_run += psum;
-
-    // O^T += V^T . P^T, 16 keys per MFMA.
-#pragma unroll
-    for (int t = 0; t < BN / 16; ++t) {
-      const int mb = t >> 1;
-      const int tp = t & 1;
+    for (int tt = 0; tt < BN / 16; ++tt) {
       float pv[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) pv[j] = s[mb][8 * tp + j];
-      const frag pb = M::pack(pv);
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        const char* vrow = Vs + (32 * db + lq) * VROW + (16 * t + 4 * h) * 2;
-        const u32x2 lo = *(const u32x2*)vrow;
-        const u32x2 hi = *(const u32x2*)(vrow + 16);
-        const u32x4 raw = {lo.x, lo.y, hi.x, hi.y};
-        o_acc[db] = M::mma(__builtin_bit_cast(frag, raw), pb, o_acc[db]);
-      }
+      for (int j = 0; j < 8; ++j) pv[j] = fast_exp2(fmaf(s[tt >> 1][8 * (tt & 1) + j], c, nb));
+      pfr[tt] = M::pack(pv);
+      l_run = dot2_sum<T>(pfr[tt], l_run);
     }
+  };
+
+  if (n_kt > 0) {
+    load_k(0);
+    store_k(kbuf);
+    lds_barrier();
+  }
+  const int n_phase = n_kt > 0 ? 2 * n_kt + 2 : 0;
+  for (int ph = 0; ph < n_phase; ++ph) {
+    const int t = ph >> 1;
+    if ((ph & 1) == 0) {
+      if (t + 1 < n_kt) load_k((t + 1) * BN);
+      if (t < n_kt) load_v(t * BN);
+    } else {
+      if (t + 1 < n_kt) store_k(kbuf + ((t + 1) & 1) * TILEB);
+      if (t < n_kt) store_v(vbuf + (t & 1) * TILEB);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if ((ph & 1) == group) {
+      // MFMA phase: G1(t-1) then G0(t)
+      __builtin_amdgcn_s_setprio(1);
+      const bool a1 = tile_active(t - 1), a0 = tile_active(t);
+      if (a1 && a0) {
+        gemm10(t);
+      } else {
+        if (a1) gemm1(t - 1);
+        if (a0) gemm0(t);
+      }
+      __builtin_amdgcn_s_setprio(0);
+    } else {
+      const int ta = group == 0 ? t : t - 1;
+      if (tile_active(ta)) softmax(ta);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
   }
 
   // Epilogue: O[qi][d] = O^T[d][qi] / l.
-  const float l_tot = l_run + xor32(l_run);
-  const float inv = 1.f / l_tot;
+  const float inv = 1.f / sum_xor32(l_run);
   if (qi < p.seq_q) {
     Bits* orow = (Bits*)p.o + b * p.o_sb + hq * p.o_sh + (int64_t)qi * p.o_ss;
 #pragma unroll
@@ -498,32 +668,41 @@ __global__ __launch_bounds__(kThreads, D == 128 ? 1 : 2) void flash_fwd_f32(Flas
 }
 
 // ---------------------------------------------------------------------------
-// V (b, kv, s, d) -> V^T (b, kv, d, s_pad), zero-filled for s >= seq_k.
-// One workgroup per (64-key tile, kv head, batch).
+// V (b, kv, s, d) -> V^T (b, kv, d, s_pad), s_pad a multiple of 64, keys past
+// seq_k zero-filled.  Within each group of 16 keys the stored order is
+//     position 16 u + 8 h + j  <-  key 16 u + 8 (j / 4) + 4 h + (j % 4)
+// which is the key order of the PV MFMA's k-index for lane half h (the S^T
+// accumulator layout puts keys 8 a + 4 h + b, b < 4, in lane half h), so a
+// lane's 8 keys are contiguous.  One workgroup per (64-key tile, kv head, b).
 // ---------------------------------------------------------------------------
 template <int D>
-__global__ __launch_bounds__(256) void vt_transpose_kernel(const uint16_t* __restrict__ v,
-                                                           uint16_t* __restrict__ vt,
-                                                           int seq_k, int sk_pad, int n_kv,
-                                                           int64_t v_sb, int64_t v_sh,
-                                                           int64_t v_ss) {
-  __shared__ uint16_t tile[64][D + 2];
-  const int kt = blockIdx.x;
-  const int hkv = blockIdx.y;
-  const int b = blockIdx.z;
+__global__ __launch_bounds__(256) void vt_pack_kernel(const uint16_t* __restrict__ v,
+                                                      uint16_t* __restrict__ vt, int seq_k,
+                                                      int sk_pad, int n_kv, int64_t v_sb,
+                                                      int64_t v_sh, int64_t v_ss) {
+  constexpr int TROW = D + 8;  // LDS row (elements), 16-byte aligned
+  __shared__ __attribute__((aligned(16))) uint16_t tile[64 * TROW];
+  const int kt = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z;
   const uint16_t* src = v + b * v_sb + hkv * v_sh;
-  for (int idx = threadIdx.x; idx < 64 * D; idx += 256) {
-    const int r = idx / D;
-    const int d = idx - r * D;
+  for (int c = threadIdx.x; c < 64 * D / 8; c += 256) {
+    const int r = c / (D / 8), col = c % (D / 8);
     const int key = kt * 64 + r;
-    tile[r][d] = key < seq_k ? src[(int64_t)key * v_ss + d] : (uint16_t)0;
+    u32x4 val = {0u, 0u, 0u, 0u};
+    if (key < seq_k) val = *(const u32x4*)(src + (int64_t)key * v_ss + col * 8);
+    *(u32x4*)(tile + r * TROW + col * 8) = val;
   }
   __syncthreads();
   uint16_t* dst = vt + ((int64_t)b * n_kv + hkv) * D * sk_pad + kt * 64;
-  for (int idx = threadIdx.x; idx < 64 * D; idx += 256) {
-    const int d = idx / 64;
-    const int r = idx - d * 64;
-    dst[(int64_t)d * sk_pad + r] = tile[r][d];
+  for (int c = threadIdx.x; c < D * 8; c += 256) {
+    const int d = c / 8, ch = c % 8;
+    const int u = ch >> 1, h = ch & 1;
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+      const int k0 = 16 * u + 8 * (j / 4) + 4 * h + (j % 4);
+      w[j / 2] = (uint32_t)tile[k0 * TROW + d] | ((uint32_t)tile[(k0 + 1) * TROW + d] << 16);
+    }
+    *(u32x4*)(dst + (int64_t)d * sk_pad + ch * 8) = u32x4{w[0], w[1], w[2], w[3]};
   }
 }
 
@@ -600,23 +779,24 @@ inline bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
 template <typename T, int D>
 int launch_flash_16(FlashParams& p, void* ws, bool causal, hipStream_t st) {
-  // Key-major V^T into the workspace.
   p.vt = ws;
   dim3 tg(p.sk_pad / 64, p.n_kv, p.batch);
-  hipLaunchKernelGGL(vt_transpose_kernel<D>, tg, dim3(256), 0, st, (const uint16_t*)p.v,
-                     (uint16_t*)ws, p.seq_k, p.sk_pad, p.n_kv, p.v_sb, p.v_sh, p.v_ss);
+  hipLaunchKernelGGL(vt_pack_kernel<D>, tg, dim3(256), 0, st, (const uint16_t*)p.v, (uint16_t*)ws,
+                     p.seq_k, p.sk_pad, p.n_kv, p.v_sb, p.v_sh, p.v_ss);
   int e = tl_launch_status();
   if (e) return e;
+  p.n_qt = (p.seq_q + PP_BM - 1) / PP_BM;
   dim3 grid((unsigned)(p.n_qt * p.n_head * p.batch));
   if (causal)
-    hipLaunchKernelGGL((flash_fwd_16<T, D, true>), grid, dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL((flash_fwd_pp<T, D, true>), grid, dim3(PP_THREADS), 0, st, p);
   else
-    hipLaunchKernelGGL((flash_fwd_16<T, D, false>), grid, dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL((flash_fwd_pp<T, D, false>), grid, dim3(PP_THREADS), 0, st, p);
   return tl_launch_status();
 }
 
 template <int D>
 int launch_flash_f32(FlashParams& p, bool causal, hipStream_t st) {
+  p.n_qt = (p.seq_q + BM - 1) / BM;
   dim3 grid((unsigned)(p.n_qt * p.n_head * p.batch));
   if (causal)
     hipLaunchKernelGGL((flash_fwd_f32<D, true>), grid, dim3(kThreads), 0, st, p);
@@ -648,7 +828,11 @@ extern "C" {
 
 size_t tl_attention_fwd_workspace_bytes(int batch, int n_kv_head, int seq_k, int d_k,
                                         int dtype) {
-  if (dtype == TL_DTYPE_F32 || batch <= 0 || n_kv_head <= 0 || seq_k <= 0 || d_k <= 0) return 0;
+  // 16-bit MFMA path: the permuted key-major V^T copy.  fp32 and the generic
+  // kernel read V in place.
+  if (dtype == TL_DTYPE_F32 || batch <= 0 || n_kv_head <= 0 || seq_k <= 0 ||
+      (d_k != 64 && d_k != 128))
+    return 0;
   const size_t sk_pad = (size_t)((seq_k + 63) / 64) * 64;
   return (size_t)batch * n_kv_head * d_k * sk_pad * 2;
 }
@@ -675,8 +859,8 @@ int tl_attention_fwd(const void* q, const void* k, const void* v, void* o, void*
   p.group = n_head / n_kv_head;
   p.seq_q = seq_q;
   p.seq_k = seq_k;
-  p.sk_pad = (seq_k + 63) / 64 * 64;
   p.n_qt = (seq_q + BM - 1) / BM;
+  p.sk_pad = (seq_k + 63) / 64 * 64;
   p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.q_ss = q_strides[2];
   p.k_sb = k_strides[0]; p.k_sh = k_strides[1]; p.k_ss = k_strides[2];
   p.v_sb = v_strides[0]; p.v_sh = v_strides[1]; p.v_ss = v_strides[2];
@@ -688,9 +872,8 @@ int tl_attention_fwd(const void* q, const void* k, const void* v, void* o, void*
     if (dtype == TL_DTYPE_F32) {
       return d_k == 64 ? launch_flash_f32<64>(p, cz, st) : launch_flash_f32<128>(p, cz, st);
     }
-    if (!workspace ||
-        workspace_bytes < tl_attention_fwd_workspace_bytes(batch, n_kv_head, seq_k, d_k, dtype) ||
-        !aligned16(workspace))
+    if (!workspace || !aligned16(workspace) ||
+        workspace_bytes < tl_attention_fwd_workspace_bytes(batch, n_kv_head, seq_k, d_k, dtype))
       return TL_ERR_INVALID;
     if (dtype == TL_DTYPE_BF16)
       return d_k == 64 ? launch_flash_16<BF16, 64>(p, workspace, cz, st)
