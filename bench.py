@@ -80,13 +80,13 @@ def cpu_threads():
 # decode
 # ---------------------------------------------------------------------------
 
-def bench_decode(cfg, steps, warmup, replicas=1, cpu=True):
+def bench_decode(cfg, steps, warmup, replicas=1, cpu=True, split=0):
     from oracle import attention as oa
     from oracle import inputs as oi
     from oracle import numerics as on
     from triton_llm import gpu
     from triton_llm.kernels import attention_decode, rope_kv_append
-    from triton_llm.kernels.decode import decode_workspace_bytes
+    from triton_llm.kernels.decode import decode_workspace, decode_workspace_bytes
 
     dt = cfg.dtype
     gdt = {"bfloat16": gpu.bfloat16, "float16": np.float16, "float32": np.float32}[dt]
@@ -106,8 +106,8 @@ def bench_decode(cfg, steps, warmup, replicas=1, cpu=True):
     cos_d = gpu.to_device(cos) if cos is not None else None
     sin_d = gpu.to_device(sin) if sin is not None else None
     out = gpu.allocate((B, Hq, D), gdt)
-    ws_bytes, split = decode_workspace_bytes(B, Hq, Hkv, cfg.max_ctx, D)
-    ws = gpu.allocate((ws_bytes,), np.uint8)
+    ws_bytes, split = decode_workspace_bytes(B, Hq, Hkv, cfg.max_ctx, D, split)
+    ws = decode_workspace(B, Hq, Hkv, cfg.max_ctx, D, split)
     lib = gpu.runtime()
 
     def step(i):
@@ -294,6 +294,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="5")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--decode-split", type=int, default=0,
+                    help="positions per decode split (multiple of 16); 0 = the library's choice")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build measures one GPU only; the attention path does not "
@@ -314,7 +316,8 @@ def main():
         if cfg.kind == "decode":
             cache_mb = 2 * cfg.batch * cfg.n_kv_head * cfg.max_ctx * cfg.d_k * (4 if cfg.dtype == "float32" else 2) / 1e6
             replicas = max(1, int(np.ceil(1024 / cache_mb))) if cache_mb < 1024 else 1
-            results[name] = bench_decode(cfg, args.steps, args.warmup, replicas=replicas, cpu=cpu)
+            results[name] = bench_decode(cfg, args.steps, args.warmup, replicas=replicas, cpu=cpu,
+                                         split=args.decode_split)
         else:
             results[name] = bench_prefill(cfg, args.steps, args.warmup, cpu=cpu)
         log(f"config {name}: {results[name]['value']:.1f} {results[name]['unit']} "

@@ -114,6 +114,9 @@ int tl_attention_fwd(const void* q, const void* k, const void* v, void* o,
  * (batch, n_kv_head, max_ctx, d_k) with {batch, head, seq} strides.
  * Sequence b attends to positions [0, min(cache_lens[b] + len_add, max_ctx)).
  * split_size: positions per split (multiple of 16); 0 picks a default.
+ * Launches the split pass and, when any sequence spans more than one split,
+ * a combine pass; the workspace holds the per-split partials and may be
+ * reused by consecutive calls on one stream.
  * ------------------------------------------------------------------------- */
 int tl_decode_split_size(int batch, int n_kv_head, int max_ctx);
 size_t tl_attention_decode_workspace_bytes(int batch, int n_head, int max_ctx,

@@ -99,9 +99,12 @@ __device__ __forceinline__ void unpack2<F16>(uint32_t w, float& lo, float& hi) {
 // ---- DPP cross-lane helpers (rows of 16 lanes) --------------------------
 // dpp_ctrl encodings (GCN/CDNA DPP): row_ror:n = 0x120 + n.
 
+// Written as update_dpp with old = 0 and bound_ctrl so the compiler can fold
+// the move into the consuming VALU op (v_add_f32_dpp); row rotations never
+// read an invalid lane, so the result equals a plain DPP move.
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float x) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
 }
 
 // Sum over the 16 lanes of a DPP row; every lane of the row receives the sum.

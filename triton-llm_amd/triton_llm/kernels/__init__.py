@@ -16,6 +16,7 @@ from .decode import (
     allocate_kv_cache,
     attention_decode,
     decode_step,
+    decode_workspace,
     rope_kv_append,
 )
 
@@ -31,4 +32,5 @@ __all__ = [
     "rope_kv_append",
     "attention_decode",
     "decode_step",
+    "decode_workspace",
 ]

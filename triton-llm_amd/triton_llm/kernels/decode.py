@@ -13,6 +13,7 @@ HBM as ``(batch, n_kv_head, max_ctx, d_k)`` per K and V and is updated in place:
   ``cache_lens[b] + s`` (one kernel);
 * :func:`attention_decode` -- split-K decode + log-sum-exp combine over
   ``cache_lens[b] + len_add`` positions;
+* :func:`decode_workspace` -- a reusable split-K workspace;
 * :func:`decode_step` -- append then attend over ``cache_lens[b] + 1``
   positions, the reference's per-layer decode sequence in two launches.
 
@@ -117,6 +118,14 @@ def decode_workspace_bytes(batch: int, n_head: int, n_kv_head: int, max_ctx: int
     if split == 0:
         split = lib.tl_decode_split_size(batch, n_kv_head, max_ctx)
     return lib.tl_attention_decode_workspace_bytes(batch, n_head, max_ctx, d_k, split), split
+
+
+def decode_workspace(batch: int, n_head: int, n_kv_head: int, max_ctx: int, d_k: int,
+                     split: int = 0):
+    """A split-K workspace for these dims, reusable by consecutive calls on
+    the library stream (calls that overlap in time need one each)."""
+    nbytes, _ = decode_workspace_bytes(batch, n_head, n_kv_head, max_ctx, d_k, split)
+    return gpu.allocate((max(nbytes, 1),), np.uint8)
 
 
 def attention_decode(q_dev, k_cache, v_cache, cache_lens, n_head: int, n_kv_head: int,
