@@ -68,6 +68,19 @@ class Events:
             self.lib.tl_event_destroy(e)
 
 
+def profile_traffic(name):
+    """HBM bytes per launch recorded in profiles/<name> (rocprofv3 FETCH_SIZE +
+    WRITE_SIZE runs of this bench, scaled by a copy-kernel calibration), or None."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_threads():
     n = os.environ.get("OMP_NUM_THREADS") or os.environ.get("OPENBLAS_NUM_THREADS")
     try:
@@ -152,7 +165,7 @@ def bench_decode(cfg, steps, warmup, replicas=1, cpu=True, split=0):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": attn_bytes / (attn_med * 1e-3) / 1e9 / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": profile_traffic("decode_split_kernel_llama3.2-3b-decode.md") if cfg.name == oi.CONFIGS["5b"].name else None,
             "algorithmic_bytes": attn_bytes,
             "kernel_ms": attn_med,
         },
@@ -162,34 +175,37 @@ def bench_decode(cfg, steps, warmup, replicas=1, cpu=True, split=0):
     return res
 
 
-def cpu_decode_baseline(cfg, data, oa, on, budget_s=15.0):
-    """NumPy fp32 decode attention on a bounded sample of sequences."""
+def cpu_decode_baseline(cfg, data, oa, on, budget_s=10.0):
+    """NumPy fp32 decode attention over every sequence of the workload,
+    repeated until ``budget_s`` of CPU time; the median pass is reported."""
     dt = cfg.dtype
     lens = data["lens"] + 1
     B, Hkv, D = cfg.batch, cfg.n_kv_head, cfg.d_k
-    order = list(range(B))
-    # fp32 copies of the sampled sequences (conversion not timed)
-    done, t_total, nbytes = [], 0.0, 0
-    for b in order:
+    # fp32 copies of each sequence's valid prefix (conversion not timed)
+    seqs = []
+    for b in range(B):
         L = int(lens[b])
-        kf = on.from_storage(data["k_cache"][b:b + 1, :, :L], dt)
-        vf = on.from_storage(data["v_cache"][b:b + 1, :, :L], dt)
-        qf = on.from_storage(data["q"][b:b + 1], dt)
+        seqs.append((on.from_storage(data["q"][b:b + 1], dt),
+                     on.from_storage(data["k_cache"][b:b + 1, :, :L], dt),
+                     on.from_storage(data["v_cache"][b:b + 1, :, :L], dt), L))
+    e = 4 if dt == "float32" else 2
+    nbytes = int(np.sum(2 * Hkv * lens.astype(np.int64) * D * e)) + 2 * B * cfg.n_head * D * e
+    passes, t_total = [], 0.0
+    while t_total < budget_s or len(passes) < 3:
         t0 = time.perf_counter()
-        oa.decode_ref(qf, kf, vf, np.array([L]), sm_scale=cfg.scale)
-        t_total += time.perf_counter() - t0
-        nbytes += 2 * Hkv * L * D * (4 if dt == "float32" else 2) + 2 * cfg.n_head * D * 2
-        done.append(b)
-        if t_total > budget_s:
-            break
+        for qf, kf, vf, L in seqs:
+            oa.decode_ref(qf, kf, vf, np.array([L]), sm_scale=cfg.scale)
+        passes.append(time.perf_counter() - t0)
+        t_total += passes[-1]
+    t = float(np.median(passes))
     return {
-        "value": nbytes / t_total / 1e9,
+        "value": nbytes / t / 1e9,
         "unit": "GB/s",
         "cores": cpu_threads(),
         "kind": "port",
-        "sample": f"{len(done)} of {B} sequences ({int(np.sum(lens[done]))} positions), "
-                  f"NumPy fp32 oracle decode, {t_total:.2f}s; bytes counted as the GPU's "
-                  f"{DT_SHORT[dt]} K/V reads",
+        "sample": f"the whole workload ({B} sequences, {int(np.sum(lens))} positions), NumPy fp32 "
+                  f"oracle decode, median of {len(passes)} passes ({t_total:.1f}s); bytes counted as "
+                  f"the GPU's {DT_SHORT[dt]} K/V/q/o traffic",
     }
 
 
@@ -249,42 +265,60 @@ def bench_prefill(cfg, steps, warmup, cpu=True):
             "peak": peak,
             "unit": "TFLOP/s",
             "frac": tf / peak,
-            "traffic": None,
+            "traffic": profile_traffic("flash_fwd_pp_llama3.2-3b-prefill.md") if cfg.name == oi.CONFIGS["5a"].name else None,
             "algorithmic_flops": flops,
             "kernel_ms": ms,
         },
     }
     if cpu:
-        res["cpu_baseline"] = cpu_prefill_baseline(cfg, raw, oa, on)
+        res["cpu_baseline"] = cpu_prefill_baseline(cfg, raw, oa, on, oi)
     return res
 
 
-def cpu_prefill_baseline(cfg, raw, oa, on, budget_s=15.0):
-    """NumPy fp32 causal attention on a bounded sample: one KV group, query
-    tiles of 512 rows taken from the end of the sequence (the longest rows)."""
+def cpu_prefill_baseline(cfg, raw, oa, on, oi, budget_s=10.0):
+    """NumPy fp32 causal attention of the whole workload (every KV group, all
+    rows, blockwise over 512-row query tiles inside the oracle), repeated
+    until ``budget_s``; the median pass is reported."""
     dt = cfg.dtype
     B, Hq, Hkv, S, D = cfg.batch, cfg.n_head, cfg.n_kv_head, cfg.seq, cfg.d_k
     g = Hq // Hkv
-    q = on.from_storage(raw["q"][:1, :g], dt)
-    k = on.from_storage(raw["k"][:1, :1], dt)
-    v = on.from_storage(raw["v"][:1, :1], dt)
-    t_total, flops, tiles = 0.0, 0, 0
-    for start in range(max(0, S - 512), -1, -512):
-        rows = np.arange(start, min(S, start + 512))
+    groups = [(on.from_storage(raw["q"][b:b + 1, h * g:(h + 1) * g], dt),
+               on.from_storage(raw["k"][b:b + 1, h:h + 1], dt),
+               on.from_storage(raw["v"][b:b + 1, h:h + 1], dt))
+              for b in range(B) for h in range(Hkv)]
+    flops = oi.prefill_flops(cfg)
+    passes, t_total = [], 0.0
+    while t_total < budget_s or not passes:
         t0 = time.perf_counter()
-        oa.attention_bhsd(q, k, v, causal=True, sm_scale=cfg.scale, rows=rows)
-        t_total += time.perf_counter() - t0
-        flops += int(np.sum(4 * g * D * (rows + 1)))
-        tiles += 1
-        if t_total > budget_s:
-            break
+        for q, k, v in groups:
+            oa.attention_bhsd(q, k, v, causal=True, sm_scale=cfg.scale, block_q=512)
+        passes.append(time.perf_counter() - t0)
+        t_total += passes[-1]
+    t = float(np.median(passes))
     return {
-        "value": flops / t_total / 1e12,
+        "value": flops / t / 1e12,
         "unit": "TFLOP/s",
         "cores": cpu_threads(),
         "kind": "port",
-        "sample": f"{tiles} x 512-row query tiles of 1 KV group ({g} heads), NumPy fp32 oracle, {t_total:.2f}s",
+        "sample": f"the whole workload ({B * Hkv} KV groups of {g} heads x {S} rows, 512-row "
+                  f"query tiles), NumPy fp32 oracle, median of {len(passes)} passes ({t_total:.1f}s)",
     }
+
+
+def copy_probe(mib):
+    """Five plain device-to-device copies of ``mib`` MiB each (one blit kernel
+    per copy): a dispatch of known HBM traffic -- mib MiB read, mib MiB
+    written -- that scales the FETCH_SIZE / WRITE_SIZE counters."""
+    from triton_llm import gpu
+
+    n = mib << 20
+    src = gpu.zeros((n,), np.uint8)
+    dst = gpu.allocate((n,), np.uint8)
+    lib = gpu.runtime()
+    for _ in range(5):
+        assert lib.tl_memcpy_dtod(dst.ptr, src.ptr, n) == 0
+    gpu.synchronize()
+    print(json.dumps({"copy_probe_bytes": n, "copies": 5}))
 
 
 def main():
@@ -294,6 +328,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="5")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe-mb", type=int, default=0,
+                    help="only run 5 device-to-device copies of this many MiB (the known-size "
+                         "reference for calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     ap.add_argument("--decode-split", type=int, default=0,
                     help="positions per decode split (multiple of 16); 0 = the library's choice")
     args = ap.parse_args()
@@ -307,6 +344,9 @@ def main():
     from triton_llm import gpu
 
     gpu.synchronize()  # initialise
+    if args.copy_probe_mb:
+        copy_probe(args.copy_probe_mb)
+        return
     cpu = not args.no_cpu
     sel = {"5": ["5a", "5b"], "all": ["1", "2", "3", "4", "5a", "5b"]}.get(args.config, [args.config])
     results = {}

@@ -5,11 +5,10 @@
 // i of head h attends to keys j of KV head h / group with j <= i + (Sk - Sq)
 // when causal; scores are (q . k) * sm_scale; online softmax over key tiles;
 // output = acc / row_sum.  The reference runs one program per (row, head)
-// with vector multiply-reduce; this kernel is a flash-style tiled kernel on
-// MFMA:
-//
-//   workgroup = 4 waves = BM = 128 query rows of one query head;
-//   each wave owns 32 query rows; key tiles of BN = 64 staged through LDS.
+// with vector multiply-reduce; these kernels are flash-style tiled kernels on
+// MFMA: each wave owns 32 query rows of one query head and walks key tiles
+// of BN = 64 staged through LDS (16-bit kernel: 8 waves = 256 rows per
+// workgroup in two ping-pong groups; fp32 kernel: 4 waves = 128 rows).
 //
 // It computes the TRANSPOSED products  S^T = K . Q^T  and  O^T = V^T . P^T
 // with 32x32 MFMA tiles.  In the 32x32 accumulator layout lane l holds
