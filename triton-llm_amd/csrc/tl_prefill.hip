@@ -194,6 +194,13 @@ __device__ __forceinline__ float sum_xor32(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// s_waitcnt vmcnt(N) (gfx9 encoding; expcnt and lgkmcnt left unconstrained).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
 // Workgroup barrier that orders LDS only (global prefetches stay in flight).
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
@@ -219,7 +226,7 @@ __global__ __launch_bounds__(PP_THREADS, 2) void flash_fwd_pp(FlashParams p) {
   constexpr int NKS = D / 16;         // k-steps of S^T
   static_assert(RPW * 8 == NREG, "tile must split into 1 KiB regions per wave");
 
-  __shared__ __attribute__((aligned(1024))) char smem[4 * TILEB];  // K0 K1 V0 V1
+  __shared__ __attribute__((aligned(1024))) char smem[6 * TILEB];  // K0 K1 K2 V0 V1 V2
 
   int b, hq, qt;
   decode_block(p, b, hq, qt);
@@ -281,41 +288,61 @@ __global__ __launch_bounds__(PP_THREADS, 2) void flash_fwd_pp(FlashParams p) {
     const int vrow = (wave + 8 * i) * VT_RPR + lane / 8;
     vt_off[i] = vrow * p.sk_pad + ((lane % 8) ^ vt_swz(vrow)) * 8;
   }
-  // Tiles are staged through registers: global loads are issued at the start
-  // of phase 2t and written to LDS at the start of phase 2t+1 (the target
-  // buffers are already free then), so their latency overlaps a whole phase.
-  // (Direct global -> LDS loads were tried; with them in the loop the
-  // compiler's wait insertion only ever waits for all LDS reads, which
-  // serialises the operand prefetch.)
-  u32x4 kst[RPW], vst[RPW];
-  auto load_k = [&](int kb) {
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-      const int key = min(kb + ld_row[i], p.seq_k - 1);  // rows past the end: any valid row
-      kst[i] = *(const u32x4*)(kbase + (int64_t)key * p.k_ss + ld_col[i]);
-    }
-  };
-  auto load_v = [&](int kb) {
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) vst[i] = *(const u32x4*)(vtbase + kb + vt_off[i]);
-  };
-  auto store_k = [&](char* buf) {
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) *(u32x4*)(buf + (wave + 8 * i) * 1024 + lane * 16) = kst[i];
-  };
-  auto store_v = [&](char* buf) {
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) *(u32x4*)(buf + (wave + 8 * i) * 1024 + lane * 16) = vst[i];
+  // Tiles go straight from global memory into LDS (global_load_lds_dwordx4:
+  // lane l of one wave instruction lands at the LDS region base + 16 l), three
+  // buffers each for K and V^T, issued about two tiles ahead: in its MFMA phase
+  // for tile t (phase 2t for group 0, 2t+1 for group 1) a wave issues its share
+  // of K_{t+2} and V^T_{t+1}, spread between its MFMAs.  A wave blocks while
+  // the CU's vector-memory path drains other waves' loads, so the issue is
+  // placed where the wave waits on the matrix pipe anyway, and the softmax
+  // wave of the phase issues no memory operations at all.  Each wave waits for
+  // its own loads with s_waitcnt vmcnt before the phase barrier that precedes
+  // their first use.  The loads are inline asm so
+  // that the compiler's wait insertion does not see LDS-DMA inside the loop:
+  // with the builtin it falls back to lgkmcnt(0) before every LDS operand read,
+  // which serialises the pipelined operand reads of the MFMA stream.  (M0 is a
+  // reserved register the compiler only sets right before the few instructions
+  // that read it; none of those appear in this kernel.)
+  auto dma = [&](const void* gaddr, char* lds) {
+    const uint32_t la = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(size_t)(__attribute__((address_space(3))) char*)lds);
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(la), "v"(gaddr) : "memory");
   };
   char* kbuf = smem;
-  char* vbuf = smem + 2 * TILEB;
+  char* vbuf = smem + 3 * TILEB;
+  auto issue_k = [&](int t) {  // K_t -> kbuf[t % 3]
+    char* buf = kbuf + (t % 3) * TILEB;
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      const int key = min(t * BN + ld_row[i], p.seq_k - 1);  // rows past the end: any valid row
+      dma(kbase + (int64_t)key * p.k_ss + ld_col[i], buf + (wave + 8 * i) * 1024);
+    }
+  };
+  auto issue_v = [&](int t) {  // V^T_t -> vbuf[t % 3]
+    char* buf = vbuf + (t % 3) * TILEB;
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) dma(vtbase + t * BN + vt_off[i], buf + (wave + 8 * i) * 1024);
+  };
+  // Entry e < 2 * RPW of the loads a wave issues in its MFMA phase for tile
+  // t: K_{t+2} region e (e < RPW), then V^T_{t+1} region e - RPW.
+  auto issue_entry = [&](int t, int e) {
+    if (e < RPW) {
+      if (t + 2 < n_kt) {
+        const int key = min((t + 2) * BN + ld_row[e], p.seq_k - 1);
+        dma(kbase + (int64_t)key * p.k_ss + ld_col[e], kbuf + ((t + 2) % 3) * TILEB + (wave + 8 * e) * 1024);
+      }
+    } else if (t + 1 < n_kt) {
+      const int i = e - RPW;
+      dma(vtbase + (t + 1) * BN + vt_off[i], vbuf + ((t + 1) % 3) * TILEB + (wave + 8 * i) * 1024);
+    }
+  };
 
   const float c = p.scale_log2;
   auto tile_active = [&](int t) { return t >= 0 && t < n_kt && t * BN < wave_k_end; };
 
   // G0(t): S^T = K_t . Q^T
   auto gemm0 = [&](int t) {
-    const char* Kb = kbuf + (t & 1) * TILEB;
+    const char* Kb = kbuf + (t % 3) * TILEB;
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
@@ -333,7 +360,7 @@ __global__ __launch_bounds__(PP_THREADS, 2) void flash_fwd_pp(FlashParams p) {
   // G1(t): O^T += V_t^T . P_t^T.  Lane (d = 32 db + lq, half h) reads the 8
   // keys 16 tt + 8 h .. +7 of the permuted V^T row d: one 16-byte chunk.
   auto gemm1 = [&](int t) {
-    const char* Vb = vbuf + (t & 1) * TILEB;
+    const char* Vb = vbuf + (t % 3) * TILEB;
 #pragma unroll
     for (int tt = 0; tt < BN / 16; ++tt)
 #pragma unroll
@@ -360,12 +387,14 @@ __global__ __launch_bounds__(PP_THREADS, 2) void flash_fwd_pp(FlashParams p) {
 #pragma unroll
     for (int tt = 0; tt < BN / 16; ++tt) v_addr[tt] = lq * (BN * 2) + (((2 * tt + h) ^ swv) << 4);
   }
+  // The wave's tile loads (issue_entry) ride along: one every 4 jobs.
   auto gemm10 = [&](int t) {
     constexpr int NG = BN / 16 * NDB;  // jobs per GEMM (== 2 * NKS)
     static_assert(NG == 2 * NKS, "S and PV job counts must match");
+    static_assert(2 * RPW <= (NG + 2) / 4, "every load needs an issue slot");
     constexpr int kPrefetch = 2;
-    const char* Kb = kbuf + (t & 1) * TILEB;
-    const char* Vb = vbuf + ((t - 1) & 1) * TILEB;
+    const char* Kb = kbuf + (t % 3) * TILEB;
+    const char* Vb = vbuf + ((t + 2) % 3) * TILEB;  // V^T_{t-1}
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
@@ -385,6 +414,7 @@ __global__ __launch_bounds__(PP_THREADS, 2) void flash_fwd_pp(FlashParams p) {
       const int tt = g / NDB, db = g % NDB;
       o_acc[db] = M::mma(__builtin_bit_cast(frag, vfr[g]), pfr[tt], o_acc[db]);
       s[g & 1] = M::mma(__builtin_bit_cast(frag, kfr[g]), qf[g >> 1], s[g & 1]);
+      if (g % 4 == 1 && g / 4 < 2 * RPW) issue_entry(t, g / 4);
       __builtin_amdgcn_sched_barrier(0);  // keep reads kPrefetch jobs ahead
     }
   };
@@ -432,28 +462,29 @@ __global__ __launch_bounds__(PP_THREADS, 2) void flash_fwd_pp(FlashParams p) {
   };
 
   if (n_kt > 0) {
-    load_k(0);
-    store_k(kbuf);
+    // Q is in registers before any DMA is issued (the compiler's own wait for
+    // Q must not cover loads it cannot see).
+    wait_vmcnt<0>();
+    issue_k(0);
+    if (n_kt > 1) issue_k(1);
+    issue_v(0);
+    if (n_kt > 1) wait_vmcnt<2 * RPW>();  // K_0 landed; K_1, V^T_0 may be in flight
+    else wait_vmcnt<RPW>();
     lds_barrier();
   }
   const int n_phase = n_kt > 0 ? 2 * n_kt + 2 : 0;
   for (int ph = 0; ph < n_phase; ++ph) {
     const int t = ph >> 1;
-    if ((ph & 1) == 0) {
-      if (t + 1 < n_kt) load_k((t + 1) * BN);
-      if (t < n_kt) load_v(t * BN);
-    } else {
-      if (t + 1 < n_kt) store_k(kbuf + ((t + 1) & 1) * TILEB);
-      if (t < n_kt) store_v(vbuf + (t & 1) * TILEB);
-    }
-    __builtin_amdgcn_sched_barrier(0);
     if ((ph & 1) == group) {
-      // MFMA phase: G1(t-1) then G0(t)
+      // MFMA phase: G1(t-1) then G0(t), plus this wave's loads for K_{t+2}
+      // and V^T_{t+1}.
       __builtin_amdgcn_s_setprio(1);
       const bool a1 = tile_active(t - 1), a0 = tile_active(t);
       if (a1 && a0) {
         gemm10(t);
       } else {
+#pragma unroll
+        for (int e = 0; e < 2 * RPW; ++e) issue_entry(t, e);
         if (a1) gemm1(t - 1);
         if (a0) gemm0(t);
       }
@@ -463,6 +494,15 @@ __global__ __launch_bounds__(PP_THREADS, 2) void flash_fwd_pp(FlashParams p) {
       if (tile_active(ta)) softmax(ta);
     }
     __builtin_amdgcn_sched_barrier(0);
+    if (ph & 1) {
+      // Phase 2t+2 reads K_{t+1} and V^T_t, issued in this wave's MFMA phase
+      // for tile t-1 (or the prologue); only the loads it issued for tile t
+      // (phase 2t or 2t+1) may still be in flight.
+      const int n_new = (t + 2 < n_kt ? RPW : 0) + (t + 1 < n_kt ? RPW : 0);
+      if (n_new == 2 * RPW) wait_vmcnt<2 * RPW>();
+      else if (n_new == RPW) wait_vmcnt<RPW>();
+      else wait_vmcnt<0>();
+    }
     lds_barrier();
   }
 
