@@ -324,8 +324,11 @@ def copy_probe(mib):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=50)
+    # The GPU's clock ramps up over the first tens of milliseconds of sustained
+    # load; 100 untimed steps (~50 ms per workload) put the timed steps at the
+    # steady-state clock (3 warmup steps under-report prefill by ~10%).
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--config", default="5")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe-mb", type=int, default=0,

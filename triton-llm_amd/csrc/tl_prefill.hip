@@ -34,6 +34,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace {
 
 constexpr int BM = 128;  // query rows per workgroup
@@ -179,6 +181,35 @@ __device__ __forceinline__ float dot2_sum<F16>(f16x8 pf, float acc) {
     acc = __builtin_amdgcn_fdot2(pr, one, acc, false);
   }
   return acc;
+}
+
+// Two fp32 values -> one 32-bit word of two 16-bit values (low half first),
+// rounded to nearest even.
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(const float (&x)[2]);
+template <>
+__device__ __forceinline__ uint32_t pack2<BF16>(const float (&x)[2]) {
+  const bf16x2 v = {(__bf16)x[0], (__bf16)x[1]};
+  return __builtin_bit_cast(uint32_t, v);
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<F16>(const float (&x)[2]) {
+  const f16x2 v = {(_Float16)x[0], (_Float16)x[1]};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// acc + lo + hi of a packed 16-bit pair (v_dot2 with (1, 1)).
+template <typename T>
+__device__ __forceinline__ float dot2_word(uint32_t w, float acc);
+template <>
+__device__ __forceinline__ float dot2_word<BF16>(uint32_t w, float acc) {
+  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), one, acc, false);
+}
+template <>
+__device__ __forceinline__ float dot2_word<F16>(uint32_t w, float acc) {
+  const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), one, acc, false);
 }
 
 // Max of lane l and lane l ^ 32 (both lanes receive it).
@@ -525,6 +556,330 @@ __global__ __launch_bounds__(PP_THREADS, 2) void flash_fwd_pp(FlashParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// 16-bit (f16 / bf16) kernel, software-pipelined inside each wave.
+//
+// Workgroup = 8 waves = 256 query rows, 32 per wave; all waves walk the same
+// 64-key K / V^T tiles.  Per tile t a wave runs
+//     region A(t):  exp / pack / row sum of S_t -> P_t         (VALU)
+//                   interleaved with S_{t+1} = K_{t+1} . Q^T   (16 MFMAs)
+//     region B(t):  O^T += V_t^T . P_t^T                       (16 MFMAs)
+//                   interleaved with mask + row max of S_{t+1} (VALU)
+//                   and this wave's loads for K_{t+3}, V^T_{t+2}
+// so the wave keeps issuing VALU work while its own MFMAs run in the matrix
+// pipe, and both waves sharing a SIMD contribute VALU issue at all times.
+// (A two-group ping-pong, where one wave does all the softmax of a phase
+// while the other issues MFMAs, is bound by one wave's VALU issue rate:
+// measured ~2000 cycles of softmax against ~1250 of MFMA per phase.)
+//
+// The running max is raised (and O rescaled) only when a tile's max exceeds
+// it by more than kRescaleLog2, between the regions of an iteration.
+// K / V^T tiles go global -> LDS with four buffers each, issued three (K)
+// and two (V^T) tiles ahead; one workgroup barrier per tile.
+// ---------------------------------------------------------------------------
+constexpr int IP_BM = 256;
+constexpr int IP_THREADS = 512;
+constexpr int IP_NBUF = 4;
+
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(IP_THREADS, 2) void flash_fwd_ip(FlashParams p) {
+  using M = Mfma<T>;
+  using frag = typename M::frag;
+  using Bits = typename T::bits;
+  constexpr int BN = PP_BN;
+  constexpr int ROWB = D * 2;         // bytes per K row in LDS
+  constexpr int TILEB = BN * ROWB;    // bytes per K or V^T tile
+  constexpr int NSL = ROWB / 16;      // 16-byte slots per K row
+  constexpr int RPR = 1024 / ROWB;    // K rows per 1 KiB region
+  constexpr int NREG = TILEB / 1024;  // 1 KiB regions per tile
+  constexpr int RPW = NREG / 8;       // regions per wave per tile
+  constexpr int NDB = D / 32;         // 32-row blocks of O^T
+  constexpr int NKS = D / 16;         // k-steps of S^T
+  constexpr int NG = 2 * NKS;         // MFMA jobs per product (S: NKS x 2, PV: 4 x NDB)
+  static_assert(RPW * 8 == NREG, "tile must split into 1 KiB regions per wave");
+  static_assert(BN / 16 * NDB == NG, "S and PV job counts must match");
+  static_assert(2 * RPW <= (NG + 2) / 4, "every tile load needs an issue slot");
+
+  __shared__ __attribute__((aligned(1024))) char smem[2 * IP_NBUF * TILEB];  // K0..K3 V0..V3
+
+  int b, hq, qt;
+  decode_block(p, b, hq, qt);
+  const int hkv = hq / p.group;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int lq = lane & 31;
+  const int h = lane >> 5;
+  const int off = p.seq_k - p.seq_q;  // bottom-right causal offset
+
+  const int q_first = qt * IP_BM;
+  const int q_last = min(p.seq_q, q_first + IP_BM) - 1;
+  int k_end = p.seq_k;
+  if (CAUSAL) k_end = max(0, min(p.seq_k, q_last + off + 1));
+  const int n_kt = (k_end + BN - 1) / BN;  // tiles the workgroup loads
+
+  const int q0 = q_first + 32 * wave;  // first row of this wave
+  const int qi = q0 + lq;              // this lane's query row
+  int wave_k_end = p.seq_k;
+  if (CAUSAL) wave_k_end = max(0, min(p.seq_k, min(q0 + 31, p.seq_q - 1) + off + 1));
+  if (q0 >= p.seq_q) wave_k_end = 0;                 // no rows: no compute
+  const int n_kw = (wave_k_end + BN - 1) / BN;        // tiles this wave computes (<= n_kt)
+
+  frag qf[NKS];
+  {
+    const Bits* qrow = (const Bits*)p.q + b * p.q_sb + hq * p.q_sh + (int64_t)qi * p.q_ss;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      u32x4 raw = {0u, 0u, 0u, 0u};
+      if (qi < p.seq_q) raw = *(const u32x4*)(qrow + 16 * ks + 8 * h);
+      qf[ks] = __builtin_bit_cast(frag, raw);
+    }
+  }
+
+  f32x16 o_acc[NDB];
+#pragma unroll
+  for (int i = 0; i < NDB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o_acc[i][r] = 0.f;
+  float m_run = -INFINITY;  // running max of scaled scores (log2 domain)
+  float l_run = 0.f;        // this lane's half of the row sum
+  float mx_next = -INFINITY;  // scaled max of the next tile's scores
+  const float c = p.scale_log2;
+
+  // ---- tile loads: global -> LDS (see flash_fwd_pp for the layout) --------
+  // Wave w fills 1 KiB regions w + 8 i of a tile.  Each load is the
+  // scalar-base form global_load_lds_dwordx4 voff, s[base]: the per-lane byte
+  // offset within a tile is a constant, the tile base advances in SGPRs and
+  // the LDS address (M0) is scalar, so a load costs no VALU work.
+  const char* kg = (const char*)((const Bits*)p.k + b * p.k_sb + hkv * p.k_sh);
+  const char* vg = (const char*)((const Bits*)p.vt + ((int64_t)b * p.n_kv + hkv) * D * p.sk_pad);
+  constexpr int VT_RPR = 1024 / (BN * 2);  // V^T rows per 1 KiB region (8)
+  auto k_row = [&](int i) { return (wave + 8 * i) * RPR + lane / NSL; };
+  auto k_col = [&](int i) { return ((lane % NSL) ^ lds_swz<D>(k_row(i))) * 8; };
+  uint32_t k_voff[RPW], v_voff[RPW];  // bytes; the host keeps them below 2^32
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    k_voff[i] = (uint32_t)(((int64_t)k_row(i) * p.k_ss + k_col(i)) * 2);
+    const int vrow = (wave + 8 * i) * VT_RPR + lane / 8;
+    v_voff[i] = (uint32_t)(((int64_t)vrow * p.sk_pad + ((lane % 8) ^ vt_swz(vrow)) * 8) * 2);
+  }
+  const uint32_t wave_lds = __builtin_amdgcn_readfirstlane((uint32_t)wave * 1024u);
+  const uint32_t lds_k0 = (uint32_t)(size_t)(__attribute__((address_space(3))) char*)smem;
+  const uint32_t lds_v0 = lds_k0 + IP_NBUF * TILEB;
+  auto dma = [&](const char* gbase, uint32_t voff, uint32_t la) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(la), "v"(voff), "s"(gbase) : "memory");
+  };
+  auto load_k = [&](int t, int i) {  // region i of K_t -> K buffer t % 4
+    uint32_t voff = k_voff[i];
+    if (t * BN + BN > p.seq_k)  // last tile: rows past the end re-read the last row
+      voff = (uint32_t)(((int64_t)min(k_row(i), p.seq_k - 1 - t * BN) * p.k_ss + k_col(i)) * 2);
+    dma(kg + (int64_t)t * BN * p.k_ss * 2, voff, lds_k0 + (t % IP_NBUF) * TILEB + i * 8192 + wave_lds);
+  };
+  auto load_v = [&](int t, int i) {  // region i of V^T_t -> V^T buffer t % 4
+    dma(vg + (int64_t)t * BN * 2, v_voff[i], lds_v0 + (t % IP_NBUF) * TILEB + i * 8192 + wave_lds);
+  };
+  // Entry e < 2 RPW of the loads issued during iteration t: K_{t+3} region e,
+  // then V^T_{t+2} region e - RPW.
+  auto load_entry = [&](int t, int e) {
+    if (e < RPW) {
+      if (t + 3 < n_kt) load_k(t + 3, e);
+    } else if (t + 2 < n_kt) {
+      load_v(t + 2, e - RPW);
+    }
+  };
+
+  // ---- LDS operand addresses -------------------------------------------------
+  // K row 32 mb + lq, 16-byte chunk (2 ks + h) ^ swz(row): with 2 ks even,
+  // (2 ks + h) ^ swz = 2 ks ^ (h ^ swz), so the address is one lane base XOR
+  // (ks << 5), and mb / the buffer add as immediates or a per-tile base.
+  // V^T row 32 db + lq, chunk (2 tt + h) ^ vt_swz(row): likewise base ^ (tt << 5).
+  const int k_lane = lq * ROWB + ((h ^ lds_swz<D>(lq)) << 4);
+  const int v_lane = lq * (BN * 2) + ((h ^ vt_swz(lq)) << 4);
+  // LDS operand reads run this many MFMA jobs ahead of their use (K, V^T).
+  constexpr int kPrefetchK = 2, kPrefetchV = 1;
+
+  // Mask S_t (keys past seq_k or above the causal diagonal) and return its
+  // scaled row max.  key = kb + 32 mb + 8 (r/4) + 4 h + r % 4.
+  auto mask_and_max = [&](f32x16 (&st)[2], int t) {
+    const int kb = t * BN;
+    const bool need_mask = (kb + BN > p.seq_k) || (CAUSAL && kb + BN - 1 > q0 + off);
+    if (need_mask) {
+      int lim = p.seq_k - 1 - kb - 4 * h;
+      if (CAUSAL) lim = min(lim, qi + off - kb - 4 * h);
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kl = 32 * mb + 8 * (r >> 2) + (r & 3);
+          st[mb][r] = kl <= lim ? st[mb][r] : -INFINITY;
+        }
+    }
+    float mx = st[0][0];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int r = (mb == 0 ? 1 : 0); r < 16; ++r) mx = fmaxf(mx, st[mb][r]);
+    return max_xor32(mx) * c;  // c > 0: scaling preserves the order
+  };
+
+  // S_t = K_t . Q^T on its own (prologue).
+  auto s_gemm = [&](f32x16 (&st)[2], int t) {
+    const char* Kb = smem + (t % IP_NBUF) * TILEB;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const frag a = __builtin_bit_cast(frag, *(const u32x4*)(Kb + (k_lane ^ ((g >> 1) << 5)) + 32 * (g & 1) * ROWB));
+      st[g & 1] = M::mma(a, qf[g >> 1], g < 2 ? f32x16{} : st[g & 1]);
+    }
+  };
+
+  // One tile step: P_t = exp(S_t - m) packed (VALU), S_{t+1} = K_{t+1} . Q^T
+  // (NG MFMAs) and O^T += V_t^T . P_t^T (NG MFMAs) in one instruction stream
+  // of 20 steps.  Step j < 16 exponentiates score pair j (P chunk j / 4);
+  // S job j runs at step j; PV job q (P chunk q / NDB) runs at step
+  // 4 (q / NDB) + 4 + q % NDB, the first step after its chunk is complete.
+  // This wave's tile loads ride along every fourth step.
+  // DO_S / DO_P: compute S_{t+1} / the softmax + PV of tile t.
+  u32x4 pw[BN / 16];  // P_t, packed 16-bit, as the PV MFMA's B operand
+  auto tile_step = [&](f32x16 (&cur)[2], f32x16 (&nxt)[2], int t, auto do_s_tag, auto do_p_tag) {
+    constexpr bool DO_S = decltype(do_s_tag)::value;
+    constexpr bool DO_P = decltype(do_p_tag)::value;
+    const float nb = (m_run == -INFINITY) ? 0.f : -m_run;
+    const int kb_lane = k_lane + ((t + 1) % IP_NBUF) * TILEB;              // K_{t+1}
+    const int vb_lane = v_lane + (IP_NBUF + t % IP_NBUF) * TILEB;          // V^T_t
+    u32x4 kfr[NG], vfr[NG];
+    auto fetch_k = [&](int g) {
+      kfr[g] = *(const u32x4*)(smem + (kb_lane ^ ((g >> 1) << 5)) + 32 * (g & 1) * ROWB);
+    };
+    auto fetch_v = [&](int q) {
+      const int tt = q / NDB, db = q % NDB;
+      vfr[q] = *(const u32x4*)(smem + (vb_lane ^ (tt << 5)) + 32 * db * (BN * 2));
+    };
+    if constexpr (DO_S) {
+#pragma unroll
+      for (int g = 0; g < kPrefetchK; ++g) fetch_k(g);
+    }
+    if constexpr (DO_P) {
+#pragma unroll
+      for (int q = 0; q < kPrefetchV; ++q) fetch_v(q);
+    }
+#pragma unroll
+    for (int j = 0; j < 20; ++j) {
+      if constexpr (DO_S) {
+        if (j < NG) {
+          if (j + kPrefetchK < NG) fetch_k(j + kPrefetchK);
+          nxt[j & 1] = M::mma(__builtin_bit_cast(frag, kfr[j]), qf[j >> 1], j < 2 ? f32x16{} : nxt[j & 1]);
+        }
+      }
+      if constexpr (DO_P) {
+        if (j < 16) {
+          const int tt = j >> 2, j2 = j & 3;
+          const float x0 = cur[tt >> 1][8 * (tt & 1) + 2 * j2];
+          const float x1 = cur[tt >> 1][8 * (tt & 1) + 2 * j2 + 1];
+          float pr2[2] = {fast_exp2(fmaf(x0, c, nb)), fast_exp2(fmaf(x1, c, nb))};
+          const uint32_t w = pack2<T>(pr2);
+          pw[tt][j2] = w;
+          l_run = dot2_word<T>(w, l_run);
+        }
+#pragma unroll
+        for (int q = 0; q < NG; ++q) {
+          if (4 * (q / NDB) + 4 + q % NDB == j) {
+            if (q + kPrefetchV < NG) fetch_v(q + kPrefetchV);
+            o_acc[q % NDB] = M::mma(__builtin_bit_cast(frag, vfr[q]), __builtin_bit_cast(frag, pw[q / NDB]),
+                                    o_acc[q % NDB]);
+          }
+        }
+      }
+      if (j % 4 == 1 && j / 4 < 2 * RPW) load_entry(t, j / 4);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // ---- prologue -------------------------------------------------------------
+  f32x16 sa[2], sb[2];
+  if (n_kt > 0) {
+    // Q is in registers before any DMA is issued (the compiler's own wait for
+    // Q must not cover loads it cannot see).
+    wait_vmcnt<0>();
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) load_k(0, i);
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) if (1 < n_kt) load_k(1, i);
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) load_v(0, i);
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) if (2 < n_kt) load_k(2, i);
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) if (1 < n_kt) load_v(1, i);
+    // K_0 first: everything issued after it may still be in flight.
+    const int after0 = (1 < n_kt ? 2 * RPW : 0) + RPW + (2 < n_kt ? RPW : 0) + (1 < n_kt ? RPW : 0);
+    if (after0 == 4 * RPW) wait_vmcnt<4 * RPW>();
+    else if (after0 == 3 * RPW) wait_vmcnt<3 * RPW>();
+    else wait_vmcnt<RPW>();
+    lds_barrier();
+    if (n_kw > 0) {
+      s_gemm(sa, 0);
+      mx_next = mask_and_max(sa, 0);
+    }
+    // K_1 and V^T_0 for iteration 0; K_2 and V^T_1 may still be in flight.
+    const int late = (2 < n_kt ? RPW : 0) + (1 < n_kt ? RPW : 0);
+    if (late == 2 * RPW) wait_vmcnt<2 * RPW>();
+    else if (late == RPW) wait_vmcnt<RPW>();
+    else wait_vmcnt<0>();
+    lds_barrier();
+  }
+
+  // ---- main loop: iteration t uses S_t in `cur`, builds S_{t+1} in `nxt` ----
+  auto iteration = [&](f32x16 (&cur)[2], f32x16 (&nxt)[2], int t) {
+    const bool act = t < n_kw, act_next = t + 1 < n_kw;
+    if (act) {
+      // Raise the running max (and rescale) only when this tile exceeds it by
+      // more than 2^kRescaleLog2.
+      if (__any(mx_next > m_run + kRescaleLog2)) {
+        const float m_new = fmaxf(m_run, mx_next);
+        const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2(m_run - m_new);
+        m_run = m_new;
+        l_run *= alpha;
+#pragma unroll
+        for (int i = 0; i < NDB; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o_acc[i][r] *= alpha;
+      }
+    }
+    if (act && act_next) tile_step(cur, nxt, t, std::true_type{}, std::true_type{});
+    else if (act) tile_step(cur, nxt, t, std::false_type{}, std::true_type{});
+    else tile_step(cur, nxt, t, std::false_type{}, std::false_type{});
+    if (act_next) mx_next = mask_and_max(nxt, t + 1);
+    // Iteration t+1 reads K_{t+2} and V^T_{t+1}, issued during iteration t-1
+    // (or the prologue); only this iteration's loads may still be in flight.
+    const int n_new = (t + 3 < n_kt ? RPW : 0) + (t + 2 < n_kt ? RPW : 0);
+    if (n_new == 2 * RPW) wait_vmcnt<2 * RPW>();
+    else if (n_new == RPW) wait_vmcnt<RPW>();
+    else wait_vmcnt<0>();
+    lds_barrier();
+  };
+  for (int t = 0; t < n_kt; t += 2) {
+    iteration(sa, sb, t);
+    if (t + 1 < n_kt) iteration(sb, sa, t + 1);
+  }
+
+  // Epilogue: O[qi][d] = O^T[d][qi] / l.
+  const float inv = 1.f / sum_xor32(l_run);
+  if (qi < p.seq_q) {
+    Bits* orow = (Bits*)p.o + b * p.o_sb + hq * p.o_sh + (int64_t)qi * p.o_ss;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d0 = 32 * db + 8 * rq + 4 * h;
+        uint32_t w0 = (uint32_t)from_f32<T>(o_acc[db][4 * rq + 0] * inv) |
+                      ((uint32_t)from_f32<T>(o_acc[db][4 * rq + 1] * inv) << 16);
+        uint32_t w1 = (uint32_t)from_f32<T>(o_acc[db][4 * rq + 2] * inv) |
+                      ((uint32_t)from_f32<T>(o_acc[db][4 * rq + 3] * inv) << 16);
+        *(u32x2*)(orow + d0) = u32x2{w0, w1};
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // fp32 kernel (v_mfma_f32_32x32x2_f32).  K-step mapping for S^T: lane half h
 // covers d = h*D/2 + 4c + i for step (c, i), so both K (LDS) and Q (global)
 // are read as 16-byte chunks.
@@ -824,12 +1179,12 @@ int launch_flash_16(FlashParams& p, void* ws, bool causal, hipStream_t st) {
                      p.seq_k, p.sk_pad, p.n_kv, p.v_sb, p.v_sh, p.v_ss);
   int e = tl_launch_status();
   if (e) return e;
-  p.n_qt = (p.seq_q + PP_BM - 1) / PP_BM;
+  p.n_qt = (p.seq_q + IP_BM - 1) / IP_BM;
   dim3 grid((unsigned)(p.n_qt * p.n_head * p.batch));
   if (causal)
-    hipLaunchKernelGGL((flash_fwd_pp<T, D, true>), grid, dim3(PP_THREADS), 0, st, p);
+    hipLaunchKernelGGL((flash_fwd_ip<T, D, true>), grid, dim3(IP_THREADS), 0, st, p);
   else
-    hipLaunchKernelGGL((flash_fwd_pp<T, D, false>), grid, dim3(PP_THREADS), 0, st, p);
+    hipLaunchKernelGGL((flash_fwd_ip<T, D, false>), grid, dim3(IP_THREADS), 0, st, p);
   return tl_launch_status();
 }
 
@@ -857,7 +1212,14 @@ bool mfma_shape_ok(const FlashParams& p, int d_k, int dtype) {
   const int64_t s[] = {p.q_sb, p.q_sh, p.q_ss, p.k_sb, p.k_sh, p.k_ss,
                        p.v_sb, p.v_sh, p.v_ss, p.o_sb, p.o_sh, p.o_ss};
   for (int64_t x : s)
-    if (x % vec) return false;
+    if (x < 0 || x % vec) return false;
+  if (dtype != TL_DTYPE_F32) {
+    // The 16-bit kernel addresses a K tile (64 rows) and a head's V^T copy
+    // with 32-bit byte offsets.
+    const int64_t sk_pad = (p.seq_k + 63) / 64 * 64;
+    if ((64 * p.k_ss + d_k) * 2 >= ((int64_t)1 << 32) || (int64_t)d_k * sk_pad * 2 >= ((int64_t)1 << 32))
+      return false;
+  }
   return aligned16(p.q) && aligned16(p.k) && aligned16(p.v) && aligned16(p.o);
 }
 
