@@ -631,7 +631,17 @@ __global__ __launch_bounds__(IP_THREADS, 2) void flash_fwd_ip(FlashParams p) {
     for (int ks = 0; ks < NKS; ++ks) {
       u32x4 raw = {0u, 0u, 0u, 0u};
       if (qi < p.seq_q) raw = *(const u32x4*)(qrow + 16 * ks + 8 * h);
-      qf[ks] = __builtin_bit_cast(frag, raw);
+      // q <- round(q * sm_scale * log2 e): S then comes out of the MFMA
+      // already in the exp2 domain (a relative perturbation of q of at most
+      // half an ulp of the 16-bit type, like the rounding of P itself).
+      uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float lo, hi;
+        unpack2<T>(w[i], lo, hi);
+        w[i] = (uint32_t)from_f32<T>(lo * p.scale_log2) | ((uint32_t)from_f32<T>(hi * p.scale_log2) << 16);
+      }
+      qf[ks] = __builtin_bit_cast(frag, u32x4{w[0], w[1], w[2], w[3]});
     }
   }
 
@@ -640,10 +650,18 @@ __global__ __launch_bounds__(IP_THREADS, 2) void flash_fwd_ip(FlashParams p) {
   for (int i = 0; i < NDB; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o_acc[i][r] = 0.f;
-  float m_run = -INFINITY;  // running max of scaled scores (log2 domain)
-  float l_run = 0.f;        // this lane's half of the row sum
-  float mx_next = -INFINITY;  // scaled max of the next tile's scores
-  const float c = p.scale_log2;
+  // Scores are kept relative to a per-row offset m_run (log2 domain): every
+  // S tile is accumulated on top of s_init = -m_run (the MFMA's C operand), so
+  // p = exp2(S) needs no per-score arithmetic.  m_run starts at 0 ("fresh":
+  // no visible key yet); it is set by the first visible tile and raised only
+  // when a tile's max exceeds it by more than 2^kRescaleLog2.
+  float m_run = 0.f;
+  bool fresh = true;
+  float l_run = 0.f;          // this lane's half of the row sum
+  float mx_next = -INFINITY;  // max of the next tile's relative scores
+  f32x16 s_init;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) s_init[r] = 0.f;
 
   // ---- tile loads: global -> LDS (see flash_fwd_pp for the layout) --------
   // Wave w fills 1 KiB regions w + 8 i of a tile.  Each load is the
@@ -695,7 +713,7 @@ __global__ __launch_bounds__(IP_THREADS, 2) void flash_fwd_ip(FlashParams p) {
   const int k_lane = lq * ROWB + ((h ^ lds_swz<D>(lq)) << 4);
   const int v_lane = lq * (BN * 2) + ((h ^ vt_swz(lq)) << 4);
   // LDS operand reads run this many MFMA jobs ahead of their use (K, V^T).
-  constexpr int kPrefetchK = 2, kPrefetchV = 1;
+  constexpr int kPrefetchK = 2, kPrefetchV = 2;
 
   // Mask S_t (keys past seq_k or above the causal diagonal) and return its
   // scaled row max.  key = kb + 32 mb + 8 (r/4) + 4 h + r % 4.
@@ -718,7 +736,7 @@ __global__ __launch_bounds__(IP_THREADS, 2) void flash_fwd_ip(FlashParams p) {
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
       for (int r = (mb == 0 ? 1 : 0); r < 16; ++r) mx = fmaxf(mx, st[mb][r]);
-    return max_xor32(mx) * c;  // c > 0: scaling preserves the order
+    return max_xor32(mx);
   };
 
   // S_t = K_t . Q^T on its own (prologue).
@@ -727,22 +745,28 @@ __global__ __launch_bounds__(IP_THREADS, 2) void flash_fwd_ip(FlashParams p) {
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       const frag a = __builtin_bit_cast(frag, *(const u32x4*)(Kb + (k_lane ^ ((g >> 1) << 5)) + 32 * (g & 1) * ROWB));
-      st[g & 1] = M::mma(a, qf[g >> 1], g < 2 ? f32x16{} : st[g & 1]);
+      st[g & 1] = M::mma(a, qf[g >> 1], g < 2 ? s_init : st[g & 1]);
     }
   };
 
   // One tile step: P_t = exp(S_t - m) packed (VALU), S_{t+1} = K_{t+1} . Q^T
   // (NG MFMAs) and O^T += V_t^T . P_t^T (NG MFMAs) in one instruction stream
   // of 20 steps.  Step j < 16 exponentiates score pair j (P chunk j / 4);
-  // S job j runs at step j; PV job q (P chunk q / NDB) runs at step
+  // S jobs 2j, 2j + 1 run at step j; PV job q (P chunk q / NDB) runs at step
   // 4 (q / NDB) + 4 + q % NDB, the first step after its chunk is complete.
-  // This wave's tile loads ride along every fourth step.
-  // DO_S / DO_P: compute S_{t+1} / the softmax + PV of tile t.
+  // With MAXS the row max of S_{t+1} is folded in over the steps after the
+  // last S job, while only PV MFMAs remain, so no serial max follows the
+  // stream.  This wave's tile loads ride along every fourth step.
+  // DO_S / DO_P / MAXS: compute S_{t+1} / the softmax + PV of tile t / the
+  // max of S_{t+1} (only when tile t+1 needs no mask).
   u32x4 pw[BN / 16];  // P_t, packed 16-bit, as the PV MFMA's B operand
-  auto tile_step = [&](f32x16 (&cur)[2], f32x16 (&nxt)[2], int t, auto do_s_tag, auto do_p_tag) {
+  auto tile_step = [&](f32x16 (&cur)[2], f32x16 (&nxt)[2], int t, auto do_s_tag, auto do_p_tag,
+                       auto maxs_tag) {
     constexpr bool DO_S = decltype(do_s_tag)::value;
     constexpr bool DO_P = decltype(do_p_tag)::value;
-    const float nb = (m_run == -INFINITY) ? 0.f : -m_run;
+    constexpr bool MAXS = decltype(maxs_tag)::value;
+    constexpr int kMaxStep0 = NG / 2 + 2;  // first step of the in-stream max
+    float mx = -INFINITY;
     const int kb_lane = k_lane + ((t + 1) % IP_NBUF) * TILEB;              // K_{t+1}
     const int vb_lane = v_lane + (IP_NBUF + t % IP_NBUF) * TILEB;          // V^T_t
     u32x4 kfr[NG], vfr[NG];
@@ -764,17 +788,29 @@ __global__ __launch_bounds__(IP_THREADS, 2) void flash_fwd_ip(FlashParams p) {
 #pragma unroll
     for (int j = 0; j < 20; ++j) {
       if constexpr (DO_S) {
-        if (j < NG) {
-          if (j + kPrefetchK < NG) fetch_k(j + kPrefetchK);
-          nxt[j & 1] = M::mma(__builtin_bit_cast(frag, kfr[j]), qf[j >> 1], j < 2 ? f32x16{} : nxt[j & 1]);
+#pragma unroll
+        for (int g = 2 * j; g < 2 * j + 2; ++g) {
+          if (g < NG) {
+            if (g + kPrefetchK < NG) fetch_k(g + kPrefetchK);
+            nxt[g & 1] = M::mma(__builtin_bit_cast(frag, kfr[g]), qf[g >> 1], g < 2 ? s_init : nxt[g & 1]);
+          }
         }
+      }
+      if constexpr (MAXS) {
+        // four scores per step: nxt[mb][r], 4 (j - kMaxStep0) <= 16 mb + r < +4
+        const int i0 = 4 * (j - kMaxStep0);
+        if (i0 >= 0 && i0 < 32) {
+          mx = fmaxf(mx, fmaxf(fmaxf(nxt[i0 >> 4][i0 & 15], nxt[i0 >> 4][(i0 & 15) + 1]),
+                               fmaxf(nxt[i0 >> 4][(i0 & 15) + 2], nxt[i0 >> 4][(i0 & 15) + 3])));
+        }
+        if (j == kMaxStep0 + 8) mx_next = max_xor32(mx);
       }
       if constexpr (DO_P) {
         if (j < 16) {
           const int tt = j >> 2, j2 = j & 3;
           const float x0 = cur[tt >> 1][8 * (tt & 1) + 2 * j2];
           const float x1 = cur[tt >> 1][8 * (tt & 1) + 2 * j2 + 1];
-          float pr2[2] = {fast_exp2(fmaf(x0, c, nb)), fast_exp2(fmaf(x1, c, nb))};
+          float pr2[2] = {fast_exp2(x0), fast_exp2(x1)};
           const uint32_t w = pack2<T>(pr2);
           pw[tt][j2] = w;
           l_run = dot2_word<T>(w, l_run);
@@ -830,24 +866,39 @@ __global__ __launch_bounds__(IP_THREADS, 2) void flash_fwd_ip(FlashParams p) {
   // ---- main loop: iteration t uses S_t in `cur`, builds S_{t+1} in `nxt` ----
   auto iteration = [&](f32x16 (&cur)[2], f32x16 (&nxt)[2], int t) {
     const bool act = t < n_kw, act_next = t + 1 < n_kw;
+    const int kb1 = (t + 1) * BN;
+    const bool mask_next = (kb1 + BN > p.seq_k) || (CAUSAL && kb1 + BN - 1 > q0 + off);
     if (act) {
-      // Raise the running max (and rescale) only when this tile exceeds it by
-      // more than 2^kRescaleLog2.
-      if (__any(mx_next > m_run + kRescaleLog2)) {
-        const float m_new = fmaxf(m_run, mx_next);
-        const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2(m_run - m_new);
-        m_run = m_new;
+      // Move the offset when this tile's max exceeds it by more than
+      // 2^kRescaleLog2, or when a fresh row sees its first visible key.
+      const bool grow = fresh ? (mx_next != -INFINITY) : (mx_next > kRescaleLog2);
+      if (__any(grow)) {
+        // delta >= 0 unless fresh (then o_acc and l are still zero)
+        const float delta = fresh ? (mx_next == -INFINITY ? 0.f : mx_next) : fmaxf(mx_next, 0.f);
+        const float alpha = fast_exp2(-delta);
+        m_run += delta;
+        fresh = fresh && (mx_next == -INFINITY);
         l_run *= alpha;
 #pragma unroll
         for (int i = 0; i < NDB; ++i)
 #pragma unroll
           for (int r = 0; r < 16; ++r) o_acc[i][r] *= alpha;
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) cur[mb][r] -= delta;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s_init[r] = -m_run;
       }
     }
-    if (act && act_next) tile_step(cur, nxt, t, std::true_type{}, std::true_type{});
-    else if (act) tile_step(cur, nxt, t, std::false_type{}, std::true_type{});
-    else tile_step(cur, nxt, t, std::false_type{}, std::false_type{});
-    if (act_next) mx_next = mask_and_max(nxt, t + 1);
+    if (act && act_next && !mask_next) {
+      tile_step(cur, nxt, t, std::true_type{}, std::true_type{}, std::true_type{});
+    } else {
+      if (act && act_next) tile_step(cur, nxt, t, std::true_type{}, std::true_type{}, std::false_type{});
+      else if (act) tile_step(cur, nxt, t, std::false_type{}, std::true_type{}, std::false_type{});
+      else tile_step(cur, nxt, t, std::false_type{}, std::false_type{}, std::false_type{});
+      if (act_next) mx_next = mask_and_max(nxt, t + 1);
+    }
     // Iteration t+1 reads K_{t+2} and V^T_{t+1}, issued during iteration t-1
     // (or the prologue); only this iteration's loads may still be in flight.
     const int n_new = (t + 3 < n_kt ? RPW : 0) + (t + 2 < n_kt ? RPW : 0);
@@ -863,6 +914,330 @@ __global__ __launch_bounds__(IP_THREADS, 2) void flash_fwd_ip(FlashParams p) {
 
   // Epilogue: O[qi][d] = O^T[d][qi] / l.
   const float inv = 1.f / sum_xor32(l_run);
+  if (qi < p.seq_q) {
+    Bits* orow = (Bits*)p.o + b * p.o_sb + hq * p.o_sh + (int64_t)qi * p.o_ss;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d0 = 32 * db + 8 * rq + 4 * h;
+        uint32_t w0 = (uint32_t)from_f32<T>(o_acc[db][4 * rq + 0] * inv) |
+                      ((uint32_t)from_f32<T>(o_acc[db][4 * rq + 1] * inv) << 16);
+        uint32_t w1 = (uint32_t)from_f32<T>(o_acc[db][4 * rq + 2] * inv) |
+                      ((uint32_t)from_f32<T>(o_acc[db][4 * rq + 3] * inv) << 16);
+        *(u32x2*)(orow + d0) = u32x2{w0, w1};
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 16-bit (f16 / bf16) kernel: two wave groups in ping-pong, light softmax.
+//
+// Workgroup = 8 waves = 2 groups of 4; wave w owns 32 query rows, group g
+// the rows [128 g, 128 g + 128) of the workgroup's 256.  Per tile t a group
+// runs G(t) = {O^T += V_{t-1}^T . P_{t-1}^T, S_t = K_t . Q^T} (32 MFMAs in
+// one stream) and A(t) = softmax of S_t -> P_t, in phases separated by
+// workgroup barriers:
+//     phase 2t   : group 0 runs G(t)   group 1 runs A(t-1)
+//     phase 2t+1 : group 0 runs A(t)   group 1 runs G(t)
+// so on every SIMD (waves w and w + 4 share one) one wave keeps the matrix
+// pipe busy while the other does its softmax.  The softmax is kept short so
+// it hides under the partner's MFMAs:
+//   * Q is pre-scaled by sm_scale * log2 e and every S tile accumulates on
+//     top of s_init = -m (the MFMA's C operand), so P = exp2(S) with no
+//     per-score arithmetic;
+//   * the row max is a tree (independent max3 chains), the row sum four
+//     independent fp32 add chains (v_dot2 would stall behind the partner's
+//     MFMAs);
+//   * the running max moves only when a tile exceeds it by 2^kRescaleLog2.
+// K / V^T tiles go global -> LDS (scalar-base global_load_lds, no VALU work),
+// three buffers each, issued by each wave between the MFMAs of its G phase
+// two tiles ahead.
+// ---------------------------------------------------------------------------
+constexpr int P2_BM = 256;
+constexpr int P2_THREADS = 512;
+constexpr int P2_NBUF = 3;
+
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(P2_THREADS, 2) void flash_fwd_pp2(FlashParams p) {
+  using M = Mfma<T>;
+  using frag = typename M::frag;
+  using Bits = typename T::bits;
+  constexpr int BN = PP_BN;
+  constexpr int ROWB = D * 2;         // bytes per K row in LDS
+  constexpr int TILEB = BN * ROWB;    // bytes per K or V^T tile
+  constexpr int NSL = ROWB / 16;      // 16-byte slots per K row
+  constexpr int RPR = 1024 / ROWB;    // K rows per 1 KiB region
+  constexpr int NREG = TILEB / 1024;  // 1 KiB regions per tile
+  constexpr int RPW = NREG / 8;       // regions per wave per tile
+  constexpr int NDB = D / 32;         // 32-row blocks of O^T
+  constexpr int NKS = D / 16;         // k-steps of S^T
+  constexpr int NG = 2 * NKS;         // MFMA jobs per product
+  static_assert(RPW * 8 == NREG, "tile must split into 1 KiB regions per wave");
+  static_assert(BN / 16 * NDB == NG, "S and PV job counts must match");
+  static_assert(2 * RPW <= (NG + 2) / 4, "every tile load needs an issue slot");
+
+  __shared__ __attribute__((aligned(1024))) char smem[2 * P2_NBUF * TILEB];  // K0..K2 V0..V2
+
+  int b, hq, qt;
+  decode_block(p, b, hq, qt);
+  const int hkv = hq / p.group;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int group = wave >> 2;
+  const int lq = lane & 31;
+  const int h = lane >> 5;
+  const int off = p.seq_k - p.seq_q;  // bottom-right causal offset
+
+  const int q_first = qt * P2_BM;
+  const int q_last = min(p.seq_q, q_first + P2_BM) - 1;
+  int k_end = p.seq_k;
+  if (CAUSAL) k_end = max(0, min(p.seq_k, q_last + off + 1));
+  const int n_kt = (k_end + BN - 1) / BN;  // tiles the workgroup loads
+
+  const int q0 = q_first + 128 * group + 32 * (wave & 3);  // first row of this wave
+  const int qi = q0 + lq;                                  // this lane's query row
+  int wave_k_end = p.seq_k;
+  if (CAUSAL) wave_k_end = max(0, min(p.seq_k, min(q0 + 31, p.seq_q - 1) + off + 1));
+  if (q0 >= p.seq_q) wave_k_end = 0;  // no rows: no compute
+
+  // Q, pre-scaled: q <- round(q * sm_scale * log2 e), so S comes out of the
+  // MFMA in the exp2 domain (a relative perturbation of q of at most half an
+  // ulp of the 16-bit type, like the rounding of P itself).
+  frag qf[NKS];
+  {
+    const Bits* qrow = (const Bits*)p.q + b * p.q_sb + hq * p.q_sh + (int64_t)qi * p.q_ss;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      u32x4 raw = {0u, 0u, 0u, 0u};
+      if (qi < p.seq_q) raw = *(const u32x4*)(qrow + 16 * ks + 8 * h);
+      uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float lo, hi;
+        unpack2<T>(w[i], lo, hi);
+        w[i] = (uint32_t)from_f32<T>(lo * p.scale_log2) | ((uint32_t)from_f32<T>(hi * p.scale_log2) << 16);
+      }
+      qf[ks] = __builtin_bit_cast(frag, u32x4{w[0], w[1], w[2], w[3]});
+    }
+  }
+
+  f32x16 o_acc[NDB];
+#pragma unroll
+  for (int i = 0; i < NDB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o_acc[i][r] = 0.f;
+  // Scores are kept relative to a per-row offset m_run (log2 domain): S
+  // accumulates on top of s_init = -m_run.  m_run starts at 0 with `fresh`
+  // set (no visible key yet); it is set by the first visible tile and then
+  // raised only when a tile's max exceeds it by more than 2^kRescaleLog2.
+  float m_run = 0.f;
+  bool fresh = true;
+  float l4[4] = {0.f, 0.f, 0.f, 0.f};  // this lane's half of the row sum, 4 chains
+  f32x16 s_init;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) s_init[r] = 0.f;
+  f32x16 s[2];        // S_t (relative scores)
+  u32x4 pw[BN / 16];  // P_t packed 16-bit, the PV MFMA's B operand
+
+  // ---- tile loads: global -> LDS ---------------------------------------------
+  // Wave w fills 1 KiB regions w + 8 i of a tile; lane l of a region holds K
+  // row R * RPR + l / NSL, chunk (l % NSL) ^ swz(row) (V^T: row R * 8 + l / 8,
+  // chunk (l % 8) ^ vt_swz(row)).  Scalar-base form: the per-lane byte offset
+  // is constant, the tile base and the LDS address (M0) are scalars.
+  const char* kg = (const char*)((const Bits*)p.k + b * p.k_sb + hkv * p.k_sh);
+  const char* vg = (const char*)((const Bits*)p.vt + ((int64_t)b * p.n_kv + hkv) * D * p.sk_pad);
+  constexpr int VT_RPR = 1024 / (BN * 2);
+  auto k_row = [&](int i) { return (wave + 8 * i) * RPR + lane / NSL; };
+  auto k_col = [&](int i) { return ((lane % NSL) ^ lds_swz<D>(k_row(i))) * 8; };
+  // Offsets for a full K tile, and for the last (possibly partial) K tile of
+  // the sequence, whose rows past seq_k re-read its last row.
+  const int t_klast = (p.seq_k - 1) / BN;
+  uint32_t k_voff[RPW], k_voff_last[RPW], v_voff[RPW];  // bytes; the host keeps them below 2^32
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    k_voff[i] = (uint32_t)(((int64_t)k_row(i) * p.k_ss + k_col(i)) * 2);
+    k_voff_last[i] =
+        (uint32_t)(((int64_t)min(k_row(i), p.seq_k - 1 - t_klast * BN) * p.k_ss + k_col(i)) * 2);
+    const int vrow = (wave + 8 * i) * VT_RPR + lane / 8;
+    v_voff[i] = (uint32_t)(((int64_t)vrow * p.sk_pad + ((lane % 8) ^ vt_swz(vrow)) * 8) * 2);
+  }
+  const uint32_t wave_lds = __builtin_amdgcn_readfirstlane((uint32_t)wave * 1024u);
+  const uint32_t lds_k0 = (uint32_t)(size_t)(__attribute__((address_space(3))) char*)smem;
+  const uint32_t lds_v0 = lds_k0 + P2_NBUF * TILEB;
+  auto dma = [&](const char* gbase, uint32_t voff, uint32_t la) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(la), "v"(voff), "s"(gbase) : "memory");
+  };
+  // Loads are unconditional (no branches inside the MFMA stream): a slot
+  // past the last tile re-loads the last tile into its dead buffer.
+  auto load_k = [&](int slot, int i) {  // region i of K_{min(slot, n_kt-1)} -> K buffer slot % 3
+    const int tk = min(slot, n_kt - 1);
+    const uint32_t voff = tk == t_klast ? k_voff_last[i] : k_voff[i];
+    dma(kg + (int64_t)tk * BN * p.k_ss * 2, voff, lds_k0 + (slot % P2_NBUF) * TILEB + i * 8192 + wave_lds);
+  };
+  auto load_v = [&](int slot, int i) {  // region i of V^T_{min(slot, n_kt-1)} -> V^T buffer slot % 3
+    const int tv = min(slot, n_kt - 1);
+    dma(vg + (int64_t)tv * BN * 2, v_voff[i], lds_v0 + (slot % P2_NBUF) * TILEB + i * 8192 + wave_lds);
+  };
+  // Entry e < 2 RPW of the loads a wave issues in its G phase for tile t:
+  // K_{t+2} region e, then V^T_{t+1} region e - RPW.
+  auto load_entry = [&](int t, int e) {
+    if (e < RPW) load_k(t + 2, e);
+    else load_v(t + 1, e - RPW);
+  };
+
+  // ---- LDS operand addresses --------------------------------------------------
+  // K row 32 mb + lq, chunk (2 ks + h) ^ swz(row) = 2 ks ^ (h ^ swz): one lane
+  // base XOR (ks << 5); V^T row 32 db + lq: base ^ (tt << 5).
+  const int k_lane = lq * ROWB + ((h ^ lds_swz<D>(lq)) << 4);
+  const int v_lane = lq * (BN * 2) + ((h ^ vt_swz(lq)) << 4);
+  constexpr int kPrefetch = 2;  // operand reads run this many jobs ahead
+
+  auto tile_active = [&](int t) { return t >= 0 && t < n_kt && t * BN < wave_k_end; };
+
+  // G(t): PV job g (keys 16 (g / NDB).., d-block g % NDB) of tile t-1 and S
+  // job g (k-step g / 2, key block g % 2) of tile t, alternating; DO_PV /
+  // DO_S select the halves (first / last tile).  Loads ride every 4th job.
+  auto g_phase = [&](int t, auto do_pv_tag, auto do_s_tag) {
+    constexpr bool DO_PV = decltype(do_pv_tag)::value;
+    constexpr bool DO_S = decltype(do_s_tag)::value;
+    const int kb_lane = k_lane + (t % P2_NBUF) * TILEB;                     // K_t
+    const int vb_lane = v_lane + (P2_NBUF + (t + 2) % P2_NBUF) * TILEB;     // V^T_{t-1}
+    u32x4 kfr[NG], vfr[NG];
+    auto fetch = [&](int g) {
+      if constexpr (DO_PV) {
+        const int tt = g / NDB, db = g % NDB;
+        vfr[g] = *(const u32x4*)(smem + (vb_lane ^ (tt << 5)) + 32 * db * (BN * 2));
+      }
+      if constexpr (DO_S) kfr[g] = *(const u32x4*)(smem + (kb_lane ^ ((g >> 1) << 5)) + 32 * (g & 1) * ROWB);
+    };
+#pragma unroll
+    for (int g = 0; g < kPrefetch; ++g) fetch(g);
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      if (g + kPrefetch < NG) fetch(g + kPrefetch);
+      if constexpr (DO_PV) {
+        const int tt = g / NDB, db = g % NDB;
+        o_acc[db] = M::mma(__builtin_bit_cast(frag, vfr[g]), __builtin_bit_cast(frag, pw[tt]), o_acc[db]);
+      }
+      if constexpr (DO_S)
+        s[g & 1] = M::mma(__builtin_bit_cast(frag, kfr[g]), qf[g >> 1], g < 2 ? s_init : s[g & 1]);
+      if (g % 4 == 1 && g / 4 < 2 * RPW) load_entry(t, g / 4);
+      __builtin_amdgcn_sched_barrier(0);  // keep reads kPrefetch jobs ahead
+    }
+  };
+
+  // A(t): masked softmax of S_t -> P_t.  key = kb + 32 mb + 8 (r/4) + 4 h + r % 4.
+  auto a_phase = [&](int t) {
+    const int kb = t * BN;
+    const bool need_mask = (kb + BN > p.seq_k) || (CAUSAL && kb + BN - 1 > q0 + off);
+    if (need_mask) {
+      int lim = p.seq_k - 1 - kb - 4 * h;
+      if (CAUSAL) lim = min(lim, qi + off - kb - 4 * h);
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kl = 32 * mb + 8 * (r >> 2) + (r & 3);
+          s[mb][r] = kl <= lim ? s[mb][r] : -INFINITY;
+        }
+    }
+    // row max: four independent chains of 8, then a lane-pair exchange
+    float mq[4];
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) {
+      const f32x16& v = s[c4 >> 1];
+      const int o = 8 * (c4 & 1);
+      mq[c4] = fmaxf(fmaxf(fmaxf(v[o], v[o + 1]), v[o + 2]), fmaxf(fmaxf(v[o + 3], v[o + 4]), v[o + 5]));
+      mq[c4] = fmaxf(mq[c4], fmaxf(v[o + 6], v[o + 7]));
+    }
+    const float mx = max_xor32(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3])));
+    const bool grow = fresh ? (mx != -INFINITY) : (mx > kRescaleLog2);
+    if (__any(grow)) {
+      // delta >= 0 unless fresh (then o_acc and l are still zero)
+      const float delta = fresh ? (mx == -INFINITY ? 0.f : mx) : fmaxf(mx, 0.f);
+      const float alpha = fast_exp2(-delta);
+      m_run += delta;
+      fresh = fresh && (mx == -INFINITY);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) l4[k] *= alpha;
+#pragma unroll
+      for (int i = 0; i < NDB; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o_acc[i][r] *= alpha;
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[mb][r] -= delta;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s_init[r] = -m_run;
+    }
+    // P = exp2(S): P chunk tt (keys 16 tt..) = s[tt / 2][8 (tt % 2) + 0..7]
+#pragma unroll
+    for (int tt = 0; tt < BN / 16; ++tt)
+#pragma unroll
+      for (int j2 = 0; j2 < 4; ++j2) {
+        float pr2[2] = {fast_exp2(s[tt >> 1][8 * (tt & 1) + 2 * j2]),
+                        fast_exp2(s[tt >> 1][8 * (tt & 1) + 2 * j2 + 1])};
+        pw[tt][j2] = pack2<T>(pr2);
+        // fp32 adds, not v_dot2 on the packed pair: on gfx950 the dot2
+        // instructions do not co-execute with the partner wave's MFMAs
+        // (measured: a dot2 stream runs 2.6x slower beside an MFMA stream,
+        // an add stream ~10%).
+        l4[j2] += pr2[0] + pr2[1];
+      }
+  };
+
+  // ---- prologue: K_0, K_1, V^T_0 ------------------------------------------
+  if (n_kt > 0) {
+    // Q is in registers before any DMA is issued (the compiler's own wait for
+    // Q must not cover loads it cannot see).
+    wait_vmcnt<0>();
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) load_k(0, i);
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) load_k(1, i);
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) load_v(0, i);
+    wait_vmcnt<2 * RPW>();  // K_0 landed; K_1, V^T_0 may be in flight
+    lds_barrier();
+  }
+  const int n_phase = n_kt > 0 ? 2 * n_kt + 2 : 0;
+  for (int ph = 0; ph < n_phase; ++ph) {
+    const int t = ph >> 1;
+    if ((ph & 1) == group) {
+      __builtin_amdgcn_s_setprio(1);
+      const bool a1 = tile_active(t - 1), a0 = tile_active(t);
+      if (a1 && a0) {
+        g_phase(t, std::true_type{}, std::true_type{});
+      } else if (a1) {
+        g_phase(t, std::true_type{}, std::false_type{});
+      } else if (a0) {
+        g_phase(t, std::false_type{}, std::true_type{});
+      } else {
+#pragma unroll
+        for (int e = 0; e < 2 * RPW; ++e) load_entry(t, e);
+      }
+      __builtin_amdgcn_s_setprio(0);
+    } else {
+      const int ta = group == 0 ? t : t - 1;
+      if (tile_active(ta)) a_phase(ta);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (ph & 1) {
+      // Phase 2t+2 reads K_{t+1} and V^T_t, issued in this wave's G phase for
+      // tile t-1 (or the prologue); only its 2 RPW loads for tile t may still
+      // be in flight.
+      wait_vmcnt<2 * RPW>();
+    }
+    lds_barrier();
+  }
+  // No LDS-DMA may land after the workgroup has left its LDS.
+  wait_vmcnt<0>();
+
+  // Epilogue: O[qi][d] = O^T[d][qi] / l.
+  const float inv = 1.f / sum_xor32((l4[0] + l4[1]) + (l4[2] + l4[3]));
   if (qi < p.seq_q) {
     Bits* orow = (Bits*)p.o + b * p.o_sb + hq * p.o_sh + (int64_t)qi * p.o_ss;
 #pragma unroll
@@ -1179,12 +1554,12 @@ int launch_flash_16(FlashParams& p, void* ws, bool causal, hipStream_t st) {
                      p.seq_k, p.sk_pad, p.n_kv, p.v_sb, p.v_sh, p.v_ss);
   int e = tl_launch_status();
   if (e) return e;
-  p.n_qt = (p.seq_q + IP_BM - 1) / IP_BM;
+  p.n_qt = (p.seq_q + P2_BM - 1) / P2_BM;
   dim3 grid((unsigned)(p.n_qt * p.n_head * p.batch));
   if (causal)
-    hipLaunchKernelGGL((flash_fwd_ip<T, D, true>), grid, dim3(IP_THREADS), 0, st, p);
+    hipLaunchKernelGGL((flash_fwd_pp2<T, D, true>), grid, dim3(P2_THREADS), 0, st, p);
   else
-    hipLaunchKernelGGL((flash_fwd_ip<T, D, false>), grid, dim3(IP_THREADS), 0, st, p);
+    hipLaunchKernelGGL((flash_fwd_pp2<T, D, false>), grid, dim3(P2_THREADS), 0, st, p);
   return tl_launch_status();
 }
 
