@@ -20,6 +20,10 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource, dword 3 for CDNA (32-bit data format, no swizzle).
+constexpr int kBufRsrcWord3 = 0x00020000;
 
 // Storage type tags.  `bits` is the raw 16/32-bit pattern type.
 struct F32 {

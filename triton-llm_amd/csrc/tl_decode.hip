@@ -44,8 +44,6 @@ constexpr int kStreams = 16;  // lane-groups per workgroup
 constexpr int kUnroll = 4;    // keys in flight per stream
 constexpr int kKeysPerIter = kStreams * kUnroll;
 constexpr float kRescaleLog2 = 8.f;
-// Raw buffer resource, dword 3 for CDNA (32-bit data format, no swizzle).
-constexpr int kRsrcWord3 = 0x00020000;
 constexpr int kAuxNontemporal = 2;  // buffer-load cache policy: nt
 
 template <int W>
@@ -54,7 +52,7 @@ struct Slice {
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcWord3);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufRsrcWord3);
 }
 
 // Nontemporal load of one W-word row slice at byte offset voff + soff.

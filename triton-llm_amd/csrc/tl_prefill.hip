@@ -1157,7 +1157,7 @@ __global__ __launch_bounds__(P2_THREADS, 2) void flash_fwd_pp2(FlashParams p) {
     if (__any(grow)) {
       // delta >= 0 unless fresh (then o_acc and l are still zero)
       const float delta = fresh ? (mx == -INFINITY ? 0.f : mx) : fmaxf(mx, 0.f);
-      const float alpha = fast_exp2(-delta);
+      const float alpha = fresh ? 1.f : fast_exp2(-delta);  // fresh: nothing to scale, 2^-mx may overflow
       m_run += delta;
       fresh = fresh && (mx == -INFINITY);
 #pragma unroll
@@ -1235,6 +1235,332 @@ __global__ __launch_bounds__(P2_THREADS, 2) void flash_fwd_pp2(FlashParams p) {
   }
   // No LDS-DMA may land after the workgroup has left its LDS.
   wait_vmcnt<0>();
+
+  // Epilogue: O[qi][d] = O^T[d][qi] / l.
+  const float inv = 1.f / sum_xor32((l4[0] + l4[1]) + (l4[2] + l4[3]));
+  if (qi < p.seq_q) {
+    Bits* orow = (Bits*)p.o + b * p.o_sb + hq * p.o_sh + (int64_t)qi * p.o_ss;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d0 = 32 * db + 8 * rq + 4 * h;
+        uint32_t w0 = (uint32_t)from_f32<T>(o_acc[db][4 * rq + 0] * inv) |
+                      ((uint32_t)from_f32<T>(o_acc[db][4 * rq + 1] * inv) << 16);
+        uint32_t w1 = (uint32_t)from_f32<T>(o_acc[db][4 * rq + 2] * inv) |
+                      ((uint32_t)from_f32<T>(o_acc[db][4 * rq + 3] * inv) << 16);
+        *(u32x2*)(orow + d0) = u32x2{w0, w1};
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 16-bit (f16 / bf16) kernel: ping-pong over 128-key tiles.
+//
+// Same scheme as flash_fwd_pp2 (two groups of four waves alternating a G
+// phase -- PV of tile t-1 and S of tile t, now 2 x 32 MFMAs -- with an A
+// phase, the softmax of tile t) but with 128-key tiles, so every phase does
+// twice the work for the same fixed costs (the phase barrier, the LDS
+// latency before a G phase's first MFMA, the loop).  Registers: O^T 64, S
+// 64, P 32, Q 32, s_init 16 per lane.  LDS: two 32 KiB buffers each for K
+// and V^T (d_k 128).  Group 0 issues all loads of tile t+1 (K) and t (V^T)
+// early in its G phase for tile t, so they have the rest of that phase and
+// the next to land.
+// ---------------------------------------------------------------------------
+constexpr int P3_BM = 256;
+constexpr int P3_BN = 128;
+constexpr int P3_THREADS = 512;
+
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp3(FlashParams p) {
+  using M = Mfma<T>;
+  using frag = typename M::frag;
+  using Bits = typename T::bits;
+  constexpr int BN = P3_BN;
+  constexpr int ROWB = D * 2;          // bytes per K row in LDS
+  constexpr int VROWB = BN * 2;        // bytes per V^T row in LDS (256)
+  constexpr int TILEB = BN * ROWB;     // bytes per K or V^T tile
+  constexpr int NSL = ROWB / 16;       // 16-byte slots per K row
+  constexpr int RPR = 1024 / ROWB;     // K rows per 1 KiB region
+  constexpr int NREG = TILEB / 1024;   // 1 KiB regions per tile
+  constexpr int RPW = NREG / 4;        // regions per group-0 wave per tile (K or V^T)
+  constexpr int NDB = D / 32;          // 32-row blocks of O^T
+  constexpr int NKS = D / 16;          // k-steps of S^T
+  constexpr int NMB = BN / 32;         // 32-key blocks of S^T
+  constexpr int NG = NMB * NKS;        // MFMA jobs per product
+  static_assert(BN / 16 * NDB == NG, "S and PV job counts must match");
+  static_assert(2 * RPW <= NG / 2, "every tile load needs an issue slot");
+
+  __shared__ __attribute__((aligned(1024))) char smem[4 * TILEB];  // K0 K1 V0 V1
+
+  int b, hq, qt;
+  decode_block(p, b, hq, qt);
+  const int hkv = hq / p.group;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: phase branches are scalar
+  const int group = wave >> 2;
+  const int lq = lane & 31;
+  const int h = lane >> 5;
+  const int off = p.seq_k - p.seq_q;  // bottom-right causal offset
+
+  const int q_first = qt * P3_BM;
+  const int q_last = min(p.seq_q, q_first + P3_BM) - 1;
+  int k_end = p.seq_k;
+  if (CAUSAL) k_end = max(0, min(p.seq_k, q_last + off + 1));
+  const int n_kt = (k_end + BN - 1) / BN;  // tiles the workgroup loads
+
+  const int q0 = q_first + 128 * group + 32 * (wave & 3);  // first row of this wave
+  const int qi = q0 + lq;                                  // this lane's query row
+  int wave_k_end = p.seq_k;
+  if (CAUSAL) wave_k_end = max(0, min(p.seq_k, min(q0 + 31, p.seq_q - 1) + off + 1));
+  if (q0 >= p.seq_q) wave_k_end = 0;  // no rows: no compute
+
+  // Q pre-scaled by sm_scale * log2 e (see flash_fwd_pp2).
+  frag qf[NKS];
+  {
+    const Bits* qrow = (const Bits*)p.q + b * p.q_sb + hq * p.q_sh + (int64_t)qi * p.q_ss;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      u32x4 raw = {0u, 0u, 0u, 0u};
+      if (qi < p.seq_q) raw = *(const u32x4*)(qrow + 16 * ks + 8 * h);
+      uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float lo, hi;
+        unpack2<T>(w[i], lo, hi);
+        w[i] = (uint32_t)from_f32<T>(lo * p.scale_log2) | ((uint32_t)from_f32<T>(hi * p.scale_log2) << 16);
+      }
+      qf[ks] = __builtin_bit_cast(frag, u32x4{w[0], w[1], w[2], w[3]});
+    }
+  }
+
+  f32x16 o_acc[NDB];
+#pragma unroll
+  for (int i = 0; i < NDB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o_acc[i][r] = 0.f;
+  float m_run = 0.f;  // offset of the relative scores (see flash_fwd_pp2)
+  bool fresh = true;
+  float l4[4] = {0.f, 0.f, 0.f, 0.f};
+  f32x16 s_init;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) s_init[r] = 0.f;
+  f32x16 s[NMB];      // S_t (relative scores)
+  u32x4 pw[BN / 16];  // P_t packed 16-bit
+
+  // ---- tile loads (group 0 only, scalar-base LDS-DMA) ------------------------
+  // K: region R holds rows R * RPR + l / NSL, slot l % NSL = chunk (l % NSL) ^
+  // swz(row).  V^T: region R holds rows 4 R + l / 16 (256-byte rows), slot
+  // l % 16 = chunk (l % 16) ^ swz128(row).  Wave w of group 0 fills regions
+  // w + 4 i; the swizzle term does not depend on i, so one lane offset per
+  // tensor serves every region and the region step goes into the scalar base.
+  // K is read through a buffer resource whose size stops at the last key the
+  // workgroup uses: rows past it read as zeros (and are masked), with no
+  // per-lane clamp.  V^T tiles always lie inside the padded workspace.
+  const char* kg = (const char*)((const Bits*)p.k + b * p.k_sb + hkv * p.k_sh);
+  const char* vg = (const char*)((const Bits*)p.vt + ((int64_t)b * p.n_kv + hkv) * D * p.sk_pad);
+  const int wq = wave & 3;
+  const int k_row0 = wq * RPR + lane / NSL;  // row of region wq; region wq + 4 i adds 4 i RPR
+  const uint32_t k_voff = (uint32_t)(((int64_t)k_row0 * p.k_ss + ((lane % NSL) ^ lds_swz<D>(k_row0)) * 8) * 2);
+  const int v_row0 = 4 * wq + lane / 16;
+  const uint32_t v_voff =
+      (uint32_t)(((int64_t)v_row0 * p.sk_pad + ((lane % 16) ^ lds_swz<128>(v_row0)) * 8) * 2);
+  const uint32_t wave_lds = __builtin_amdgcn_readfirstlane((uint32_t)wq * 1024u);
+  const uint32_t lds_k0 = (uint32_t)(size_t)(__attribute__((address_space(3))) char*)smem;
+  const uint32_t lds_v0 = lds_k0 + 2 * TILEB;
+  const int k_rows = min(p.seq_k, n_kt * BN);  // keys the workgroup reads
+  const int64_t k_ss2 = p.k_ss * 2;
+  const uint32_t v_region = 16u * (uint32_t)p.sk_pad * 2u;  // bytes of 16 V^T rows
+  auto dma = [&](const i32x4& rsrc, uint32_t voff, uint32_t la) __attribute__((always_inline)) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(la), "v"(voff), "s"(rsrc)
+                 : "memory");
+  };
+  auto rsrc_of = [&](const char* base, uint32_t bytes) __attribute__((always_inline)) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    // every word wave-uniform, so the resource stays in SGPRs
+    return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+                 __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu)),
+                 __builtin_amdgcn_readfirstlane((int)bytes), kBufRsrcWord3};
+  };
+  // Regions wq + 4 i of K_tk (tile rows 4 i RPR .. 4 (i + 1) RPR - 1) into K
+  // buffer `buf`; rows past k_rows read as zeros and cost no traffic.
+  auto load_k = [&](int tk, int buf, int i) __attribute__((always_inline)) {
+    const int r0 = tk * BN + 4 * i * RPR;
+    const int rows = min(max(k_rows - r0, 0), 4 * RPR);
+    dma(rsrc_of(kg + (int64_t)r0 * k_ss2, (uint32_t)rows * (uint32_t)k_ss2), k_voff,
+        lds_k0 + buf * TILEB + i * 4096 + wave_lds);
+  };
+  // Regions wq + 4 i of V^T_tv (rows 16 i .. 16 i + 15) into V^T buffer `buf`;
+  // nothing is read for tv >= n_kt.
+  auto load_v = [&](int tv, int buf, int i) __attribute__((always_inline)) {
+    dma(rsrc_of(vg + ((int64_t)16 * i * p.sk_pad + (int64_t)tv * BN) * 2, tv < n_kt ? v_region : 0u), v_voff,
+        lds_v0 + buf * TILEB + i * 4096 + wave_lds);
+  };
+
+  // ---- LDS operand addresses -------------------------------------------------
+  const int k_lane = lq * ROWB + ((h ^ lds_swz<D>(lq)) << 4);
+  const int v_lane = lq * VROWB + ((h ^ lds_swz<128>(lq)) << 4);
+  constexpr int kPrefetch = 2;
+  static_assert(NMB == 4, "S jobs are ordered for four key blocks");
+  constexpr auto s_mb = [](int g) { return 2 * (g / (2 * NKS)) + (g & 1); };
+  constexpr auto s_ks = [](int g) { return (g % (2 * NKS)) >> 1; };
+
+  // G(t): job g = PV job g of tile t-1 (keys 16 (g / NDB).., d-block g % NDB)
+  // and S job g of tile t.  S jobs fill key blocks in pairs (0 1, then 2 3),
+  // alternating the pair, so only half of S is live while the first half of
+  // P is consumed.  Every G phase runs both products: the P of a tile a wave
+  // does not use is zero (its PV adds nothing) and the S of such a tile is
+  // never read, which keeps one straight-line MFMA stream per group.  Group 0
+  // issues, one every other job, the loads of K_{t+1} and then V^T_t.
+  auto g_phase = [&](int t, auto dma_tag) __attribute__((always_inline)) {
+    constexpr bool DO_DMA = decltype(dma_tag)::value;
+    int kb_lane = k_lane + (t & 1) * TILEB;               // K_t
+    int vb_lane = v_lane + (2 + ((t + 1) & 1)) * TILEB;  // V^T_{t-1}
+    // Opaque per phase, so the per-job addresses are formed in the job that
+    // uses them instead of being hoisted and kept live across the loop.
+    asm volatile("" : "+v"(kb_lane), "+v"(vb_lane));
+    u32x4 kfr[NG], vfr[NG];
+    auto fetch = [&](int g) __attribute__((always_inline)) {
+      const int tt = g / NDB, db = g % NDB;
+      vfr[g] = *(const u32x4*)(smem + (vb_lane ^ (tt << 5)) + 32 * db * VROWB);
+      const int ks = s_ks(g), mb = s_mb(g);
+      kfr[g] = *(const u32x4*)(smem + (kb_lane ^ (ks << 5)) + 32 * mb * ROWB);
+    };
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int g = 0; g < kPrefetch; ++g) fetch(g);
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      if (g + kPrefetch < NG) fetch(g + kPrefetch);
+      {
+        const int tt = g / NDB, db = g % NDB;
+        o_acc[db] = M::mma(__builtin_bit_cast(frag, vfr[g]), __builtin_bit_cast(frag, pw[tt]), o_acc[db]);
+      }
+      {
+        const int ks = s_ks(g), mb = s_mb(g);
+        s[mb] = M::mma(__builtin_bit_cast(frag, kfr[g]), qf[ks], ks == 0 ? s_init : s[mb]);
+      }
+      if constexpr (DO_DMA) {
+        if (g % 2 == 1 && g / 2 < RPW) load_k(t + 1, (t + 1) & 1, g / 2);
+        if (g % 2 == 1 && g / 2 >= RPW && g / 2 < 2 * RPW) load_v(t, t & 1, g / 2 - RPW);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __builtin_amdgcn_s_setprio(0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // A(t): masked softmax of S_t -> P_t.  key = kb + 32 mb + 8 (r/4) + 4 h + r % 4.
+  // A tile the wave does not use yields P = 0.
+  auto a_phase = [&](int t) __attribute__((always_inline)) {
+    const int kb = t * BN;
+    if (t >= n_kt || kb >= wave_k_end) {
+#pragma unroll
+      for (int tt = 0; tt < BN / 16; ++tt) pw[tt] = u32x4{0u, 0u, 0u, 0u};
+      __builtin_amdgcn_sched_barrier(0);
+      return;
+    }
+    const bool need_mask = (kb + BN > p.seq_k) || (CAUSAL && kb + BN - 1 > q0 + off);
+    if (need_mask) {
+      int lim = p.seq_k - 1 - kb - 4 * h;
+      if (CAUSAL) lim = min(lim, qi + off - kb - 4 * h);
+#pragma unroll
+      for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kl = 32 * mb + 8 * (r >> 2) + (r & 3);
+          s[mb][r] = kl <= lim ? s[mb][r] : -INFINITY;
+        }
+    }
+    float mq[NMB];
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) {
+      const f32x16& v = s[mb];
+      float a = fmaxf(fmaxf(fmaxf(v[0], v[1]), v[2]), fmaxf(fmaxf(v[3], v[4]), v[5]));
+      float c2 = fmaxf(fmaxf(fmaxf(v[8], v[9]), v[10]), fmaxf(fmaxf(v[11], v[12]), v[13]));
+      a = fmaxf(a, fmaxf(v[6], v[7]));
+      c2 = fmaxf(c2, fmaxf(v[14], v[15]));
+      mq[mb] = fmaxf(a, c2);
+    }
+    float mxl = mq[0];
+#pragma unroll
+    for (int mb = 1; mb < NMB; ++mb) mxl = fmaxf(mxl, mq[mb]);
+    const float mx = max_xor32(mxl);
+    const bool grow = fresh ? (mx != -INFINITY) : (mx > kRescaleLog2);
+    if (__any(grow)) {
+      const float delta = fresh ? (mx == -INFINITY ? 0.f : mx) : fmaxf(mx, 0.f);
+      const float alpha = fresh ? 1.f : fast_exp2(-delta);  // fresh: nothing to scale, 2^-mx may overflow
+      m_run += delta;
+      fresh = fresh && (mx == -INFINITY);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) l4[k] *= alpha;
+#pragma unroll
+      for (int i = 0; i < NDB; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o_acc[i][r] *= alpha;
+#pragma unroll
+      for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[mb][r] -= delta;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s_init[r] = -m_run;
+    }
+    // P chunk tt (keys 16 tt..) = s[tt / 2][8 (tt % 2) + 0..7]; fp32 row sums
+    // (v_dot2 does not co-execute with the partner's MFMAs).
+#pragma unroll
+    for (int tt = 0; tt < BN / 16; ++tt)
+#pragma unroll
+      for (int j2 = 0; j2 < 4; ++j2) {
+        float pr2[2] = {fast_exp2(s[tt >> 1][8 * (tt & 1) + 2 * j2]),
+                        fast_exp2(s[tt >> 1][8 * (tt & 1) + 2 * j2 + 1])};
+        pw[tt][j2] = pack2<T>(pr2);
+        l4[j2] += pr2[0] + pr2[1];
+      }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // ---- prologue ----------------------------------------------------------------
+  // K_0 by all eight waves.  P and the V^T buffer the first PV products (of
+  // tile -1) read start as zeros, so those products add nothing.
+#pragma unroll
+  for (int tt = 0; tt < BN / 16; ++tt) pw[tt] = u32x4{0u, 0u, 0u, 0u};
+  if (n_kt > 0) {
+#pragma unroll
+    for (int i = tid; i < TILEB / 16; i += P3_THREADS) *(u32x4*)(smem + 3 * TILEB + 16 * i) = u32x4{0u, 0u, 0u, 0u};
+    wait_vmcnt<0>();  // Q is in registers before any DMA is issued
+#pragma unroll
+    for (int i = group; i < RPW; i += 2) load_k(0, 0, i);  // regions wq + 4 i, split by group
+    wait_vmcnt<0>();
+    lds_barrier();
+  }
+  // Phases 2t (group 0: G(t), group 1: A(t-1)) and 2t+1 (group 0: A(t),
+  // group 1: G(t)) for t = 0 .. n_kt.  One loop per group keeps S and P
+  // from both being live across the loop edge.  Phase 2t+2 reads K_{t+1} and
+  // V^T_t, which group 0 issued during phase 2t and waits for at the end of
+  // phase 2t+1.
+  if (n_kt > 0) {
+    if (group == 0) {
+      for (int t = 0; t <= n_kt; ++t) {
+        g_phase(t, std::true_type{});
+        lds_barrier();
+        a_phase(t);
+        wait_vmcnt<0>();
+        lds_barrier();
+      }
+    } else {
+      lds_barrier();  // phase 0: nothing to do (A of tile -1)
+      g_phase(0, std::false_type{});
+      lds_barrier();
+      for (int t = 1; t <= n_kt; ++t) {
+        a_phase(t - 1);
+        lds_barrier();
+        g_phase(t, std::false_type{});
+        lds_barrier();
+      }
+    }
+  }
+  wait_vmcnt<0>();  // no LDS-DMA may land after the workgroup has left its LDS
 
   // Epilogue: O[qi][d] = O^T[d][qi] / l.
   const float inv = 1.f / sum_xor32((l4[0] + l4[1]) + (l4[2] + l4[3]));
@@ -1437,7 +1763,7 @@ __global__ __launch_bounds__(kThreads, D == 128 ? 1 : 2) void flash_fwd_f32(Flas
 }
 
 // ---------------------------------------------------------------------------
-// V (b, kv, s, d) -> V^T (b, kv, d, s_pad), s_pad a multiple of 64, keys past
+// V (b, kv, s, d) -> V^T (b, kv, d, s_pad), s_pad a multiple of 128, keys past
 // seq_k zero-filled.  Within each group of 16 keys the stored order is
 //     position 16 u + 8 h + j  <-  key 16 u + 8 (j / 4) + 4 h + (j % 4)
 // which is the key order of the PV MFMA's k-index for lane half h (the S^T
@@ -1554,12 +1880,12 @@ int launch_flash_16(FlashParams& p, void* ws, bool causal, hipStream_t st) {
                      p.seq_k, p.sk_pad, p.n_kv, p.v_sb, p.v_sh, p.v_ss);
   int e = tl_launch_status();
   if (e) return e;
-  p.n_qt = (p.seq_q + P2_BM - 1) / P2_BM;
+  p.n_qt = (p.seq_q + P3_BM - 1) / P3_BM;
   dim3 grid((unsigned)(p.n_qt * p.n_head * p.batch));
   if (causal)
-    hipLaunchKernelGGL((flash_fwd_pp2<T, D, true>), grid, dim3(P2_THREADS), 0, st, p);
+    hipLaunchKernelGGL((flash_fwd_pp3<T, D, true>), grid, dim3(P3_THREADS), 0, st, p);
   else
-    hipLaunchKernelGGL((flash_fwd_pp2<T, D, false>), grid, dim3(P2_THREADS), 0, st, p);
+    hipLaunchKernelGGL((flash_fwd_pp3<T, D, false>), grid, dim3(P3_THREADS), 0, st, p);
   return tl_launch_status();
 }
 
@@ -1591,7 +1917,7 @@ bool mfma_shape_ok(const FlashParams& p, int d_k, int dtype) {
   if (dtype != TL_DTYPE_F32) {
     // The 16-bit kernel addresses a K tile (64 rows) and a head's V^T copy
     // with 32-bit byte offsets.
-    const int64_t sk_pad = (p.seq_k + 63) / 64 * 64;
+    const int64_t sk_pad = (p.seq_k + 127) / 128 * 128;
     if ((64 * p.k_ss + d_k) * 2 >= ((int64_t)1 << 32) || (int64_t)d_k * sk_pad * 2 >= ((int64_t)1 << 32))
       return false;
   }
@@ -1609,7 +1935,7 @@ size_t tl_attention_fwd_workspace_bytes(int batch, int n_kv_head, int seq_k, int
   if (dtype == TL_DTYPE_F32 || batch <= 0 || n_kv_head <= 0 || seq_k <= 0 ||
       (d_k != 64 && d_k != 128))
     return 0;
-  const size_t sk_pad = (size_t)((seq_k + 63) / 64) * 64;
+  const size_t sk_pad = (size_t)((seq_k + 127) / 128) * 128;
   return (size_t)batch * n_kv_head * d_k * sk_pad * 2;
 }
 
@@ -1636,7 +1962,7 @@ int tl_attention_fwd(const void* q, const void* k, const void* v, void* o, void*
   p.seq_q = seq_q;
   p.seq_k = seq_k;
   p.n_qt = (seq_q + BM - 1) / BM;
-  p.sk_pad = (seq_k + 63) / 64 * 64;
+  p.sk_pad = (seq_k + 127) / 128 * 128;
   p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.q_ss = q_strides[2];
   p.k_sb = k_strides[0]; p.k_sh = k_strides[1]; p.k_ss = k_strides[2];
   p.v_sb = v_strides[0]; p.v_sh = v_strides[1]; p.v_ss = v_strides[2];
