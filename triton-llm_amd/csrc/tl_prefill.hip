@@ -1370,8 +1370,9 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp3(FlashParams p) {
   const uint32_t lds_k0 = (uint32_t)(size_t)(__attribute__((address_space(3))) char*)smem;
   const uint32_t lds_v0 = lds_k0 + 2 * TILEB;
   const int k_rows = min(p.seq_k, n_kt * BN);  // keys the workgroup reads
-  const int64_t k_ss2 = p.k_ss * 2;
-  const uint32_t v_region = 16u * (uint32_t)p.sk_pad * 2u;  // bytes of 16 V^T rows
+  const uint32_t k_ss2 = (uint32_t)p.k_ss * 2u;
+  const uint32_t k_step = 4u * RPR * k_ss2;                // bytes of 4 regions of K rows
+  const uint32_t v_step = 16u * (uint32_t)p.sk_pad * 2u;  // bytes of 16 V^T rows
   auto dma = [&](const i32x4& rsrc, uint32_t voff, uint32_t la) __attribute__((always_inline)) {
     asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(la), "v"(voff), "s"(rsrc)
                  : "memory");
@@ -1383,19 +1384,23 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp3(FlashParams p) {
                  __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu)),
                  __builtin_amdgcn_readfirstlane((int)bytes), kBufRsrcWord3};
   };
-  // Regions wq + 4 i of K_tk (tile rows 4 i RPR .. 4 (i + 1) RPR - 1) into K
-  // buffer `buf`; rows past k_rows read as zeros and cost no traffic.
-  auto load_k = [&](int tk, int buf, int i) __attribute__((always_inline)) {
-    const int r0 = tk * BN + 4 * i * RPR;
-    const int rows = min(max(k_rows - r0, 0), 4 * RPR);
-    dma(rsrc_of(kg + (int64_t)r0 * k_ss2, (uint32_t)rows * (uint32_t)k_ss2), k_voff,
-        lds_k0 + buf * TILEB + i * 4096 + wave_lds);
+  // One resource per tile, built once per phase; the region offset goes into
+  // the (range-checked) lane offset.  K rows past k_rows read as zeros and
+  // cost no traffic; nothing is read for V^T tiles past the last one.
+  auto k_rsrc = [&](int tk) __attribute__((always_inline)) {
+    const int rows = min(max(k_rows - tk * BN, 0), BN);
+    return rsrc_of(kg + (int64_t)tk * BN * k_ss2, (uint32_t)rows * k_ss2);
   };
-  // Regions wq + 4 i of V^T_tv (rows 16 i .. 16 i + 15) into V^T buffer `buf`;
-  // nothing is read for tv >= n_kt.
-  auto load_v = [&](int tv, int buf, int i) __attribute__((always_inline)) {
-    dma(rsrc_of(vg + ((int64_t)16 * i * p.sk_pad + (int64_t)tv * BN) * 2, tv < n_kt ? v_region : 0u), v_voff,
-        lds_v0 + buf * TILEB + i * 4096 + wave_lds);
+  auto v_rsrc = [&](int tv) __attribute__((always_inline)) {
+    return rsrc_of(vg + (int64_t)tv * BN * 2, tv < n_kt ? (uint32_t)D * (uint32_t)p.sk_pad * 2u : 0u);
+  };
+  // Regions wq + 4 i of a K tile (tile rows 4 i RPR ..) into K buffer `buf`.
+  auto load_k = [&](const i32x4& rs, int buf, int i) __attribute__((always_inline)) {
+    dma(rs, k_voff + (uint32_t)i * k_step, lds_k0 + buf * TILEB + i * 4096 + wave_lds);
+  };
+  // Regions wq + 4 i of a V^T tile (rows 16 i ..) into V^T buffer `buf`.
+  auto load_v = [&](const i32x4& rs, int buf, int i) __attribute__((always_inline)) {
+    dma(rs, v_voff + (uint32_t)i * v_step, lds_v0 + buf * TILEB + i * 4096 + wave_lds);
   };
 
   // ---- LDS operand addresses -------------------------------------------------
@@ -1415,6 +1420,11 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp3(FlashParams p) {
   // issues, one every other job, the loads of K_{t+1} and then V^T_t.
   auto g_phase = [&](int t, auto dma_tag) __attribute__((always_inline)) {
     constexpr bool DO_DMA = decltype(dma_tag)::value;
+    i32x4 rk = {0, 0, 0, 0}, rv = {0, 0, 0, 0};
+    if constexpr (DO_DMA) {
+      rk = k_rsrc(t + 1);
+      rv = v_rsrc(t);
+    }
     int kb_lane = k_lane + (t & 1) * TILEB;               // K_t
     int vb_lane = v_lane + (2 + ((t + 1) & 1)) * TILEB;  // V^T_{t-1}
     // Opaque per phase, so the per-job addresses are formed in the job that
@@ -1442,8 +1452,8 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp3(FlashParams p) {
         s[mb] = M::mma(__builtin_bit_cast(frag, kfr[g]), qf[ks], ks == 0 ? s_init : s[mb]);
       }
       if constexpr (DO_DMA) {
-        if (g % 2 == 1 && g / 2 < RPW) load_k(t + 1, (t + 1) & 1, g / 2);
-        if (g % 2 == 1 && g / 2 >= RPW && g / 2 < 2 * RPW) load_v(t, t & 1, g / 2 - RPW);
+        if (g % 2 == 1 && g / 2 < RPW) load_k(rk, (t + 1) & 1, g / 2);
+        if (g % 2 == 1 && g / 2 >= RPW && g / 2 < 2 * RPW) load_v(rv, t & 1, g / 2 - RPW);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -1530,7 +1540,7 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp3(FlashParams p) {
     for (int i = tid; i < TILEB / 16; i += P3_THREADS) *(u32x4*)(smem + 3 * TILEB + 16 * i) = u32x4{0u, 0u, 0u, 0u};
     wait_vmcnt<0>();  // Q is in registers before any DMA is issued
 #pragma unroll
-    for (int i = group; i < RPW; i += 2) load_k(0, 0, i);  // regions wq + 4 i, split by group
+    for (int i = group; i < RPW; i += 2) load_k(k_rsrc(0), 0, i);  // regions wq + 4 i, split by group
     wait_vmcnt<0>();
     lds_barrier();
   }
@@ -1915,10 +1925,12 @@ bool mfma_shape_ok(const FlashParams& p, int d_k, int dtype) {
   for (int64_t x : s)
     if (x < 0 || x % vec) return false;
   if (dtype != TL_DTYPE_F32) {
-    // The 16-bit kernel addresses a K tile (64 rows) and a head's V^T copy
-    // with 32-bit byte offsets.
+    // The 16-bit kernel addresses a K tile (128 rows) and a head's V^T copy
+    // with 32-bit byte offsets, and bounds a K tile's reads by its row count
+    // times the row stride (rows must not overlap).
     const int64_t sk_pad = (p.seq_k + 127) / 128 * 128;
-    if ((64 * p.k_ss + d_k) * 2 >= ((int64_t)1 << 32) || (int64_t)d_k * sk_pad * 2 >= ((int64_t)1 << 32))
+    if (p.k_ss < d_k || (128 * p.k_ss + d_k) * 2 >= ((int64_t)1 << 32) ||
+        (int64_t)d_k * sk_pad * 2 >= ((int64_t)1 << 32))
       return false;
   }
   return aligned16(p.q) && aligned16(p.k) && aligned16(p.v) && aligned16(p.o);
