@@ -128,3 +128,29 @@ def test_prefill_reads_cache_layout_and_seq_major_rows():
     got = on.from_storage(H.download(o_d), dt).transpose(0, 2, 1, 3)
     exp = oa.attention_bhsd(q_rows.transpose(0, 2, 1, 3), kc[:, :, :S], vc[:, :, :S], causal=True, dtype=dt)
     compare("cache-layout", got, exp, TOL[dt])
+
+
+@pytest.mark.parametrize("cus,seq_q,seq_k,n_head,n_kv,causal", [
+    (16, 1536, 1536, 8, 8, True),    # 2 workgroups per XCD list, 3 rounds: balanced-triple order
+    (16, 1024, 1024, 8, 8, True),    # 2 rounds: alternating order
+    (16, 1280, 1280, 8, 8, False),   # 5 tiles on 2 workgroups: partial last round
+    (24, 1536, 256, 16, 8, True),    # bottom-right causal: tiles with no visible key between others
+    (8, 768, 768, 6, 2, True),       # 2 (batch, kv) units: one list, 3 workgroups
+])
+def test_prefill_persistent_schedules(monkeypatch, cus, seq_q, seq_k, n_head, n_kv, causal):
+    """The persistent kernel walks several query tiles per workgroup (forced by capping the CU
+    count), switching tiles with prefetched Q / K and, after a tile with no visible key, cold."""
+    monkeypatch.setenv("TRITON_LLM_HIP_MAX_CUS", str(cus))
+    dtype, d_k = "bfloat16", 128
+    cfg = oi.Config("sched", "prefill", dtype, 1, n_head, n_kv, d_k, 77, 1 / np.sqrt(d_k), seq=seq_q)
+    print(f"[case] persistent cus={cus} sq={seq_q} sk={seq_k} Hq={n_head} Hkv={n_kv} causal={causal}", flush=True)
+    rng = np.random.default_rng(cus + seq_q + seq_k)
+    q = on.to_storage(rng.standard_normal((1, n_head, seq_q, d_k), dtype=np.float32), dtype)
+    k = on.to_storage(rng.standard_normal((1, n_kv, seq_k, d_k), dtype=np.float32), dtype)
+    v = on.to_storage(rng.standard_normal((1, n_kv, seq_k, d_k), dtype=np.float32), dtype)
+    o_d = flash_attention(H.upload(q, dtype), H.upload(k, dtype), H.upload(v, dtype), causal=causal,
+                          sm_scale=cfg.scale)
+    got = on.from_storage(H.download(o_d), dtype)
+    exp = oa.attention_bhsd(q, k, v, causal=causal, sm_scale=cfg.scale, dtype=dtype)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(exp))
+    compare(f"persistent cus={cus} sq={seq_q} sk={seq_k}", np.nan_to_num(got), np.nan_to_num(exp), TOL[dtype])

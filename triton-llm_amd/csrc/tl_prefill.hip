@@ -33,6 +33,7 @@
 #include "tl_common.h"
 
 #include <math.h>
+#include <stdlib.h>
 
 #include <type_traits>
 
@@ -54,6 +55,12 @@ struct FlashParams {
   int64_t v_sb, v_sh, v_ss;
   int64_t o_sb, o_sh, o_ss;
   float scale_log2;
+  // Static tile schedule of the persistent 16-bit kernel (see flash_fwd_pp4).
+  int n_queues;    // 8 (one tile list per XCD) or 1
+  int q_units;     // (batch, kv head) units per list
+  int q_tiles;     // tiles per list: q_units * n_qt * group
+  int q_machines;  // workgroups per list
+  int q_triple;    // first three rounds use the balanced-triple order
 };
 
 template <typename T>
@@ -1591,6 +1598,443 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp3(FlashParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// 16-bit kernel, persistent: flash_fwd_pp3's phases, one workgroup per CU
+// walking a static list of query tiles.
+//
+// Tiles (b, hq, qt) form n_queues lists -- one per XCD when the (batch, kv
+// head) units divide by 8, so that the K/V tiles a list reads stay in one
+// XCD's L2 (the dispatcher hands workgroups to XCDs round-robin, so
+// workgroup L serves list L % n_queues) -- each ordered by qt descending,
+// i.e. by causal cost.  Workgroup j of a list takes ranks j, then by rounds
+// of q_machines in alternating direction (a round pair then sums to the same
+// cost for every workgroup when costs fall linearly with rank); with an odd
+// number of rounds the first three use a balanced-triple order whose rank
+// sums differ by at most one.
+//
+// Tile switches do not wait for memory: during a tile's last G phase group 0
+// loads the next tile's first K tile (into the K buffer the next tile starts
+// from) and group 1's next Q rows (into the V^T buffer no later phase reads);
+// group 1 loads group 0's next Q rows into a fifth LDS buffer early in the
+// tile.  At the switch each wave copies its next Q from LDS, while the
+// finished tile's output stores drain in the background.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void decode_tile(const FlashParams& p, int queue, int i, int& b, int& hq, int& qt) {
+  const int per_qt = p.q_units * p.group;  // tiles per qt step in a list
+  const int qt_rev = i / per_qt;
+  const int rem = i - qt_rev * per_qt;
+  const int u = queue * p.q_units + rem / p.group;  // (batch, kv head) unit
+  const int hkv = u % p.n_kv;
+  b = u / p.n_kv;
+  qt = p.n_qt - 1 - qt_rev;
+  hq = hkv * p.group + rem % p.group;
+}
+
+// Rank (position in its list) of workgroup j's r-th tile; >= q_tiles: none.
+__device__ __forceinline__ int sched_rank(const FlashParams& p, int j, int r) {
+  const int m = p.q_machines;
+  if (p.q_triple && r < 3) {
+    const int hm = m / 2;
+    if (r == 0) return j;
+    if (r == 1) return m + (j < hm ? m - 1 - 2 * j : 2 * m - 2 - 2 * j);
+    return 2 * m + (j < hm ? hm + j : j - hm);
+  }
+  const int rr = p.q_triple ? r - 3 : r;
+  return r * m + ((rr & 1) ? m - 1 - j : j);
+}
+
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp4(FlashParams p) {
+  using M = Mfma<T>;
+  using frag = typename M::frag;
+  using Bits = typename T::bits;
+  constexpr int BN = P3_BN;
+  constexpr int ROWB = D * 2;          // bytes per K / Q row in LDS
+  constexpr int VROWB = BN * 2;        // bytes per V^T row in LDS (256)
+  constexpr int TILEB = BN * ROWB;     // bytes per K, V^T or 128-row Q tile
+  constexpr int NSL = ROWB / 16;       // 16-byte slots per K row
+  constexpr int RPR = 1024 / ROWB;     // K rows per 1 KiB region
+  constexpr int NREG = TILEB / 1024;   // 1 KiB regions per tile
+  constexpr int RPW = NREG / 4;        // regions per loading wave per tile
+  constexpr int NDB = D / 32;          // 32-row blocks of O^T
+  constexpr int NKS = D / 16;          // k-steps of S^T
+  constexpr int NMB = BN / 32;         // 32-key blocks of S^T
+  constexpr int NG = NMB * NKS;        // MFMA jobs per product
+  static_assert(BN / 16 * NDB == NG, "S and PV job counts must match");
+  static_assert(2 * RPW <= NG / 2, "every tile load needs an issue slot");
+  static_assert(BN == 128 && P3_BM == 256, "a group's 128 Q rows fill one K-sized buffer");
+
+  // K0 K1 V0 V1 Qn (group 0's next Q rows)
+  __shared__ __attribute__((aligned(1024))) char smem[5 * TILEB];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: phase branches are scalar
+  const int group = wave >> 2;
+  const int wq = wave & 3;
+  const int lq = lane & 31;
+  const int h = lane >> 5;
+  const int off = p.seq_k - p.seq_q;  // bottom-right causal offset
+  const int queue = blockIdx.x % p.n_queues;
+  const int mach = blockIdx.x / p.n_queues;
+
+  // ---- per-lane constants ----------------------------------------------------
+  // K and Q: region R holds rows R * RPR + l / NSL, slot l % NSL = chunk
+  // (l % NSL) ^ swz(row).  V^T: region R holds rows 4 R + l / 16 (256-byte
+  // rows), slot l % 16 = chunk (l % 16) ^ swz128(row).  Wave wq of the loading
+  // group fills regions wq + 4 i; the swizzle term does not depend on i, so
+  // one lane offset per tensor serves every region (region steps are added).
+  const int k_row0 = wq * RPR + lane / NSL;
+  const int k_chunk = (lane % NSL) ^ lds_swz<D>(k_row0);
+  const uint32_t k_voff = (uint32_t)(((int64_t)k_row0 * p.k_ss + k_chunk * 8) * 2);
+  const uint32_t q_voff = (uint32_t)(((int64_t)k_row0 * p.q_ss + k_chunk * 8) * 2);
+  const int v_row0 = 4 * wq + lane / 16;
+  const uint32_t v_voff =
+      (uint32_t)(((int64_t)v_row0 * p.sk_pad + ((lane % 16) ^ lds_swz<128>(v_row0)) * 8) * 2);
+  const uint32_t wave_lds = __builtin_amdgcn_readfirstlane((uint32_t)wq * 1024u);
+  const uint32_t lds_k0 = (uint32_t)(size_t)(__attribute__((address_space(3))) char*)smem;
+  const uint32_t lds_v0 = lds_k0 + 2 * TILEB;
+  const uint32_t lds_qn = lds_k0 + 4 * TILEB;
+  const uint32_t k_ss2 = (uint32_t)p.k_ss * 2u;
+  const uint32_t q_ss2 = (uint32_t)p.q_ss * 2u;
+  const uint32_t k_step = 4u * RPR * k_ss2;                // bytes of 4 regions of K rows
+  const uint32_t q_step = 4u * RPR * q_ss2;                // bytes of 4 regions of Q rows
+  const uint32_t v_step = 16u * (uint32_t)p.sk_pad * 2u;  // bytes of 16 V^T rows
+  const int k_lane = lq * ROWB + ((h ^ lds_swz<D>(lq)) << 4);
+  const int v_lane = lq * VROWB + ((h ^ lds_swz<128>(lq)) << 4);
+
+  // ---- tile state --------------------------------------------------------------
+  struct Tile {
+    int b, hq, qt, n_kt, k_rows;
+    const char* kg;
+  };
+  auto make_tile = [&](int rank) __attribute__((always_inline)) {
+    Tile tl;
+    decode_tile(p, queue, rank, tl.b, tl.hq, tl.qt);
+    const int q_last = min(p.seq_q, tl.qt * P3_BM + P3_BM) - 1;
+    int k_end = p.seq_k;
+    if (CAUSAL) k_end = max(0, min(p.seq_k, q_last + off + 1));
+    tl.n_kt = (k_end + BN - 1) / BN;             // K tiles the workgroup loads
+    tl.k_rows = min(p.seq_k, tl.n_kt * BN);      // keys the workgroup reads
+    tl.kg = (const char*)((const Bits*)p.k + tl.b * p.k_sb + (tl.hq / p.group) * p.k_sh);
+    return tl;
+  };
+
+  auto dma = [&](const i32x4& rsrc, uint32_t voff, uint32_t la) __attribute__((always_inline)) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(la), "v"(voff), "s"(rsrc)
+                 : "memory");
+  };
+  auto rsrc_of = [&](const char* base, uint32_t bytes) __attribute__((always_inline)) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    // every word wave-uniform, so the resource stays in SGPRs
+    return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+                 __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu)),
+                 __builtin_amdgcn_readfirstlane((int)bytes), kBufRsrcWord3};
+  };
+  // K tile tk of a tile: rows past its k_rows read as zeros, no traffic.
+  auto k_rsrc = [&](const Tile& tl, int tk) __attribute__((always_inline)) {
+    const int rows = min(max(tl.k_rows - tk * BN, 0), BN);
+    return rsrc_of(tl.kg + (int64_t)tk * BN * k_ss2, (uint32_t)rows * k_ss2);
+  };
+  // V^T tile tv of a tile (nothing past its last K tile).
+  auto v_rsrc = [&](const Tile& tl, int tv) __attribute__((always_inline)) {
+    const char* vg = (const char*)((const Bits*)p.vt + ((int64_t)tl.b * p.n_kv + tl.hq / p.group) * D * p.sk_pad);
+    return rsrc_of(vg + (int64_t)tv * BN * 2, tv < tl.n_kt ? (uint32_t)D * (uint32_t)p.sk_pad * 2u : 0u);
+  };
+  // Q rows [128 g, 128 g + 128) of a tile (rows past seq_q read as zeros).
+  auto q_rsrc = [&](const Tile& tl, int g) __attribute__((always_inline)) {
+    const int r0 = tl.qt * P3_BM + 128 * g;
+    const int rows = min(max(p.seq_q - r0, 0), 128);
+    const char* qg = (const char*)((const Bits*)p.q + tl.b * p.q_sb + tl.hq * p.q_sh + (int64_t)r0 * p.q_ss);
+    return rsrc_of(qg, (uint32_t)rows * q_ss2);
+  };
+
+  // ---- registers -------------------------------------------------------------------
+  frag qf[NKS];  // Q pre-scaled by sm_scale * log2 e
+  f32x16 o_acc[NDB];
+  float m_run, l4[4];
+  bool fresh;
+  f32x16 s_init;
+  f32x16 s[NMB];      // S_t (relative scores)
+  u32x4 pw[BN / 16];  // P_t packed 16-bit
+
+  auto scale_q = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const u32x4 raw = __builtin_bit_cast(u32x4, qf[ks]);
+      uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float lo, hi;
+        unpack2<T>(w[i], lo, hi);
+        w[i] = (uint32_t)from_f32<T>(lo * p.scale_log2) | ((uint32_t)from_f32<T>(hi * p.scale_log2) << 16);
+      }
+      qf[ks] = __builtin_bit_cast(frag, u32x4{w[0], w[1], w[2], w[3]});
+    }
+  };
+  // Cold tile start: K_0 into K buffer kb by all eight waves and this wave's
+  // Q rows from global memory; waits for both.
+  auto cold_start = [&](const Tile& tl, int kb) __attribute__((always_inline)) {
+    const i32x4 rk = k_rsrc(tl, 0);
+#pragma unroll
+    for (int i = group; i < RPW; i += 2) dma(rk, k_voff + (uint32_t)i * k_step, lds_k0 + kb * TILEB + i * 4096 + wave_lds);
+    const int qi = tl.qt * P3_BM + 128 * group + 32 * wq + lq;
+    const Bits* qrow = (const Bits*)p.q + tl.b * p.q_sb + tl.hq * p.q_sh + (int64_t)min(qi, p.seq_q - 1) * p.q_ss;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      u32x4 raw = *(const u32x4*)(qrow + 16 * ks + 8 * h);
+      if (qi >= p.seq_q) raw = u32x4{0u, 0u, 0u, 0u};
+      qf[ks] = __builtin_bit_cast(frag, raw);
+    }
+    wait_vmcnt<0>();
+    scale_q();
+  };
+
+  constexpr int kPrefetch = 2;
+  static_assert(NMB == 4, "S jobs are ordered for four key blocks");
+  constexpr auto s_mb = [](int g) { return 2 * (g / (2 * NKS)) + (g & 1); };
+  constexpr auto s_ks = [](int g) { return (g % (2 * NKS)) >> 1; };
+
+  int r = 0;
+  int rank = sched_rank(p, mach, 0);
+  if (rank >= p.q_tiles) return;
+  Tile cur = make_tile(rank);
+  int tb = 0;  // K / V^T buffer parity of the tile's K_0
+  cold_start(cur, tb);
+  lds_barrier();
+
+  for (;;) {
+    const int nrank = sched_rank(p, mach, r + 1);
+    const bool has_next = nrank < p.q_tiles;
+    const Tile nxt = make_tile(has_next ? nrank : rank);
+    const int n_kt = cur.n_kt;
+    const int q0 = cur.qt * P3_BM + 128 * group + 32 * wq;  // first row of this wave
+    const int qi = q0 + lq;                                 // this lane's query row
+    int wave_k_end = p.seq_k;
+    if (CAUSAL) wave_k_end = max(0, min(p.seq_k, min(q0 + 31, p.seq_q - 1) + off + 1));
+    if (q0 >= p.seq_q) wave_k_end = 0;  // no rows: no compute
+
+#pragma unroll
+    for (int i = 0; i < NDB; ++i)
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) o_acc[i][rr] = 0.f;
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) s_init[rr] = 0.f;
+    m_run = 0.f;
+    fresh = true;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) l4[k] = 0.f;
+
+    // G(t): PV job g of tile t-1 (none for t = 0) and S job g of tile t, as
+    // flash_fwd_pp3.  Group 0 loads, one every other job, K_{t+1} then V^T_t
+    // -- for t = n_kt the next tile's K_0 and group 1's next Q rows instead.
+    auto g_phase = [&](int t, auto dma_tag, auto pv_tag) __attribute__((always_inline)) {
+      constexpr bool DO_DMA = decltype(dma_tag)::value;
+      constexpr bool DO_PV = decltype(pv_tag)::value;
+      i32x4 rk = {0, 0, 0, 0}, rv = {0, 0, 0, 0};
+      uint32_t kvo = k_voff, vvo = v_voff, vstep = v_step;
+      if constexpr (DO_DMA) {
+        if (t < n_kt) {
+          rk = k_rsrc(cur, t + 1);
+          rv = v_rsrc(cur, t);
+        } else {
+          rk = has_next ? k_rsrc(nxt, 0) : rsrc_of(cur.kg, 0u);
+          rv = has_next ? q_rsrc(nxt, 1) : rsrc_of(cur.kg, 0u);
+          vvo = q_voff;
+          vstep = q_step;
+        }
+        asm volatile("" : "+v"(kvo), "+v"(vvo));
+      }
+      const int kbuf = (tb + t + 1) & 1;  // K_{t+1} (or the next K_0)
+      const int vbuf = (tb + t) & 1;      // V^T_t (or group 1's next Q)
+      int kb_lane = k_lane + ((tb + t) & 1) * TILEB;              // K_t
+      int vb_lane = v_lane + (2 + ((tb + t + 1) & 1)) * TILEB;   // V^T_{t-1}
+      // Opaque per phase, so the per-job addresses are formed in the job that
+      // uses them instead of being hoisted and kept live across the loop.
+      asm volatile("" : "+v"(kb_lane), "+v"(vb_lane));
+      u32x4 kfr[NG], vfr[NG];
+      auto fetch = [&](int g) __attribute__((always_inline)) {
+        if constexpr (DO_PV) {
+          const int tt = g / NDB, db = g % NDB;
+          vfr[g] = *(const u32x4*)(smem + (vb_lane ^ (tt << 5)) + 32 * db * VROWB);
+        }
+        const int ks = s_ks(g), mb = s_mb(g);
+        kfr[g] = *(const u32x4*)(smem + (kb_lane ^ (ks << 5)) + 32 * mb * ROWB);
+      };
+      __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int g = 0; g < kPrefetch; ++g) fetch(g);
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        if (g + kPrefetch < NG) fetch(g + kPrefetch);
+        if constexpr (DO_PV) {
+          const int tt = g / NDB, db = g % NDB;
+          o_acc[db] = M::mma(__builtin_bit_cast(frag, vfr[g]), __builtin_bit_cast(frag, pw[tt]), o_acc[db]);
+        }
+        {
+          const int ks = s_ks(g), mb = s_mb(g);
+          s[mb] = M::mma(__builtin_bit_cast(frag, kfr[g]), qf[ks], ks == 0 ? s_init : s[mb]);
+        }
+        if constexpr (DO_DMA) {
+          if (g % 2 == 1 && g / 2 < RPW) {
+            const int i = g / 2;
+            dma(rk, kvo + (uint32_t)i * k_step, lds_k0 + kbuf * TILEB + i * 4096 + wave_lds);
+          }
+          if (g % 2 == 1 && g / 2 >= RPW && g / 2 < 2 * RPW) {
+            const int i = g / 2 - RPW;
+            dma(rv, vvo + (uint32_t)i * vstep, lds_v0 + vbuf * TILEB + i * 4096 + wave_lds);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      __builtin_amdgcn_s_setprio(0);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // A(t): masked softmax of S_t -> P_t, as flash_fwd_pp3.
+    auto a_phase = [&](int t) __attribute__((always_inline)) {
+      const int kb = t * BN;
+      if (t >= n_kt || kb >= wave_k_end) {
+#pragma unroll
+        for (int tt = 0; tt < BN / 16; ++tt) pw[tt] = u32x4{0u, 0u, 0u, 0u};
+        __builtin_amdgcn_sched_barrier(0);
+        return;
+      }
+      const bool need_mask = (kb + BN > p.seq_k) || (CAUSAL && kb + BN - 1 > q0 + off);
+      if (need_mask) {
+        int lim = p.seq_k - 1 - kb - 4 * h;
+        if (CAUSAL) lim = min(lim, qi + off - kb - 4 * h);
+#pragma unroll
+        for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+          for (int rr = 0; rr < 16; ++rr) {
+            const int kl = 32 * mb + 8 * (rr >> 2) + (rr & 3);
+            s[mb][rr] = kl <= lim ? s[mb][rr] : -INFINITY;
+          }
+      }
+      float mq[NMB];
+#pragma unroll
+      for (int mb = 0; mb < NMB; ++mb) {
+        const f32x16& v = s[mb];
+        float a = fmaxf(fmaxf(fmaxf(v[0], v[1]), v[2]), fmaxf(fmaxf(v[3], v[4]), v[5]));
+        float c2 = fmaxf(fmaxf(fmaxf(v[8], v[9]), v[10]), fmaxf(fmaxf(v[11], v[12]), v[13]));
+        a = fmaxf(a, fmaxf(v[6], v[7]));
+        c2 = fmaxf(c2, fmaxf(v[14], v[15]));
+        mq[mb] = fmaxf(a, c2);
+      }
+      float mxl = mq[0];
+#pragma unroll
+      for (int mb = 1; mb < NMB; ++mb) mxl = fmaxf(mxl, mq[mb]);
+      const float mx = max_xor32(mxl);
+      const bool grow = fresh ? (mx != -INFINITY) : (mx > kRescaleLog2);
+      if (__any(grow)) {
+        const float delta = fresh ? (mx == -INFINITY ? 0.f : mx) : fmaxf(mx, 0.f);
+        const float alpha = fresh ? 1.f : fast_exp2(-delta);  // fresh: nothing to scale, 2^-mx may overflow
+        m_run += delta;
+        fresh = fresh && (mx == -INFINITY);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) l4[k] *= alpha;
+#pragma unroll
+        for (int i = 0; i < NDB; ++i)
+#pragma unroll
+          for (int rr = 0; rr < 16; ++rr) o_acc[i][rr] *= alpha;
+#pragma unroll
+        for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+          for (int rr = 0; rr < 16; ++rr) s[mb][rr] -= delta;
+#pragma unroll
+        for (int rr = 0; rr < 16; ++rr) s_init[rr] = -m_run;
+      }
+      // P chunk tt (keys 16 tt..) = s[tt / 2][8 (tt % 2) + 0..7]; fp32 row sums
+      // (v_dot2 does not co-execute with the partner's MFMAs).
+#pragma unroll
+      for (int tt = 0; tt < BN / 16; ++tt)
+#pragma unroll
+        for (int j2 = 0; j2 < 4; ++j2) {
+          float pr2[2] = {fast_exp2(s[tt >> 1][8 * (tt & 1) + 2 * j2]),
+                          fast_exp2(s[tt >> 1][8 * (tt & 1) + 2 * j2 + 1])};
+          pw[tt][j2] = pack2<T>(pr2);
+          l4[j2] += pr2[0] + pr2[1];
+        }
+      __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // ---- phases 2t (group 0: G(t), group 1: A(t-1)) and 2t+1 (group 0: A(t),
+    // group 1: G(t)) for t = 0 .. n_kt, as flash_fwd_pp3.  Phase 2t+2 reads
+    // K_{t+1} and V^T_t, which group 0 issued in phase 2t and waited for at
+    // the end of phase 2t+1. ----------------------------------------------------------
+    if (n_kt > 0) {
+      if (group == 0) {
+        g_phase(0, std::true_type{}, std::false_type{});
+        lds_barrier();
+        a_phase(0);
+        wait_vmcnt<0>();
+        lds_barrier();
+        for (int t = 1; t <= n_kt; ++t) {
+          g_phase(t, std::true_type{}, std::true_type{});
+          lds_barrier();
+          a_phase(t);
+          wait_vmcnt<0>();
+          lds_barrier();
+        }
+      } else {
+        lds_barrier();  // phase 0: nothing to do (A of tile -1)
+        g_phase(0, std::false_type{}, std::false_type{});
+        lds_barrier();
+        // Group 0's next Q rows into the fifth buffer (read only at the switch).
+        if (has_next) {
+          const i32x4 rq = q_rsrc(nxt, 0);
+#pragma unroll
+          for (int i = 0; i < RPW; ++i) dma(rq, q_voff + (uint32_t)i * q_step, lds_qn + i * 4096 + wave_lds);
+        }
+        for (int t = 1; t <= n_kt; ++t) {
+          a_phase(t - 1);
+          lds_barrier();
+          g_phase(t, std::false_type{}, std::true_type{});
+          if (t == n_kt) wait_vmcnt<0>();
+          lds_barrier();
+        }
+      }
+    }
+
+    // ---- tile switch ---------------------------------------------------------------
+    // Epilogue: O[qi][d] = O^T[d][qi] / l (stores are not waited for).
+    const float inv = 1.f / sum_xor32((l4[0] + l4[1]) + (l4[2] + l4[3]));
+    if (qi < p.seq_q) {
+      Bits* orow = (Bits*)p.o + cur.b * p.o_sb + cur.hq * p.o_sh + (int64_t)qi * p.o_ss;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const int d0 = 32 * db + 8 * rq + 4 * h;
+          uint32_t w0 = (uint32_t)from_f32<T>(o_acc[db][4 * rq + 0] * inv) |
+                        ((uint32_t)from_f32<T>(o_acc[db][4 * rq + 1] * inv) << 16);
+          uint32_t w1 = (uint32_t)from_f32<T>(o_acc[db][4 * rq + 2] * inv) |
+                        ((uint32_t)from_f32<T>(o_acc[db][4 * rq + 3] * inv) << 16);
+          *(u32x2*)(orow + d0) = u32x2{w0, w1};
+        }
+    }
+    if (!has_next) break;
+    const int ntb = (tb + n_kt + 1) & 1;  // where the next K_0 went
+    if (n_kt > 0) {
+      // next Q rows: group 0's in the fifth buffer, group 1's in V^T buffer (tb + n_kt) & 1
+      const int qbase = group == 0 ? 4 * TILEB : (2 + ((tb + n_kt) & 1)) * TILEB;
+      int ql = qbase + 32 * wq * ROWB + k_lane;
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) qf[ks] = __builtin_bit_cast(frag, *(const u32x4*)(smem + (ql ^ (ks << 5))));
+      scale_q();
+    } else {
+      cold_start(nxt, ntb);  // no phase ran to prefetch it
+    }
+    lds_barrier();  // every wave holds its Q before the buffers are reused
+    cur = nxt;
+    rank = nrank;
+    tb = ntb;
+    ++r;
+  }
+  wait_vmcnt<0>();  // no LDS-DMA may land after the workgroup has left its LDS
+}
+
+// ---------------------------------------------------------------------------
 // fp32 kernel (v_mfma_f32_32x32x2_f32).  K-step mapping for S^T: lane half h
 // covers d = h*D/2 + 4c + i for step (c, i), so both K (LDS) and Q (global)
 // are read as 16-byte chunks.
@@ -1882,20 +2326,56 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(FlashParams p, int D, 
 
 inline bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
+// Bytes of the key-major V^T copy: keys padded to a multiple of 128.
+size_t vt_bytes(int batch, int n_kv, int seq_k, int d_k) {
+  const size_t sk_pad = (size_t)((seq_k + 127) / 128) * 128;
+  return (size_t)batch * n_kv * d_k * sk_pad * 2;
+}
+
+// Compute units of the current device (cached per device), capped by
+// TRITON_LLM_HIP_MAX_CUS when set (tests use it to force multi-round tile
+// schedules on small shapes).
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  int n = 256;
+  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
+    if (cus[dev] == 0) {
+      int c = 0;
+      if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+      cus[dev] = c;
+    }
+    n = cus[dev];
+  }
+  if (const char* cap = getenv("TRITON_LLM_HIP_MAX_CUS")) {
+    const int c = atoi(cap);
+    if (c > 0 && c < n) n = c;
+  }
+  return n;
+}
+
 template <typename T, int D>
 int launch_flash_16(FlashParams& p, void* ws, bool causal, hipStream_t st) {
   p.vt = ws;
+  p.n_qt = (p.seq_q + P3_BM - 1) / P3_BM;
+  // Tile lists: one per XCD when the (batch, kv head) units split evenly.
+  const int units = p.batch * p.n_kv;
+  p.n_queues = units % 8 == 0 ? 8 : 1;
+  p.q_units = units / p.n_queues;
+  p.q_tiles = p.q_units * p.n_qt * p.group;
+  p.q_machines = min((device_cus() + p.n_queues - 1) / p.n_queues, p.q_tiles);
+  const int rounds = p.q_tiles / p.q_machines;
+  p.q_triple = (p.q_tiles % p.q_machines == 0 && rounds % 2 == 1 && rounds >= 3 && p.q_machines % 2 == 0) ? 1 : 0;
   dim3 tg(p.sk_pad / 64, p.n_kv, p.batch);
   hipLaunchKernelGGL(vt_pack_kernel<D>, tg, dim3(256), 0, st, (const uint16_t*)p.v, (uint16_t*)ws,
                      p.seq_k, p.sk_pad, p.n_kv, p.v_sb, p.v_sh, p.v_ss);
   int e = tl_launch_status();
   if (e) return e;
-  p.n_qt = (p.seq_q + P3_BM - 1) / P3_BM;
-  dim3 grid((unsigned)(p.n_qt * p.n_head * p.batch));
+  dim3 grid((unsigned)(p.q_machines * p.n_queues));
   if (causal)
-    hipLaunchKernelGGL((flash_fwd_pp3<T, D, true>), grid, dim3(P3_THREADS), 0, st, p);
+    hipLaunchKernelGGL((flash_fwd_pp4<T, D, true>), grid, dim3(P3_THREADS), 0, st, p);
   else
-    hipLaunchKernelGGL((flash_fwd_pp3<T, D, false>), grid, dim3(P3_THREADS), 0, st, p);
+    hipLaunchKernelGGL((flash_fwd_pp4<T, D, false>), grid, dim3(P3_THREADS), 0, st, p);
   return tl_launch_status();
 }
 
@@ -1925,12 +2405,12 @@ bool mfma_shape_ok(const FlashParams& p, int d_k, int dtype) {
   for (int64_t x : s)
     if (x < 0 || x % vec) return false;
   if (dtype != TL_DTYPE_F32) {
-    // The 16-bit kernel addresses a K tile (128 rows) and a head's V^T copy
-    // with 32-bit byte offsets, and bounds a K tile's reads by its row count
-    // times the row stride (rows must not overlap).
+    // The 16-bit kernel addresses a K or Q tile (128 rows) and a head's V^T
+    // copy with 32-bit byte offsets, and bounds a K or Q tile's reads by its
+    // row count times the row stride (rows must not overlap).
     const int64_t sk_pad = (p.seq_k + 127) / 128 * 128;
-    if (p.k_ss < d_k || (128 * p.k_ss + d_k) * 2 >= ((int64_t)1 << 32) ||
-        (int64_t)d_k * sk_pad * 2 >= ((int64_t)1 << 32))
+    if (p.k_ss < d_k || (128 * p.k_ss + d_k) * 2 >= ((int64_t)1 << 32) || p.q_ss < d_k ||
+        (128 * p.q_ss + d_k) * 2 >= ((int64_t)1 << 32) || (int64_t)d_k * sk_pad * 2 >= ((int64_t)1 << 32))
       return false;
   }
   return aligned16(p.q) && aligned16(p.k) && aligned16(p.v) && aligned16(p.o);
@@ -1947,8 +2427,7 @@ size_t tl_attention_fwd_workspace_bytes(int batch, int n_kv_head, int seq_k, int
   if (dtype == TL_DTYPE_F32 || batch <= 0 || n_kv_head <= 0 || seq_k <= 0 ||
       (d_k != 64 && d_k != 128))
     return 0;
-  const size_t sk_pad = (size_t)((seq_k + 127) / 128) * 128;
-  return (size_t)batch * n_kv_head * d_k * sk_pad * 2;
+  return vt_bytes(batch, n_kv_head, seq_k, d_k);
 }
 
 int tl_attention_fwd(const void* q, const void* k, const void* v, void* o, void* workspace,
