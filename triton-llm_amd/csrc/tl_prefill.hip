@@ -1618,6 +1618,15 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp3(FlashParams p) {
 // tile.  At the switch each wave copies its next Q from LDS, while the
 // finished tile's output stores drain in the background.
 // ---------------------------------------------------------------------------
+// The lane index, read afresh at each use (an opaque read that cannot be
+// hoisted), so that lane-derived offsets are recomputed where they are used
+// instead of occupying registers across the tile loop.
+__device__ __forceinline__ int fresh_lane() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 __device__ __forceinline__ void decode_tile(const FlashParams& p, int queue, int i, int& b, int& hq, int& qt) {
   const int per_qt = p.q_units * p.group;  // tiles per qt step in a list
   const int qt_rev = i / per_qt;
@@ -1666,30 +1675,38 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp4(FlashParams p) {
   // K0 K1 V0 V1 Qn (group 0's next Q rows)
   __shared__ __attribute__((aligned(1024))) char smem[5 * TILEB];
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: phase branches are scalar
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);  // wave-uniform: phase branches are scalar
   const int group = wave >> 2;
   const int wq = wave & 3;
-  const int lq = lane & 31;
-  const int h = lane >> 5;
   const int off = p.seq_k - p.seq_q;  // bottom-right causal offset
   const int queue = blockIdx.x % p.n_queues;
   const int mach = blockIdx.x / p.n_queues;
 
-  // ---- per-lane constants ----------------------------------------------------
+  // ---- lane offsets (recomputed from fresh_lane() where used) ----------------
   // K and Q: region R holds rows R * RPR + l / NSL, slot l % NSL = chunk
   // (l % NSL) ^ swz(row).  V^T: region R holds rows 4 R + l / 16 (256-byte
   // rows), slot l % 16 = chunk (l % 16) ^ swz128(row).  Wave wq of the loading
   // group fills regions wq + 4 i; the swizzle term does not depend on i, so
   // one lane offset per tensor serves every region (region steps are added).
-  const int k_row0 = wq * RPR + lane / NSL;
-  const int k_chunk = (lane % NSL) ^ lds_swz<D>(k_row0);
-  const uint32_t k_voff = (uint32_t)(((int64_t)k_row0 * p.k_ss + k_chunk * 8) * 2);
-  const uint32_t q_voff = (uint32_t)(((int64_t)k_row0 * p.q_ss + k_chunk * 8) * 2);
-  const int v_row0 = 4 * wq + lane / 16;
-  const uint32_t v_voff =
-      (uint32_t)(((int64_t)v_row0 * p.sk_pad + ((lane % 16) ^ lds_swz<128>(v_row0)) * 8) * 2);
+  // 32-bit products: the shape check bounds 128 rows of K / Q and a head's
+  // V^T copy below 2^32 bytes.
+  auto kq_off = [&](int ln, int64_t ss) __attribute__((always_inline)) {
+    const int row = wq * RPR + ln / NSL;
+    return ((uint32_t)row * (uint32_t)ss + (uint32_t)(((ln % NSL) ^ lds_swz<D>(row)) * 8)) * 2u;
+  };
+  auto v_off = [&](int ln) __attribute__((always_inline)) {
+    const int row = 4 * wq + ln / 16;
+    return ((uint32_t)row * (uint32_t)p.sk_pad + (uint32_t)(((ln % 16) ^ lds_swz<128>(row)) * 8)) * 2u;
+  };
+  // Operand reads: lane (lq, h) reads row lq, chunk (2 ks + h) ^ swz(lq).
+  auto k_lane_of = [&](int ln) __attribute__((always_inline)) {
+    const int lq = ln & 31, h = ln >> 5;
+    return lq * ROWB + ((h ^ lds_swz<D>(lq)) << 4);
+  };
+  auto v_lane_of = [&](int ln) __attribute__((always_inline)) {
+    const int lq = ln & 31, h = ln >> 5;
+    return lq * VROWB + ((h ^ lds_swz<128>(lq)) << 4);
+  };
   const uint32_t wave_lds = __builtin_amdgcn_readfirstlane((uint32_t)wq * 1024u);
   const uint32_t lds_k0 = (uint32_t)(size_t)(__attribute__((address_space(3))) char*)smem;
   const uint32_t lds_v0 = lds_k0 + 2 * TILEB;
@@ -1699,8 +1716,6 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp4(FlashParams p) {
   const uint32_t k_step = 4u * RPR * k_ss2;                // bytes of 4 regions of K rows
   const uint32_t q_step = 4u * RPR * q_ss2;                // bytes of 4 regions of Q rows
   const uint32_t v_step = 16u * (uint32_t)p.sk_pad * 2u;  // bytes of 16 V^T rows
-  const int k_lane = lq * ROWB + ((h ^ lds_swz<D>(lq)) << 4);
-  const int v_lane = lq * VROWB + ((h ^ lds_swz<128>(lq)) << 4);
 
   // ---- tile state --------------------------------------------------------------
   struct Tile {
@@ -1766,7 +1781,8 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp4(FlashParams p) {
       for (int i = 0; i < 4; ++i) {
         float lo, hi;
         unpack2<T>(w[i], lo, hi);
-        w[i] = (uint32_t)from_f32<T>(lo * p.scale_log2) | ((uint32_t)from_f32<T>(hi * p.scale_log2) << 16);
+        const float x[2] = {lo * p.scale_log2, hi * p.scale_log2};
+        w[i] = pack2<T>(x);  // hardware convert, round to nearest even
       }
       qf[ks] = __builtin_bit_cast(frag, u32x4{w[0], w[1], w[2], w[3]});
     }
@@ -1774,10 +1790,13 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp4(FlashParams p) {
   // Cold tile start: K_0 into K buffer kb by all eight waves and this wave's
   // Q rows from global memory; waits for both.
   auto cold_start = [&](const Tile& tl, int kb) __attribute__((always_inline)) {
+    const int ln = fresh_lane();
+    const int h = ln >> 5;
     const i32x4 rk = k_rsrc(tl, 0);
+    const uint32_t kvo = kq_off(ln, p.k_ss);
 #pragma unroll
-    for (int i = group; i < RPW; i += 2) dma(rk, k_voff + (uint32_t)i * k_step, lds_k0 + kb * TILEB + i * 4096 + wave_lds);
-    const int qi = tl.qt * P3_BM + 128 * group + 32 * wq + lq;
+    for (int i = group; i < RPW; i += 2) dma(rk, kvo + (uint32_t)i * k_step, lds_k0 + kb * TILEB + i * 4096 + wave_lds);
+    const int qi = tl.qt * P3_BM + 128 * group + 32 * wq + (ln & 31);
     const Bits* qrow = (const Bits*)p.q + tl.b * p.q_sb + tl.hq * p.q_sh + (int64_t)min(qi, p.seq_q - 1) * p.q_ss;
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
@@ -1805,10 +1824,8 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp4(FlashParams p) {
   for (;;) {
     const int nrank = sched_rank(p, mach, r + 1);
     const bool has_next = nrank < p.q_tiles;
-    const Tile nxt = make_tile(has_next ? nrank : rank);
     const int n_kt = cur.n_kt;
     const int q0 = cur.qt * P3_BM + 128 * group + 32 * wq;  // first row of this wave
-    const int qi = q0 + lq;                                 // this lane's query row
     int wave_k_end = p.seq_k;
     if (CAUSAL) wave_k_end = max(0, min(p.seq_k, min(q0 + 31, p.seq_q - 1) + off + 1));
     if (q0 >= p.seq_q) wave_k_end = 0;  // no rows: no compute
@@ -1830,27 +1847,27 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp4(FlashParams p) {
     auto g_phase = [&](int t, auto dma_tag, auto pv_tag) __attribute__((always_inline)) {
       constexpr bool DO_DMA = decltype(dma_tag)::value;
       constexpr bool DO_PV = decltype(pv_tag)::value;
+      const int ln = fresh_lane();
       i32x4 rk = {0, 0, 0, 0}, rv = {0, 0, 0, 0};
-      uint32_t kvo = k_voff, vvo = v_voff, vstep = v_step;
+      uint32_t kvo = 0, vvo = 0, vstep = v_step;
       if constexpr (DO_DMA) {
+        kvo = kq_off(ln, p.k_ss);
         if (t < n_kt) {
           rk = k_rsrc(cur, t + 1);
           rv = v_rsrc(cur, t);
+          vvo = v_off(ln);
         } else {
+          const Tile nxt = make_tile(has_next ? nrank : rank);
           rk = has_next ? k_rsrc(nxt, 0) : rsrc_of(cur.kg, 0u);
           rv = has_next ? q_rsrc(nxt, 1) : rsrc_of(cur.kg, 0u);
-          vvo = q_voff;
+          vvo = kq_off(ln, p.q_ss);
           vstep = q_step;
         }
-        asm volatile("" : "+v"(kvo), "+v"(vvo));
       }
       const int kbuf = (tb + t + 1) & 1;  // K_{t+1} (or the next K_0)
       const int vbuf = (tb + t) & 1;      // V^T_t (or group 1's next Q)
-      int kb_lane = k_lane + ((tb + t) & 1) * TILEB;              // K_t
-      int vb_lane = v_lane + (2 + ((tb + t + 1) & 1)) * TILEB;   // V^T_{t-1}
-      // Opaque per phase, so the per-job addresses are formed in the job that
-      // uses them instead of being hoisted and kept live across the loop.
-      asm volatile("" : "+v"(kb_lane), "+v"(vb_lane));
+      int kb_lane = k_lane_of(ln) + ((tb + t) & 1) * TILEB;              // K_t
+      int vb_lane = v_lane_of(ln) + (2 + ((tb + t + 1) & 1)) * TILEB;   // V^T_{t-1}
       u32x4 kfr[NG], vfr[NG];
       auto fetch = [&](int g) __attribute__((always_inline)) {
         if constexpr (DO_PV) {
@@ -1901,8 +1918,10 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp4(FlashParams p) {
       }
       const bool need_mask = (kb + BN > p.seq_k) || (CAUSAL && kb + BN - 1 > q0 + off);
       if (need_mask) {
+        const int ln = fresh_lane();
+        const int h = ln >> 5;
         int lim = p.seq_k - 1 - kb - 4 * h;
-        if (CAUSAL) lim = min(lim, qi + off - kb - 4 * h);
+        if (CAUSAL) lim = min(lim, q0 + (ln & 31) + off - kb - 4 * h);
 #pragma unroll
         for (int mb = 0; mb < NMB; ++mb)
 #pragma unroll
@@ -1982,9 +2001,10 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp4(FlashParams p) {
         lds_barrier();
         // Group 0's next Q rows into the fifth buffer (read only at the switch).
         if (has_next) {
-          const i32x4 rq = q_rsrc(nxt, 0);
+          const i32x4 rq = q_rsrc(make_tile(nrank), 0);
+          const uint32_t qvo = kq_off(fresh_lane(), p.q_ss);
 #pragma unroll
-          for (int i = 0; i < RPW; ++i) dma(rq, q_voff + (uint32_t)i * q_step, lds_qn + i * 4096 + wave_lds);
+          for (int i = 0; i < RPW; ++i) dma(rq, qvo + (uint32_t)i * q_step, lds_qn + i * 4096 + wave_lds);
         }
         for (int t = 1; t <= n_kt; ++t) {
           a_phase(t - 1);
@@ -1997,35 +2017,53 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp4(FlashParams p) {
     }
 
     // ---- tile switch ---------------------------------------------------------------
-    // Epilogue: O[qi][d] = O^T[d][qi] / l (stores are not waited for).
+    // 1. Every wave copies its next Q rows out of LDS (or, after a tile that
+    //    ran no phase, loads them cold).  2. Barrier: the two Q buffers are now
+    //    free until phase 2 of the next tile.  3. Each wave stages its output
+    //    rows, normalised and rounded, in its own part of its group's Q buffer
+    //    and stores them row-contiguously (16 lanes per 256-byte row), so each
+    //    store instruction writes whole cache lines.  The stores are not
+    //    waited for here.
     const float inv = 1.f / sum_xor32((l4[0] + l4[1]) + (l4[2] + l4[3]));
-    if (qi < p.seq_q) {
-      Bits* orow = (Bits*)p.o + cur.b * p.o_sb + cur.hq * p.o_sh + (int64_t)qi * p.o_ss;
+    const int ntb = (tb + n_kt + 1) & 1;  // where the next K_0 went
+    const Tile nxt = make_tile(has_next ? nrank : rank);
+    // group 0's next Q rows are in the fifth buffer, group 1's in V^T buffer (tb + n_kt) & 1
+    const int qbuf = group == 0 ? 4 * TILEB : (2 + ((tb + n_kt) & 1)) * TILEB;
+    if (has_next) {
+      if (n_kt > 0) {
+        const int ql = qbuf + 32 * wq * ROWB + k_lane_of(fresh_lane());
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) qf[ks] = __builtin_bit_cast(frag, *(const u32x4*)(smem + (ql ^ (ks << 5))));
+        scale_q();
+      } else {
+        cold_start(nxt, ntb);  // no phase ran to prefetch it
+      }
+    }
+    lds_barrier();
+    {
+      const int ln = fresh_lane();
+      const int lq = ln & 31, h = ln >> 5;
+      const int wbase = qbuf + 32 * wq * ROWB;  // this wave's 32 rows
+      // O^T lane (lq, h) holds row lq, d = 32 db + 8 rq + 4 h + 0..3: 16-byte
+      // chunk 4 db + rq, half h.
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int rq = 0; rq < 4; ++rq) {
-          const int d0 = 32 * db + 8 * rq + 4 * h;
-          uint32_t w0 = (uint32_t)from_f32<T>(o_acc[db][4 * rq + 0] * inv) |
-                        ((uint32_t)from_f32<T>(o_acc[db][4 * rq + 1] * inv) << 16);
-          uint32_t w1 = (uint32_t)from_f32<T>(o_acc[db][4 * rq + 2] * inv) |
-                        ((uint32_t)from_f32<T>(o_acc[db][4 * rq + 3] * inv) << 16);
-          *(u32x2*)(orow + d0) = u32x2{w0, w1};
+          const float x0[2] = {o_acc[db][4 * rq + 0] * inv, o_acc[db][4 * rq + 1] * inv};
+          const float x1[2] = {o_acc[db][4 * rq + 2] * inv, o_acc[db][4 * rq + 3] * inv};
+          const int c = 4 * db + rq;
+          *(u32x2*)(smem + wbase + lq * ROWB + ((c ^ lds_swz<D>(lq)) << 4) + 8 * h) = u32x2{pack2<T>(x0), pack2<T>(x1)};
         }
+      Bits* obase = (Bits*)p.o + cur.b * p.o_sb + cur.hq * p.o_sh;
+#pragma unroll
+      for (int i = 0; i < 32 / RPR; ++i) {
+        const int rr = i * RPR + ln / NSL, cc = ln % NSL;
+        const u32x4 val = *(const u32x4*)(smem + wbase + rr * ROWB + ((cc ^ lds_swz<D>(rr)) << 4));
+        if (q0 + rr < p.seq_q) *(u32x4*)(obase + (int64_t)(q0 + rr) * p.o_ss + 8 * cc) = val;
+      }
     }
     if (!has_next) break;
-    const int ntb = (tb + n_kt + 1) & 1;  // where the next K_0 went
-    if (n_kt > 0) {
-      // next Q rows: group 0's in the fifth buffer, group 1's in V^T buffer (tb + n_kt) & 1
-      const int qbase = group == 0 ? 4 * TILEB : (2 + ((tb + n_kt) & 1)) * TILEB;
-      int ql = qbase + 32 * wq * ROWB + k_lane;
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) qf[ks] = __builtin_bit_cast(frag, *(const u32x4*)(smem + (ql ^ (ks << 5))));
-      scale_q();
-    } else {
-      cold_start(nxt, ntb);  // no phase ran to prefetch it
-    }
-    lds_barrier();  // every wave holds its Q before the buffers are reused
     cur = nxt;
     rank = nrank;
     tb = ntb;
