@@ -1930,19 +1930,18 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp4(FlashParams p) {
             s[mb][rr] = kl <= lim ? s[mb][rr] : -INFINITY;
           }
       }
+      // Row max over the tile: IEEE maximum (NaN-propagating) maps to
+      // v_maximum3_f32 with no input canonicalisation, unlike fmaxf.
+      auto mx3 = [](float x, float y, float z) { return __builtin_elementwise_maximum(__builtin_elementwise_maximum(x, y), z); };
       float mq[NMB];
 #pragma unroll
       for (int mb = 0; mb < NMB; ++mb) {
         const f32x16& v = s[mb];
-        float a = fmaxf(fmaxf(fmaxf(v[0], v[1]), v[2]), fmaxf(fmaxf(v[3], v[4]), v[5]));
-        float c2 = fmaxf(fmaxf(fmaxf(v[8], v[9]), v[10]), fmaxf(fmaxf(v[11], v[12]), v[13]));
-        a = fmaxf(a, fmaxf(v[6], v[7]));
-        c2 = fmaxf(c2, fmaxf(v[14], v[15]));
-        mq[mb] = fmaxf(a, c2);
+        const float a0 = mx3(v[0], v[1], v[2]), a1 = mx3(v[3], v[4], v[5]), a2 = mx3(v[6], v[7], v[8]);
+        const float a3 = mx3(v[9], v[10], v[11]), a4 = mx3(v[12], v[13], v[14]);
+        mq[mb] = __builtin_elementwise_maximum(mx3(a0, a1, a2), mx3(a3, a4, v[15]));
       }
-      float mxl = mq[0];
-#pragma unroll
-      for (int mb = 1; mb < NMB; ++mb) mxl = fmaxf(mxl, mq[mb]);
+      const float mxl = __builtin_elementwise_maximum(mx3(mq[0], mq[1], mq[2]), mq[3]);
       const float mx = max_xor32(mxl);
       const bool grow = fresh ? (mx != -INFINITY) : (mx > kRescaleLog2);
       if (__any(grow)) {
@@ -1977,26 +1976,26 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp4(FlashParams p) {
       __builtin_amdgcn_sched_barrier(0);
     };
 
-    // ---- phases 2t (group 0: G(t), group 1: A(t-1)) and 2t+1 (group 0: A(t),
-    // group 1: G(t)) for t = 0 .. n_kt, as flash_fwd_pp3.  Phase 2t+2 reads
-    // K_{t+1} and V^T_t, which group 0 issued in phase 2t and waited for at
-    // the end of phase 2t+1. ----------------------------------------------------------
+    // ---- group 0 runs G(t), A(t); group 1 runs A(t-1), G(t), for t = 0 .. n_kt.
+    // One barrier per t, after group 0's A(t) (which waits for the loads it
+    // issued in G(t)) and group 1's G(t): G(t+1) then finds K_{t+1} and
+    // V^T_t in LDS, and the buffers G(t+1)'s loads overwrite (K_{t-1}'s,
+    // V^T_{t-1}'s) were last read in G(t).  Between barriers the groups are
+    // not forced to alternate; G phases run at raised priority, so the MFMA
+    // work of one group overlaps the other's softmax. -------------------------------
     if (n_kt > 0) {
       if (group == 0) {
         g_phase(0, std::true_type{}, std::false_type{});
-        lds_barrier();
         a_phase(0);
         wait_vmcnt<0>();
         lds_barrier();
         for (int t = 1; t <= n_kt; ++t) {
           g_phase(t, std::true_type{}, std::true_type{});
-          lds_barrier();
           a_phase(t);
           wait_vmcnt<0>();
           lds_barrier();
         }
       } else {
-        lds_barrier();  // phase 0: nothing to do (A of tile -1)
         g_phase(0, std::false_type{}, std::false_type{});
         lds_barrier();
         // Group 0's next Q rows into the fifth buffer (read only at the switch).
@@ -2008,7 +2007,6 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp4(FlashParams p) {
         }
         for (int t = 1; t <= n_kt; ++t) {
           a_phase(t - 1);
-          lds_barrier();
           g_phase(t, std::false_type{}, std::true_type{});
           if (t == n_kt) wait_vmcnt<0>();
           lds_barrier();
