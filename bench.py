@@ -260,12 +260,12 @@ def bench_prefill(cfg, steps, warmup, cpu=True):
         "wall_ms_per_step": wall_ms,
         "roofline": {
             "bound": "mfma",
-            "kernel": "flash_fwd (+ V^T staging for 16-bit) (tl_attention_fwd)",
+            "kernel": "flash_fwd_16 + vt_pack_kernel (tl_attention_fwd)",
             "achieved": tf,
             "peak": peak,
             "unit": "TFLOP/s",
             "frac": tf / peak,
-            "traffic": profile_traffic("flash_fwd_pp_llama3.2-3b-prefill.md") if cfg.name == oi.CONFIGS["5a"].name else None,
+            "traffic": profile_traffic("flash_fwd_16_llama3.2-3b-prefill.md") if cfg.name == oi.CONFIGS["5a"].name else None,
             "algorithmic_flops": flops,
             "kernel_ms": ms,
         },

@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_workspace_queries():
     lib = _lib.load()
-    # fp32 reads V in place; the 16-bit MFMA path stages V^T: B * Hkv * D * round_up(Sk, 64) * 2.
+    # fp32 reads V in place; the 16-bit MFMA path stages V^T: B * Hkv * D * round_up(Sk, 128) * 2.
     assert lib.tl_attention_fwd_workspace_bytes(1, 8, 8192, 128, _lib.DTYPE_F32) == 0
     assert lib.tl_attention_fwd_workspace_bytes(1, 8, 8192, 128, _lib.DTYPE_BF16) == 8 * 128 * 8192 * 2
     assert lib.tl_attention_fwd_workspace_bytes(2, 3, 100, 64, _lib.DTYPE_F16) == 2 * 3 * 64 * 128 * 2

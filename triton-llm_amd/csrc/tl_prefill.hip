@@ -7,8 +7,9 @@
 // output = acc / row_sum.  The reference runs one program per (row, head)
 // with vector multiply-reduce; these kernels are flash-style tiled kernels on
 // MFMA: each wave owns 32 query rows of one query head and walks key tiles
-// of BN = 64 staged through LDS (16-bit kernel: 8 waves = 256 rows per
-// workgroup in two ping-pong groups; fp32 kernel: 4 waves = 128 rows).
+// staged through LDS (16-bit kernel: 8 waves = 256 rows per workgroup in two
+// ping-pong groups, 128-key tiles; fp32 kernel: 4 waves = 128 rows, 64-key
+// tiles).
 //
 // It computes the TRANSPOSED products  S^T = K . Q^T  and  O^T = V^T . P^T
 // with 32x32 MFMA tiles.  In the 32x32 accumulator layout lane l holds
@@ -28,7 +29,7 @@
 // registers (lane half h holds keys 8a + 4h + b, b < 4, of each 32-key
 // block) and the V^T operand is read with the matching key permutation.
 //
-// Kernels: vt_pack_kernel + flash_fwd_pp (f16 / bf16, d_k 64 / 128), flash_fwd_f32
+// Kernels: vt_pack_kernel + flash_fwd_16 (f16 / bf16, d_k 64 / 128), flash_fwd_f32
 // (fp32, d_k 64 / 128), attn_generic_kernel (any d_k <= 256).
 #include "tl_common.h"
 
@@ -55,7 +56,7 @@ struct FlashParams {
   int64_t v_sb, v_sh, v_ss;
   int64_t o_sb, o_sh, o_ss;
   float scale_log2;
-  // Static tile schedule of the persistent 16-bit kernel (see flash_fwd_pp4).
+  // Static tile schedule of the persistent 16-bit kernel (see flash_fwd_16).
   int n_queues;    // 8 (one tile list per XCD) or 1
   int q_units;     // (batch, kv head) units per list
   int q_tiles;     // tiles per list: q_units * n_qt * group
@@ -115,79 +116,51 @@ __device__ __forceinline__ void decode_block(const FlashParams& p, int& b, int& 
 }
 
 // ---------------------------------------------------------------------------
-// 16-bit (f16 / bf16) kernel: two wave groups in ping-pong.
+// 16-bit (f16 / bf16) kernel, d_k 64 / 128.
 //
-// Workgroup = 8 waves = 2 groups of 4; each wave owns 32 query rows, group g
-// the rows [128 g, 128 g + 128) of the workgroup's 256.  Both groups walk the
-// same 64-key K / V tiles.  Per tile a group runs
-//     G0(t): S^T = K_t . Q^T        (MFMA)
-//     A(t):  masked online softmax  (VALU: max, exp2, pack, row sum)
-//     G1(t): O^T += V_t^T . P_t^T   (MFMA)
-// and the work is cut into phases separated by workgroup barriers:
-//     phase 2t   : group 0 runs {G1(t-1), G0(t)}   group 1 runs A(t-1)
-//     phase 2t+1 : group 0 runs A(t)               group 1 runs {G1(t-1), G0(t)}
-// so on every SIMD (one wave of each group) one wave issues MFMAs while the
-// other does the softmax.  K_{t+1} and V^T_t are loaded into registers at
-// the start of phase 2t and written to LDS at the start of phase 2t+1, into
-// the buffers freed at the end of phase 2t-1; two buffers each.
+// Workgroup = 8 waves = 2 groups of 4, one workgroup per CU; each wave owns
+// 32 query rows, group g rows [128 g, 128 g + 128) of a 256-row query tile.
+// Both groups walk the same 128-key K / V^T tiles.  Per key tile t a wave
+// runs
+//     G(t): O^T += V^T_{t-1} . P^T_{t-1} and S^T_t = K_t . Q^T   (64 MFMAs)
+//     A(t): masked online softmax of S_t -> P_t                   (VALU)
+// group 0 in the order G(t), A(t) and group 1 in the order A(t-1), G(t), so
+// on every SIMD (one wave of each group) one wave issues MFMAs while the
+// other does its softmax.  One workgroup barrier per t publishes the next K
+// and V^T tiles (loaded by group 0 with LDS-DMA during G(t), waited for at
+// the end of A(t)) and frees the buffers the following loads overwrite; two
+// buffers each for K and V^T (128 KiB at d_k 128).
+//
+// S^T accumulators are seeded with -m_run (Q is pre-scaled by
+// sm_scale * log2 e), so P = exp2(S) directly; the row sum is kept in fp32
+// per lane (v_dot2 would not co-execute with the other wave's MFMAs).  The
+// running offset m_run is raised (and O rescaled) only when a tile's max
+// exceeds it by more than kRescaleLog2 (log2 units), which bounds P by
+// 2^kRescaleLog2.
 //
 // V is read from a key-major copy V^T [b][kv][d][Sk_pad] written once per
 // call by vt_pack_kernel, with each 16-key group stored in the order the
 // MFMA's k-index permutation wants (see vt_pack_kernel), so the 8 keys a lane
 // feeds into one PV MFMA are one contiguous 16 bytes: ds_read_b128, the same
 // fast LDS path as the K operand.  (A transposing LDS read of natural V,
-// ds_read_b64_tr_b16, measured ~3x lower LDS throughput per byte on gfx950
-// and bounded the kernel.)
+// ds_read_b64_tr_b16, measured ~3x lower LDS throughput per byte on gfx950.)
 //
 // LDS rows are unpadded; the 16-byte chunk c of row r lives in slot
-// c ^ swz(r) (lds_swz for K rows, vt_swz for V^T rows), which makes every
-// operand read conflict-free.
-//
-// Softmax per score: one max (amortised over max3), one FMA applying the
-// scale and subtracting the running max, one exp2, half a convert; the row
-// sum is a v_dot2 over the packed 16-bit P the PV product consumes.  The
-// running max is raised (and O rescaled) only when a tile's max exceeds it by
-// more than kRescaleLog2 (log2 units), which bounds P by 2^kRescaleLog2.
+// c ^ lds_swz(r) (lds_swz<D> for K and Q rows, lds_swz<128> for the 256-byte
+// V^T rows), which makes every operand read conflict-free.
 // ---------------------------------------------------------------------------
+constexpr int K16_BM = 256;       // query rows per tile
+constexpr int K16_BN = 128;       // keys per K / V^T tile
+constexpr int K16_THREADS = 512;  // 8 waves
 constexpr float kRescaleLog2 = 8.0f;
-constexpr int PP_THREADS = 512;
-constexpr int PP_BM = 256;  // query rows per workgroup
-constexpr int PP_BN = 64;   // keys per tile
 
-// V^T rows in LDS are 64 keys x 2 B = 128 B; 16 consecutive rows read the
-// same chunk, so the slot is XORed with (row / 2) % 8 (rows of one parity
-// share a bank half).
-__device__ __forceinline__ int vt_swz(int r) { return (r >> 1) & 7; }
-
+// Slot swizzle of LDS rows of D 16-bit elements: 16 consecutive rows read
+// the same 16-byte chunk of their row in one operand load, so the chunk is
+// XORed with bits of the row index that spread those rows over all banks.
 template <int D>
 __device__ __forceinline__ int lds_swz(int r) {
   if constexpr (D == 128) return 4 * (r & 3) + ((r >> 2) & 3);
   else return 4 * ((r >> 1) & 1) + ((r >> 2) & 3);
-}
-
-template <typename T>
-__device__ __forceinline__ float dot2_sum(typename Mfma<T>::frag pf, float acc);
-
-template <>
-__device__ __forceinline__ float dot2_sum<BF16>(bf16x8 pf, float acc) {
-  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    bf16x2 pr = {pf[2 * i], pf[2 * i + 1]};
-    acc = __builtin_amdgcn_fdot2_f32_bf16(pr, one, acc, false);
-  }
-  return acc;
-}
-
-template <>
-__device__ __forceinline__ float dot2_sum<F16>(f16x8 pf, float acc) {
-  const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f16x2 pr = {pf[2 * i], pf[2 * i + 1]};
-    acc = __builtin_amdgcn_fdot2(pr, one, acc, false);
-  }
-  return acc;
 }
 
 // Two fp32 values -> one 32-bit word of two 16-bit values (low half first),
@@ -205,21 +178,6 @@ __device__ __forceinline__ uint32_t pack2<F16>(const float (&x)[2]) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// acc + lo + hi of a packed 16-bit pair (v_dot2 with (1, 1)).
-template <typename T>
-__device__ __forceinline__ float dot2_word(uint32_t w, float acc);
-template <>
-__device__ __forceinline__ float dot2_word<BF16>(uint32_t w, float acc) {
-  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), one, acc, false);
-}
-template <>
-__device__ __forceinline__ float dot2_word<F16>(uint32_t w, float acc) {
-  const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
-  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), one, acc, false);
-}
-
-// Max of lane l and lane l ^ 32 (both lanes receive it).
 __device__ __forceinline__ float max_xor32(float x) {
   const uint32_t u = __float_as_uint(x);
   const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
@@ -246,1360 +204,8 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-
-template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(PP_THREADS, 2) void flash_fwd_pp(FlashParams p) {
-  using M = Mfma<T>;
-  using frag = typename M::frag;
-  using Bits = typename T::bits;
-  constexpr int BN = PP_BN;
-  constexpr int ROWB = D * 2;         // bytes per K / V row in LDS
-  constexpr int TILEB = BN * ROWB;    // bytes per K or V tile
-  constexpr int NSL = ROWB / 16;      // 16-byte slots per row
-  constexpr int RPR = 1024 / ROWB;    // rows per 1 KiB region
-  constexpr int NREG = TILEB / 1024;  // 1 KiB regions per tile
-  constexpr int RPW = NREG / 8;       // regions per wave per tile
-  constexpr int NDB = D / 32;         // 32-row blocks of O^T
-  constexpr int NKS = D / 16;         // k-steps of S^T
-  static_assert(RPW * 8 == NREG, "tile must split into 1 KiB regions per wave");
-
-  __shared__ __attribute__((aligned(1024))) char smem[6 * TILEB];  // K0 K1 K2 V0 V1 V2
-
-  int b, hq, qt;
-  decode_block(p, b, hq, qt);
-  const int hkv = hq / p.group;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int group = wave >> 2;
-  const int lq = lane & 31;
-  const int h = lane >> 5;
-  const int off = p.seq_k - p.seq_q;  // bottom-right causal offset
-
-  const int q_first = qt * PP_BM;
-  const int q_last = min(p.seq_q, q_first + PP_BM) - 1;
-  int k_end = p.seq_k;
-  if (CAUSAL) k_end = max(0, min(p.seq_k, q_last + off + 1));
-  const int n_kt = (k_end + BN - 1) / BN;
-
-  const int q0 = q_first + 128 * group + 32 * (wave & 3);  // first row of this wave
-  const int qi = q0 + lq;                                  // this lane's query row
-  int wave_k_end = p.seq_k;
-  if (CAUSAL) wave_k_end = max(0, min(p.seq_k, min(q0 + 31, p.seq_q - 1) + off + 1));
-  if (q0 >= p.seq_q) wave_k_end = 0;  // no rows: skip all compute
-
-  frag qf[NKS];
-  {
-    const Bits* qrow = (const Bits*)p.q + b * p.q_sb + hq * p.q_sh + (int64_t)qi * p.q_ss;
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      u32x4 raw = {0u, 0u, 0u, 0u};
-      if (qi < p.seq_q) raw = *(const u32x4*)(qrow + 16 * ks + 8 * h);
-      qf[ks] = __builtin_bit_cast(frag, raw);
-    }
-  }
-
-  f32x16 o_acc[NDB];
-#pragma unroll
-  for (int i = 0; i < NDB; ++i)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o_acc[i][r] = 0.f;
-  float m_run = -INFINITY;  // running max of scaled scores (log2 domain)
-  float l_run = 0.f;        // this lane's half of the row sum
-  f32x16 s[2];
-  frag pfr[BN / 16];
-
-  // Direct global -> LDS tile loads.  Wave w fills 1 KiB regions w + 8 i; lane
-  // l of a region holds row R * RPR + l / NSL, slot l % NSL, i.e. the chunk
-  // (l % NSL) ^ swz(row) of that row.
-  const Bits* kbase = (const Bits*)p.k + b * p.k_sb + hkv * p.k_sh;
-  const Bits* vtbase = (const Bits*)p.vt + ((int64_t)b * p.n_kv + hkv) * D * p.sk_pad;
-  // K tile: 64 key rows of ROWB bytes.  V^T tile: D rows of 64 keys (128 B).
-  constexpr int VT_RPR = 1024 / (BN * 2);  // V^T rows per 1 KiB region (8)
-  int ld_row[RPW], ld_col[RPW], vt_off[RPW];
-#pragma unroll
-  for (int i = 0; i < RPW; ++i) {
-    const int row = (wave + 8 * i) * RPR + lane / NSL;
-    ld_row[i] = row;
-    ld_col[i] = ((lane % NSL) ^ lds_swz<D>(row)) * 8;
-    const int vrow = (wave + 8 * i) * VT_RPR + lane / 8;
-    vt_off[i] = vrow * p.sk_pad + ((lane % 8) ^ vt_swz(vrow)) * 8;
-  }
-  // Tiles go straight from global memory into LDS (global_load_lds_dwordx4:
-  // lane l of one wave instruction lands at the LDS region base + 16 l), three
-  // buffers each for K and V^T, issued about two tiles ahead: in its MFMA phase
-  // for tile t (phase 2t for group 0, 2t+1 for group 1) a wave issues its share
-  // of K_{t+2} and V^T_{t+1}, spread between its MFMAs.  A wave blocks while
-  // the CU's vector-memory path drains other waves' loads, so the issue is
-  // placed where the wave waits on the matrix pipe anyway, and the softmax
-  // wave of the phase issues no memory operations at all.  Each wave waits for
-  // its own loads with s_waitcnt vmcnt before the phase barrier that precedes
-  // their first use.  The loads are inline asm so
-  // that the compiler's wait insertion does not see LDS-DMA inside the loop:
-  // with the builtin it falls back to lgkmcnt(0) before every LDS operand read,
-  // which serialises the pipelined operand reads of the MFMA stream.  (M0 is a
-  // reserved register the compiler only sets right before the few instructions
-  // that read it; none of those appear in this kernel.)
-  auto dma = [&](const void* gaddr, char* lds) {
-    const uint32_t la = __builtin_amdgcn_readfirstlane(
-        (uint32_t)(size_t)(__attribute__((address_space(3))) char*)lds);
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(la), "v"(gaddr) : "memory");
-  };
-  char* kbuf = smem;
-  char* vbuf = smem + 3 * TILEB;
-  auto issue_k = [&](int t) {  // K_t -> kbuf[t % 3]
-    char* buf = kbuf + (t % 3) * TILEB;
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-      const int key = min(t * BN + ld_row[i], p.seq_k - 1);  // rows past the end: any valid row
-      dma(kbase + (int64_t)key * p.k_ss + ld_col[i], buf + (wave + 8 * i) * 1024);
-    }
-  };
-  auto issue_v = [&](int t) {  // V^T_t -> vbuf[t % 3]
-    char* buf = vbuf + (t % 3) * TILEB;
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) dma(vtbase + t * BN + vt_off[i], buf + (wave + 8 * i) * 1024);
-  };
-  // Entry e < 2 * RPW of the loads a wave issues in its MFMA phase for tile
-  // t: K_{t+2} region e (e < RPW), then V^T_{t+1} region e - RPW.
-  auto issue_entry = [&](int t, int e) {
-    if (e < RPW) {
-      if (t + 2 < n_kt) {
-        const int key = min((t + 2) * BN + ld_row[e], p.seq_k - 1);
-        dma(kbase + (int64_t)key * p.k_ss + ld_col[e], kbuf + ((t + 2) % 3) * TILEB + (wave + 8 * e) * 1024);
-      }
-    } else if (t + 1 < n_kt) {
-      const int i = e - RPW;
-      dma(vtbase + (t + 1) * BN + vt_off[i], vbuf + ((t + 1) % 3) * TILEB + (wave + 8 * i) * 1024);
-    }
-  };
-
-  const float c = p.scale_log2;
-  auto tile_active = [&](int t) { return t >= 0 && t < n_kt && t * BN < wave_k_end; };
-
-  // G0(t): S^T = K_t . Q^T
-  auto gemm0 = [&](int t) {
-    const char* Kb = kbuf + (t % 3) * TILEB;
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[mb][r] = 0.f;
-      const int row = 32 * mb + lq;
-      const char* krow = Kb + row * ROWB;
-      const int sw = lds_swz<D>(row);
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        frag a = __builtin_bit_cast(frag, *(const u32x4*)(krow + (((2 * ks + h) ^ sw) << 4)));
-        s[mb] = M::mma(a, qf[ks], s[mb]);
-      }
-    }
-  };
-  // G1(t): O^T += V_t^T . P_t^T.  Lane (d = 32 db + lq, half h) reads the 8
-  // keys 16 tt + 8 h .. +7 of the permuted V^T row d: one 16-byte chunk.
-  auto gemm1 = [&](int t) {
-    const char* Vb = vbuf + (t % 3) * TILEB;
-#pragma unroll
-    for (int tt = 0; tt < BN / 16; ++tt)
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        const int row = 32 * db + lq;
-        const u32x4 raw = *(const u32x4*)(Vb + row * (BN * 2) + (((2 * tt + h) ^ vt_swz(row)) << 4));
-        o_acc[db] = M::mma(__builtin_bit_cast(frag, raw), pfr[tt], o_acc[db]);
-      }
-  };
-  // {G1(t-1), G0(t)} as one stream: PV and S MFMAs alternate (NDB + 2
-  // independent accumulator chains), and the LDS operand reads run kPrefetch
-  // jobs ahead of their MFMA so no MFMA waits on LDS latency.
-  //
-  // Operand addresses: the swizzle term of K row 32 mb + lq does not depend on
-  // mb, and that of V^T row 32 db + lq does not depend on db, so one lane
-  // constant per k-step (K) and per 16-key step (V^T) covers every read; mb
-  // and db become immediate offsets.
-  int k_addr[NKS], v_addr[BN / 16];
-  {
-    const int swk = lds_swz<D>(lq);
-    const int swv = vt_swz(lq);  // == vt_swz(32 db + lq) for every db
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) k_addr[ks] = lq * ROWB + (((2 * ks + h) ^ swk) << 4);
-#pragma unroll
-    for (int tt = 0; tt < BN / 16; ++tt) v_addr[tt] = lq * (BN * 2) + (((2 * tt + h) ^ swv) << 4);
-  }
-  // The wave's tile loads (issue_entry) ride along: one every 4 jobs.
-  auto gemm10 = [&](int t) {
-    constexpr int NG = BN / 16 * NDB;  // jobs per GEMM (== 2 * NKS)
-    static_assert(NG == 2 * NKS, "S and PV job counts must match");
-    static_assert(2 * RPW <= (NG + 2) / 4, "every load needs an issue slot");
-    constexpr int kPrefetch = 2;
-    const char* Kb = kbuf + (t % 3) * TILEB;
-    const char* Vb = vbuf + ((t + 2) % 3) * TILEB;  // V^T_{t-1}
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[mb][r] = 0.f;
-    u32x4 kfr[NG], vfr[NG];
-    auto fetch = [&](int g) {
-      const int tt = g / NDB, db = g % NDB;  // PV job: keys 16 tt.., d-block db
-      vfr[g] = *(const u32x4*)(Vb + v_addr[tt] + 32 * db * (BN * 2));
-      const int ks = g >> 1, mb = g & 1;  // S job: k-step ks, key block mb
-      kfr[g] = *(const u32x4*)(Kb + k_addr[ks] + 32 * mb * ROWB);
-    };
-#pragma unroll
-    for (int g = 0; g < kPrefetch; ++g) fetch(g);
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      if (g + kPrefetch < NG) fetch(g + kPrefetch);
-      const int tt = g / NDB, db = g % NDB;
-      o_acc[db] = M::mma(__builtin_bit_cast(frag, vfr[g]), pfr[tt], o_acc[db]);
-      s[g & 1] = M::mma(__builtin_bit_cast(frag, kfr[g]), qf[g >> 1], s[g & 1]);
-      if (g % 4 == 1 && g / 4 < 2 * RPW) issue_entry(t, g / 4);
-      __builtin_amdgcn_sched_barrier(0);  // keep reads kPrefetch jobs ahead
-    }
-  };
-  // A(t): masked online softmax of S_t -> P_t
-  auto softmax = [&](int t) {
-    const int kb = t * BN;
-    const bool need_mask = (kb + BN > p.seq_k) || (CAUSAL && kb + BN - 1 > q0 + off);
-    if (need_mask) {
-      // key = kb + 32mb + 8(r/4) + 4h + r%4 must be < seq_k and <= qi + off.
-      int lim = p.seq_k - 1 - kb - 4 * h;
-      if (CAUSAL) lim = min(lim, qi + off - kb - 4 * h);
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int kl = 32 * mb + 8 * (r >> 2) + (r & 3);
-          s[mb][r] = kl <= lim ? s[mb][r] : -INFINITY;
-        }
-    }
-    float mx = s[0][0];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int r = (mb == 0 ? 1 : 0); r < 16; ++r) mx = fmaxf(mx, s[mb][r]);
-    mx = max_xor32(mx) * c;  // c > 0: scaling preserves the order
-    if (__any(mx > m_run + kRescaleLog2)) {
-      const float m_new = fmaxf(m_run, mx);
-      const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2(m_run - m_new);
-      m_run = m_new;
-      l_run *= alpha;
-#pragma unroll
-      for (int i = 0; i < NDB; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o_acc[i][r] *= alpha;
-    }
-    const float nb = (m_run == -INFINITY) ? 0.f : -m_run;
-#pragma unroll
-    for (int tt = 0; tt < BN / 16; ++tt) {
-      float pv[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) pv[j] = fast_exp2(fmaf(s[tt >> 1][8 * (tt & 1) + j], c, nb));
-      pfr[tt] = M::pack(pv);
-      l_run = dot2_sum<T>(pfr[tt], l_run);
-    }
-  };
-
-  if (n_kt > 0) {
-    // Q is in registers before any DMA is issued (the compiler's own wait for
-    // Q must not cover loads it cannot see).
-    wait_vmcnt<0>();
-    issue_k(0);
-    if (n_kt > 1) issue_k(1);
-    issue_v(0);
-    if (n_kt > 1) wait_vmcnt<2 * RPW>();  // K_0 landed; K_1, V^T_0 may be in flight
-    else wait_vmcnt<RPW>();
-    lds_barrier();
-  }
-  const int n_phase = n_kt > 0 ? 2 * n_kt + 2 : 0;
-  for (int ph = 0; ph < n_phase; ++ph) {
-    const int t = ph >> 1;
-    if ((ph & 1) == group) {
-      // MFMA phase: G1(t-1) then G0(t), plus this wave's loads for K_{t+2}
-      // and V^T_{t+1}.
-      __builtin_amdgcn_s_setprio(1);
-      const bool a1 = tile_active(t - 1), a0 = tile_active(t);
-      if (a1 && a0) {
-        gemm10(t);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 2 * RPW; ++e) issue_entry(t, e);
-        if (a1) gemm1(t - 1);
-        if (a0) gemm0(t);
-      }
-      __builtin_amdgcn_s_setprio(0);
-    } else {
-      const int ta = group == 0 ? t : t - 1;
-      if (tile_active(ta)) softmax(ta);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    if (ph & 1) {
-      // Phase 2t+2 reads K_{t+1} and V^T_t, issued in this wave's MFMA phase
-      // for tile t-1 (or the prologue); only the loads it issued for tile t
-      // (phase 2t or 2t+1) may still be in flight.
-      const int n_new = (t + 2 < n_kt ? RPW : 0) + (t + 1 < n_kt ? RPW : 0);
-      if (n_new == 2 * RPW) wait_vmcnt<2 * RPW>();
-      else if (n_new == RPW) wait_vmcnt<RPW>();
-      else wait_vmcnt<0>();
-    }
-    lds_barrier();
-  }
-
-  // Epilogue: O[qi][d] = O^T[d][qi] / l.
-  const float inv = 1.f / sum_xor32(l_run);
-  if (qi < p.seq_q) {
-    Bits* orow = (Bits*)p.o + b * p.o_sb + hq * p.o_sh + (int64_t)qi * p.o_ss;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const int d0 = 32 * db + 8 * rq + 4 * h;
-        uint32_t w0 = (uint32_t)from_f32<T>(o_acc[db][4 * rq + 0] * inv) |
-                      ((uint32_t)from_f32<T>(o_acc[db][4 * rq + 1] * inv) << 16);
-        uint32_t w1 = (uint32_t)from_f32<T>(o_acc[db][4 * rq + 2] * inv) |
-                      ((uint32_t)from_f32<T>(o_acc[db][4 * rq + 3] * inv) << 16);
-        *(u32x2*)(orow + d0) = u32x2{w0, w1};
-      }
-  }
-}
-
 // ---------------------------------------------------------------------------
-// 16-bit (f16 / bf16) kernel, software-pipelined inside each wave.
-//
-// Workgroup = 8 waves = 256 query rows, 32 per wave; all waves walk the same
-// 64-key K / V^T tiles.  Per tile t a wave runs
-//     region A(t):  exp / pack / row sum of S_t -> P_t         (VALU)
-//                   interleaved with S_{t+1} = K_{t+1} . Q^T   (16 MFMAs)
-//     region B(t):  O^T += V_t^T . P_t^T                       (16 MFMAs)
-//                   interleaved with mask + row max of S_{t+1} (VALU)
-//                   and this wave's loads for K_{t+3}, V^T_{t+2}
-// so the wave keeps issuing VALU work while its own MFMAs run in the matrix
-// pipe, and both waves sharing a SIMD contribute VALU issue at all times.
-// (A two-group ping-pong, where one wave does all the softmax of a phase
-// while the other issues MFMAs, is bound by one wave's VALU issue rate:
-// measured ~2000 cycles of softmax against ~1250 of MFMA per phase.)
-//
-// The running max is raised (and O rescaled) only when a tile's max exceeds
-// it by more than kRescaleLog2, between the regions of an iteration.
-// K / V^T tiles go global -> LDS with four buffers each, issued three (K)
-// and two (V^T) tiles ahead; one workgroup barrier per tile.
-// ---------------------------------------------------------------------------
-constexpr int IP_BM = 256;
-constexpr int IP_THREADS = 512;
-constexpr int IP_NBUF = 4;
-
-template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(IP_THREADS, 2) void flash_fwd_ip(FlashParams p) {
-  using M = Mfma<T>;
-  using frag = typename M::frag;
-  using Bits = typename T::bits;
-  constexpr int BN = PP_BN;
-  constexpr int ROWB = D * 2;         // bytes per K row in LDS
-  constexpr int TILEB = BN * ROWB;    // bytes per K or V^T tile
-  constexpr int NSL = ROWB / 16;      // 16-byte slots per K row
-  constexpr int RPR = 1024 / ROWB;    // K rows per 1 KiB region
-  constexpr int NREG = TILEB / 1024;  // 1 KiB regions per tile
-  constexpr int RPW = NREG / 8;       // regions per wave per tile
-  constexpr int NDB = D / 32;         // 32-row blocks of O^T
-  constexpr int NKS = D / 16;         // k-steps of S^T
-  constexpr int NG = 2 * NKS;         // MFMA jobs per product (S: NKS x 2, PV: 4 x NDB)
-  static_assert(RPW * 8 == NREG, "tile must split into 1 KiB regions per wave");
-  static_assert(BN / 16 * NDB == NG, "S and PV job counts must match");
-  static_assert(2 * RPW <= (NG + 2) / 4, "every tile load needs an issue slot");
-
-  __shared__ __attribute__((aligned(1024))) char smem[2 * IP_NBUF * TILEB];  // K0..K3 V0..V3
-
-  int b, hq, qt;
-  decode_block(p, b, hq, qt);
-  const int hkv = hq / p.group;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int lq = lane & 31;
-  const int h = lane >> 5;
-  const int off = p.seq_k - p.seq_q;  // bottom-right causal offset
-
-  const int q_first = qt * IP_BM;
-  const int q_last = min(p.seq_q, q_first + IP_BM) - 1;
-  int k_end = p.seq_k;
-  if (CAUSAL) k_end = max(0, min(p.seq_k, q_last + off + 1));
-  const int n_kt = (k_end + BN - 1) / BN;  // tiles the workgroup loads
-
-  const int q0 = q_first + 32 * wave;  // first row of this wave
-  const int qi = q0 + lq;              // this lane's query row
-  int wave_k_end = p.seq_k;
-  if (CAUSAL) wave_k_end = max(0, min(p.seq_k, min(q0 + 31, p.seq_q - 1) + off + 1));
-  if (q0 >= p.seq_q) wave_k_end = 0;                 // no rows: no compute
-  const int n_kw = (wave_k_end + BN - 1) / BN;        // tiles this wave computes (<= n_kt)
-
-  frag qf[NKS];
-  {
-    const Bits* qrow = (const Bits*)p.q + b * p.q_sb + hq * p.q_sh + (int64_t)qi * p.q_ss;
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      u32x4 raw = {0u, 0u, 0u, 0u};
-      if (qi < p.seq_q) raw = *(const u32x4*)(qrow + 16 * ks + 8 * h);
-      // q <- round(q * sm_scale * log2 e): S then comes out of the MFMA
-      // already in the exp2 domain (a relative perturbation of q of at most
-      // half an ulp of the 16-bit type, like the rounding of P itself).
-      uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float lo, hi;
-        unpack2<T>(w[i], lo, hi);
-        w[i] = (uint32_t)from_f32<T>(lo * p.scale_log2) | ((uint32_t)from_f32<T>(hi * p.scale_log2) << 16);
-      }
-      qf[ks] = __builtin_bit_cast(frag, u32x4{w[0], w[1], w[2], w[3]});
-    }
-  }
-
-  f32x16 o_acc[NDB];
-#pragma unroll
-  for (int i = 0; i < NDB; ++i)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o_acc[i][r] = 0.f;
-  // Scores are kept relative to a per-row offset m_run (log2 domain): every
-  // S tile is accumulated on top of s_init = -m_run (the MFMA's C operand), so
-  // p = exp2(S) needs no per-score arithmetic.  m_run starts at 0 ("fresh":
-  // no visible key yet); it is set by the first visible tile and raised only
-  // when a tile's max exceeds it by more than 2^kRescaleLog2.
-  float m_run = 0.f;
-  bool fresh = true;
-  float l_run = 0.f;          // this lane's half of the row sum
-  float mx_next = -INFINITY;  // max of the next tile's relative scores
-  f32x16 s_init;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) s_init[r] = 0.f;
-
-  // ---- tile loads: global -> LDS (see flash_fwd_pp for the layout) --------
-  // Wave w fills 1 KiB regions w + 8 i of a tile.  Each load is the
-  // scalar-base form global_load_lds_dwordx4 voff, s[base]: the per-lane byte
-  // offset within a tile is a constant, the tile base advances in SGPRs and
-  // the LDS address (M0) is scalar, so a load costs no VALU work.
-  const char* kg = (const char*)((const Bits*)p.k + b * p.k_sb + hkv * p.k_sh);
-  const char* vg = (const char*)((const Bits*)p.vt + ((int64_t)b * p.n_kv + hkv) * D * p.sk_pad);
-  constexpr int VT_RPR = 1024 / (BN * 2);  // V^T rows per 1 KiB region (8)
-  auto k_row = [&](int i) { return (wave + 8 * i) * RPR + lane / NSL; };
-  auto k_col = [&](int i) { return ((lane % NSL) ^ lds_swz<D>(k_row(i))) * 8; };
-  uint32_t k_voff[RPW], v_voff[RPW];  // bytes; the host keeps them below 2^32
-#pragma unroll
-  for (int i = 0; i < RPW; ++i) {
-    k_voff[i] = (uint32_t)(((int64_t)k_row(i) * p.k_ss + k_col(i)) * 2);
-    const int vrow = (wave + 8 * i) * VT_RPR + lane / 8;
-    v_voff[i] = (uint32_t)(((int64_t)vrow * p.sk_pad + ((lane % 8) ^ vt_swz(vrow)) * 8) * 2);
-  }
-  const uint32_t wave_lds = __builtin_amdgcn_readfirstlane((uint32_t)wave * 1024u);
-  const uint32_t lds_k0 = (uint32_t)(size_t)(__attribute__((address_space(3))) char*)smem;
-  const uint32_t lds_v0 = lds_k0 + IP_NBUF * TILEB;
-  auto dma = [&](const char* gbase, uint32_t voff, uint32_t la) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(la), "v"(voff), "s"(gbase) : "memory");
-  };
-  auto load_k = [&](int t, int i) {  // region i of K_t -> K buffer t % 4
-    uint32_t voff = k_voff[i];
-    if (t * BN + BN > p.seq_k)  // last tile: rows past the end re-read the last row
-      voff = (uint32_t)(((int64_t)min(k_row(i), p.seq_k - 1 - t * BN) * p.k_ss + k_col(i)) * 2);
-    dma(kg + (int64_t)t * BN * p.k_ss * 2, voff, lds_k0 + (t % IP_NBUF) * TILEB + i * 8192 + wave_lds);
-  };
-  auto load_v = [&](int t, int i) {  // region i of V^T_t -> V^T buffer t % 4
-    dma(vg + (int64_t)t * BN * 2, v_voff[i], lds_v0 + (t % IP_NBUF) * TILEB + i * 8192 + wave_lds);
-  };
-  // Entry e < 2 RPW of the loads issued during iteration t: K_{t+3} region e,
-  // then V^T_{t+2} region e - RPW.
-  auto load_entry = [&](int t, int e) {
-    if (e < RPW) {
-      if (t + 3 < n_kt) load_k(t + 3, e);
-    } else if (t + 2 < n_kt) {
-      load_v(t + 2, e - RPW);
-    }
-  };
-
-  // ---- LDS operand addresses -------------------------------------------------
-  // K row 32 mb + lq, 16-byte chunk (2 ks + h) ^ swz(row): with 2 ks even,
-  // (2 ks + h) ^ swz = 2 ks ^ (h ^ swz), so the address is one lane base XOR
-  // (ks << 5), and mb / the buffer add as immediates or a per-tile base.
-  // V^T row 32 db + lq, chunk (2 tt + h) ^ vt_swz(row): likewise base ^ (tt << 5).
-  const int k_lane = lq * ROWB + ((h ^ lds_swz<D>(lq)) << 4);
-  const int v_lane = lq * (BN * 2) + ((h ^ vt_swz(lq)) << 4);
-  // LDS operand reads run this many MFMA jobs ahead of their use (K, V^T).
-  constexpr int kPrefetchK = 2, kPrefetchV = 2;
-
-  // Mask S_t (keys past seq_k or above the causal diagonal) and return its
-  // scaled row max.  key = kb + 32 mb + 8 (r/4) + 4 h + r % 4.
-  auto mask_and_max = [&](f32x16 (&st)[2], int t) {
-    const int kb = t * BN;
-    const bool need_mask = (kb + BN > p.seq_k) || (CAUSAL && kb + BN - 1 > q0 + off);
-    if (need_mask) {
-      int lim = p.seq_k - 1 - kb - 4 * h;
-      if (CAUSAL) lim = min(lim, qi + off - kb - 4 * h);
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int kl = 32 * mb + 8 * (r >> 2) + (r & 3);
-          st[mb][r] = kl <= lim ? st[mb][r] : -INFINITY;
-        }
-    }
-    float mx = st[0][0];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int r = (mb == 0 ? 1 : 0); r < 16; ++r) mx = fmaxf(mx, st[mb][r]);
-    return max_xor32(mx);
-  };
-
-  // S_t = K_t . Q^T on its own (prologue).
-  auto s_gemm = [&](f32x16 (&st)[2], int t) {
-    const char* Kb = smem + (t % IP_NBUF) * TILEB;
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      const frag a = __builtin_bit_cast(frag, *(const u32x4*)(Kb + (k_lane ^ ((g >> 1) << 5)) + 32 * (g & 1) * ROWB));
-      st[g & 1] = M::mma(a, qf[g >> 1], g < 2 ? s_init : st[g & 1]);
-    }
-  };
-
-  // One tile step: P_t = exp(S_t - m) packed (VALU), S_{t+1} = K_{t+1} . Q^T
-  // (NG MFMAs) and O^T += V_t^T . P_t^T (NG MFMAs) in one instruction stream
-  // of 20 steps.  Step j < 16 exponentiates score pair j (P chunk j / 4);
-  // S jobs 2j, 2j + 1 run at step j; PV job q (P chunk q / NDB) runs at step
-  // 4 (q / NDB) + 4 + q % NDB, the first step after its chunk is complete.
-  // With MAXS the row max of S_{t+1} is folded in over the steps after the
-  // last S job, while only PV MFMAs remain, so no serial max follows the
-  // stream.  This wave's tile loads ride along every fourth step.
-  // DO_S / DO_P / MAXS: compute S_{t+1} / the softmax + PV of tile t / the
-  // max of S_{t+1} (only when tile t+1 needs no mask).
-  u32x4 pw[BN / 16];  // P_t, packed 16-bit, as the PV MFMA's B operand
-  auto tile_step = [&](f32x16 (&cur)[2], f32x16 (&nxt)[2], int t, auto do_s_tag, auto do_p_tag,
-                       auto maxs_tag) {
-    constexpr bool DO_S = decltype(do_s_tag)::value;
-    constexpr bool DO_P = decltype(do_p_tag)::value;
-    constexpr bool MAXS = decltype(maxs_tag)::value;
-    constexpr int kMaxStep0 = NG / 2 + 2;  // first step of the in-stream max
-    float mx = -INFINITY;
-    const int kb_lane = k_lane + ((t + 1) % IP_NBUF) * TILEB;              // K_{t+1}
-    const int vb_lane = v_lane + (IP_NBUF + t % IP_NBUF) * TILEB;          // V^T_t
-    u32x4 kfr[NG], vfr[NG];
-    auto fetch_k = [&](int g) {
-      kfr[g] = *(const u32x4*)(smem + (kb_lane ^ ((g >> 1) << 5)) + 32 * (g & 1) * ROWB);
-    };
-    auto fetch_v = [&](int q) {
-      const int tt = q / NDB, db = q % NDB;
-      vfr[q] = *(const u32x4*)(smem + (vb_lane ^ (tt << 5)) + 32 * db * (BN * 2));
-    };
-    if constexpr (DO_S) {
-#pragma unroll
-      for (int g = 0; g < kPrefetchK; ++g) fetch_k(g);
-    }
-    if constexpr (DO_P) {
-#pragma unroll
-      for (int q = 0; q < kPrefetchV; ++q) fetch_v(q);
-    }
-#pragma unroll
-    for (int j = 0; j < 20; ++j) {
-      if constexpr (DO_S) {
-#pragma unroll
-        for (int g = 2 * j; g < 2 * j + 2; ++g) {
-          if (g < NG) {
-            if (g + kPrefetchK < NG) fetch_k(g + kPrefetchK);
-            nxt[g & 1] = M::mma(__builtin_bit_cast(frag, kfr[g]), qf[g >> 1], g < 2 ? s_init : nxt[g & 1]);
-          }
-        }
-      }
-      if constexpr (MAXS) {
-        // four scores per step: nxt[mb][r], 4 (j - kMaxStep0) <= 16 mb + r < +4
-        const int i0 = 4 * (j - kMaxStep0);
-        if (i0 >= 0 && i0 < 32) {
-          mx = fmaxf(mx, fmaxf(fmaxf(nxt[i0 >> 4][i0 & 15], nxt[i0 >> 4][(i0 & 15) + 1]),
-                               fmaxf(nxt[i0 >> 4][(i0 & 15) + 2], nxt[i0 >> 4][(i0 & 15) + 3])));
-        }
-        if (j == kMaxStep0 + 8) mx_next = max_xor32(mx);
-      }
-      if constexpr (DO_P) {
-        if (j < 16) {
-          const int tt = j >> 2, j2 = j & 3;
-          const float x0 = cur[tt >> 1][8 * (tt & 1) + 2 * j2];
-          const float x1 = cur[tt >> 1][8 * (tt & 1) + 2 * j2 + 1];
-          float pr2[2] = {fast_exp2(x0), fast_exp2(x1)};
-          const uint32_t w = pack2<T>(pr2);
-          pw[tt][j2] = w;
-          l_run = dot2_word<T>(w, l_run);
-        }
-#pragma unroll
-        for (int q = 0; q < NG; ++q) {
-          if (4 * (q / NDB) + 4 + q % NDB == j) {
-            if (q + kPrefetchV < NG) fetch_v(q + kPrefetchV);
-            o_acc[q % NDB] = M::mma(__builtin_bit_cast(frag, vfr[q]), __builtin_bit_cast(frag, pw[q / NDB]),
-                                    o_acc[q % NDB]);
-          }
-        }
-      }
-      if (j % 4 == 1 && j / 4 < 2 * RPW) load_entry(t, j / 4);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-
-  // ---- prologue -------------------------------------------------------------
-  f32x16 sa[2], sb[2];
-  if (n_kt > 0) {
-    // Q is in registers before any DMA is issued (the compiler's own wait for
-    // Q must not cover loads it cannot see).
-    wait_vmcnt<0>();
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) load_k(0, i);
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) if (1 < n_kt) load_k(1, i);
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) load_v(0, i);
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) if (2 < n_kt) load_k(2, i);
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) if (1 < n_kt) load_v(1, i);
-    // K_0 first: everything issued after it may still be in flight.
-    const int after0 = (1 < n_kt ? 2 * RPW : 0) + RPW + (2 < n_kt ? RPW : 0) + (1 < n_kt ? RPW : 0);
-    if (after0 == 4 * RPW) wait_vmcnt<4 * RPW>();
-    else if (after0 == 3 * RPW) wait_vmcnt<3 * RPW>();
-    else wait_vmcnt<RPW>();
-    lds_barrier();
-    if (n_kw > 0) {
-      s_gemm(sa, 0);
-      mx_next = mask_and_max(sa, 0);
-    }
-    // K_1 and V^T_0 for iteration 0; K_2 and V^T_1 may still be in flight.
-    const int late = (2 < n_kt ? RPW : 0) + (1 < n_kt ? RPW : 0);
-    if (late == 2 * RPW) wait_vmcnt<2 * RPW>();
-    else if (late == RPW) wait_vmcnt<RPW>();
-    else wait_vmcnt<0>();
-    lds_barrier();
-  }
-
-  // ---- main loop: iteration t uses S_t in `cur`, builds S_{t+1} in `nxt` ----
-  auto iteration = [&](f32x16 (&cur)[2], f32x16 (&nxt)[2], int t) {
-    const bool act = t < n_kw, act_next = t + 1 < n_kw;
-    const int kb1 = (t + 1) * BN;
-    const bool mask_next = (kb1 + BN > p.seq_k) || (CAUSAL && kb1 + BN - 1 > q0 + off);
-    if (act) {
-      // Move the offset when this tile's max exceeds it by more than
-      // 2^kRescaleLog2, or when a fresh row sees its first visible key.
-      const bool grow = fresh ? (mx_next != -INFINITY) : (mx_next > kRescaleLog2);
-      if (__any(grow)) {
-        // delta >= 0 unless fresh (then o_acc and l are still zero)
-        const float delta = fresh ? (mx_next == -INFINITY ? 0.f : mx_next) : fmaxf(mx_next, 0.f);
-        const float alpha = fast_exp2(-delta);
-        m_run += delta;
-        fresh = fresh && (mx_next == -INFINITY);
-        l_run *= alpha;
-#pragma unroll
-        for (int i = 0; i < NDB; ++i)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o_acc[i][r] *= alpha;
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) cur[mb][r] -= delta;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s_init[r] = -m_run;
-      }
-    }
-    if (act && act_next && !mask_next) {
-      tile_step(cur, nxt, t, std::true_type{}, std::true_type{}, std::true_type{});
-    } else {
-      if (act && act_next) tile_step(cur, nxt, t, std::true_type{}, std::true_type{}, std::false_type{});
-      else if (act) tile_step(cur, nxt, t, std::false_type{}, std::true_type{}, std::false_type{});
-      else tile_step(cur, nxt, t, std::false_type{}, std::false_type{}, std::false_type{});
-      if (act_next) mx_next = mask_and_max(nxt, t + 1);
-    }
-    // Iteration t+1 reads K_{t+2} and V^T_{t+1}, issued during iteration t-1
-    // (or the prologue); only this iteration's loads may still be in flight.
-    const int n_new = (t + 3 < n_kt ? RPW : 0) + (t + 2 < n_kt ? RPW : 0);
-    if (n_new == 2 * RPW) wait_vmcnt<2 * RPW>();
-    else if (n_new == RPW) wait_vmcnt<RPW>();
-    else wait_vmcnt<0>();
-    lds_barrier();
-  };
-  for (int t = 0; t < n_kt; t += 2) {
-    iteration(sa, sb, t);
-    if (t + 1 < n_kt) iteration(sb, sa, t + 1);
-  }
-
-  // Epilogue: O[qi][d] = O^T[d][qi] / l.
-  const float inv = 1.f / sum_xor32(l_run);
-  if (qi < p.seq_q) {
-    Bits* orow = (Bits*)p.o + b * p.o_sb + hq * p.o_sh + (int64_t)qi * p.o_ss;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const int d0 = 32 * db + 8 * rq + 4 * h;
-        uint32_t w0 = (uint32_t)from_f32<T>(o_acc[db][4 * rq + 0] * inv) |
-                      ((uint32_t)from_f32<T>(o_acc[db][4 * rq + 1] * inv) << 16);
-        uint32_t w1 = (uint32_t)from_f32<T>(o_acc[db][4 * rq + 2] * inv) |
-                      ((uint32_t)from_f32<T>(o_acc[db][4 * rq + 3] * inv) << 16);
-        *(u32x2*)(orow + d0) = u32x2{w0, w1};
-      }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// 16-bit (f16 / bf16) kernel: two wave groups in ping-pong, light softmax.
-//
-// Workgroup = 8 waves = 2 groups of 4; wave w owns 32 query rows, group g
-// the rows [128 g, 128 g + 128) of the workgroup's 256.  Per tile t a group
-// runs G(t) = {O^T += V_{t-1}^T . P_{t-1}^T, S_t = K_t . Q^T} (32 MFMAs in
-// one stream) and A(t) = softmax of S_t -> P_t, in phases separated by
-// workgroup barriers:
-//     phase 2t   : group 0 runs G(t)   group 1 runs A(t-1)
-//     phase 2t+1 : group 0 runs A(t)   group 1 runs G(t)
-// so on every SIMD (waves w and w + 4 share one) one wave keeps the matrix
-// pipe busy while the other does its softmax.  The softmax is kept short so
-// it hides under the partner's MFMAs:
-//   * Q is pre-scaled by sm_scale * log2 e and every S tile accumulates on
-//     top of s_init = -m (the MFMA's C operand), so P = exp2(S) with no
-//     per-score arithmetic;
-//   * the row max is a tree (independent max3 chains), the row sum four
-//     independent fp32 add chains (v_dot2 would stall behind the partner's
-//     MFMAs);
-//   * the running max moves only when a tile exceeds it by 2^kRescaleLog2.
-// K / V^T tiles go global -> LDS (scalar-base global_load_lds, no VALU work),
-// three buffers each, issued by each wave between the MFMAs of its G phase
-// two tiles ahead.
-// ---------------------------------------------------------------------------
-constexpr int P2_BM = 256;
-constexpr int P2_THREADS = 512;
-constexpr int P2_NBUF = 3;
-
-template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(P2_THREADS, 2) void flash_fwd_pp2(FlashParams p) {
-  using M = Mfma<T>;
-  using frag = typename M::frag;
-  using Bits = typename T::bits;
-  constexpr int BN = PP_BN;
-  constexpr int ROWB = D * 2;         // bytes per K row in LDS
-  constexpr int TILEB = BN * ROWB;    // bytes per K or V^T tile
-  constexpr int NSL = ROWB / 16;      // 16-byte slots per K row
-  constexpr int RPR = 1024 / ROWB;    // K rows per 1 KiB region
-  constexpr int NREG = TILEB / 1024;  // 1 KiB regions per tile
-  constexpr int RPW = NREG / 8;       // regions per wave per tile
-  constexpr int NDB = D / 32;         // 32-row blocks of O^T
-  constexpr int NKS = D / 16;         // k-steps of S^T
-  constexpr int NG = 2 * NKS;         // MFMA jobs per product
-  static_assert(RPW * 8 == NREG, "tile must split into 1 KiB regions per wave");
-  static_assert(BN / 16 * NDB == NG, "S and PV job counts must match");
-  static_assert(2 * RPW <= (NG + 2) / 4, "every tile load needs an issue slot");
-
-  __shared__ __attribute__((aligned(1024))) char smem[2 * P2_NBUF * TILEB];  // K0..K2 V0..V2
-
-  int b, hq, qt;
-  decode_block(p, b, hq, qt);
-  const int hkv = hq / p.group;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int group = wave >> 2;
-  const int lq = lane & 31;
-  const int h = lane >> 5;
-  const int off = p.seq_k - p.seq_q;  // bottom-right causal offset
-
-  const int q_first = qt * P2_BM;
-  const int q_last = min(p.seq_q, q_first + P2_BM) - 1;
-  int k_end = p.seq_k;
-  if (CAUSAL) k_end = max(0, min(p.seq_k, q_last + off + 1));
-  const int n_kt = (k_end + BN - 1) / BN;  // tiles the workgroup loads
-
-  const int q0 = q_first + 128 * group + 32 * (wave & 3);  // first row of this wave
-  const int qi = q0 + lq;                                  // this lane's query row
-  int wave_k_end = p.seq_k;
-  if (CAUSAL) wave_k_end = max(0, min(p.seq_k, min(q0 + 31, p.seq_q - 1) + off + 1));
-  if (q0 >= p.seq_q) wave_k_end = 0;  // no rows: no compute
-
-  // Q, pre-scaled: q <- round(q * sm_scale * log2 e), so S comes out of the
-  // MFMA in the exp2 domain (a relative perturbation of q of at most half an
-  // ulp of the 16-bit type, like the rounding of P itself).
-  frag qf[NKS];
-  {
-    const Bits* qrow = (const Bits*)p.q + b * p.q_sb + hq * p.q_sh + (int64_t)qi * p.q_ss;
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      u32x4 raw = {0u, 0u, 0u, 0u};
-      if (qi < p.seq_q) raw = *(const u32x4*)(qrow + 16 * ks + 8 * h);
-      uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float lo, hi;
-        unpack2<T>(w[i], lo, hi);
-        w[i] = (uint32_t)from_f32<T>(lo * p.scale_log2) | ((uint32_t)from_f32<T>(hi * p.scale_log2) << 16);
-      }
-      qf[ks] = __builtin_bit_cast(frag, u32x4{w[0], w[1], w[2], w[3]});
-    }
-  }
-
-  f32x16 o_acc[NDB];
-#pragma unroll
-  for (int i = 0; i < NDB; ++i)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o_acc[i][r] = 0.f;
-  // Scores are kept relative to a per-row offset m_run (log2 domain): S
-  // accumulates on top of s_init = -m_run.  m_run starts at 0 with `fresh`
-  // set (no visible key yet); it is set by the first visible tile and then
-  // raised only when a tile's max exceeds it by more than 2^kRescaleLog2.
-  float m_run = 0.f;
-  bool fresh = true;
-  float l4[4] = {0.f, 0.f, 0.f, 0.f};  // this lane's half of the row sum, 4 chains
-  f32x16 s_init;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) s_init[r] = 0.f;
-  f32x16 s[2];        // S_t (relative scores)
-  u32x4 pw[BN / 16];  // P_t packed 16-bit, the PV MFMA's B operand
-
-  // ---- tile loads: global -> LDS ---------------------------------------------
-  // Wave w fills 1 KiB regions w + 8 i of a tile; lane l of a region holds K
-  // row R * RPR + l / NSL, chunk (l % NSL) ^ swz(row) (V^T: row R * 8 + l / 8,
-  // chunk (l % 8) ^ vt_swz(row)).  Scalar-base form: the per-lane byte offset
-  // is constant, the tile base and the LDS address (M0) are scalars.
-  const char* kg = (const char*)((const Bits*)p.k + b * p.k_sb + hkv * p.k_sh);
-  const char* vg = (const char*)((const Bits*)p.vt + ((int64_t)b * p.n_kv + hkv) * D * p.sk_pad);
-  constexpr int VT_RPR = 1024 / (BN * 2);
-  auto k_row = [&](int i) { return (wave + 8 * i) * RPR + lane / NSL; };
-  auto k_col = [&](int i) { return ((lane % NSL) ^ lds_swz<D>(k_row(i))) * 8; };
-  // Offsets for a full K tile, and for the last (possibly partial) K tile of
-  // the sequence, whose rows past seq_k re-read its last row.
-  const int t_klast = (p.seq_k - 1) / BN;
-  uint32_t k_voff[RPW], k_voff_last[RPW], v_voff[RPW];  // bytes; the host keeps them below 2^32
-#pragma unroll
-  for (int i = 0; i < RPW; ++i) {
-    k_voff[i] = (uint32_t)(((int64_t)k_row(i) * p.k_ss + k_col(i)) * 2);
-    k_voff_last[i] =
-        (uint32_t)(((int64_t)min(k_row(i), p.seq_k - 1 - t_klast * BN) * p.k_ss + k_col(i)) * 2);
-    const int vrow = (wave + 8 * i) * VT_RPR + lane / 8;
-    v_voff[i] = (uint32_t)(((int64_t)vrow * p.sk_pad + ((lane % 8) ^ vt_swz(vrow)) * 8) * 2);
-  }
-  const uint32_t wave_lds = __builtin_amdgcn_readfirstlane((uint32_t)wave * 1024u);
-  const uint32_t lds_k0 = (uint32_t)(size_t)(__attribute__((address_space(3))) char*)smem;
-  const uint32_t lds_v0 = lds_k0 + P2_NBUF * TILEB;
-  auto dma = [&](const char* gbase, uint32_t voff, uint32_t la) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(la), "v"(voff), "s"(gbase) : "memory");
-  };
-  // Loads are unconditional (no branches inside the MFMA stream): a slot
-  // past the last tile re-loads the last tile into its dead buffer.
-  auto load_k = [&](int slot, int i) {  // region i of K_{min(slot, n_kt-1)} -> K buffer slot % 3
-    const int tk = min(slot, n_kt - 1);
-    const uint32_t voff = tk == t_klast ? k_voff_last[i] : k_voff[i];
-    dma(kg + (int64_t)tk * BN * p.k_ss * 2, voff, lds_k0 + (slot % P2_NBUF) * TILEB + i * 8192 + wave_lds);
-  };
-  auto load_v = [&](int slot, int i) {  // region i of V^T_{min(slot, n_kt-1)} -> V^T buffer slot % 3
-    const int tv = min(slot, n_kt - 1);
-    dma(vg + (int64_t)tv * BN * 2, v_voff[i], lds_v0 + (slot % P2_NBUF) * TILEB + i * 8192 + wave_lds);
-  };
-  // Entry e < 2 RPW of the loads a wave issues in its G phase for tile t:
-  // K_{t+2} region e, then V^T_{t+1} region e - RPW.
-  auto load_entry = [&](int t, int e) {
-    if (e < RPW) load_k(t + 2, e);
-    else load_v(t + 1, e - RPW);
-  };
-
-  // ---- LDS operand addresses --------------------------------------------------
-  // K row 32 mb + lq, chunk (2 ks + h) ^ swz(row) = 2 ks ^ (h ^ swz): one lane
-  // base XOR (ks << 5); V^T row 32 db + lq: base ^ (tt << 5).
-  const int k_lane = lq * ROWB + ((h ^ lds_swz<D>(lq)) << 4);
-  const int v_lane = lq * (BN * 2) + ((h ^ vt_swz(lq)) << 4);
-  constexpr int kPrefetch = 2;  // operand reads run this many jobs ahead
-
-  auto tile_active = [&](int t) { return t >= 0 && t < n_kt && t * BN < wave_k_end; };
-
-  // G(t): PV job g (keys 16 (g / NDB).., d-block g % NDB) of tile t-1 and S
-  // job g (k-step g / 2, key block g % 2) of tile t, alternating; DO_PV /
-  // DO_S select the halves (first / last tile).  Loads ride every 4th job.
-  auto g_phase = [&](int t, auto do_pv_tag, auto do_s_tag) {
-    constexpr bool DO_PV = decltype(do_pv_tag)::value;
-    constexpr bool DO_S = decltype(do_s_tag)::value;
-    const int kb_lane = k_lane + (t % P2_NBUF) * TILEB;                     // K_t
-    const int vb_lane = v_lane + (P2_NBUF + (t + 2) % P2_NBUF) * TILEB;     // V^T_{t-1}
-    u32x4 kfr[NG], vfr[NG];
-    auto fetch = [&](int g) {
-      if constexpr (DO_PV) {
-        const int tt = g / NDB, db = g % NDB;
-        vfr[g] = *(const u32x4*)(smem + (vb_lane ^ (tt << 5)) + 32 * db * (BN * 2));
-      }
-      if constexpr (DO_S) kfr[g] = *(const u32x4*)(smem + (kb_lane ^ ((g >> 1) << 5)) + 32 * (g & 1) * ROWB);
-    };
-#pragma unroll
-    for (int g = 0; g < kPrefetch; ++g) fetch(g);
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      if (g + kPrefetch < NG) fetch(g + kPrefetch);
-      if constexpr (DO_PV) {
-        const int tt = g / NDB, db = g % NDB;
-        o_acc[db] = M::mma(__builtin_bit_cast(frag, vfr[g]), __builtin_bit_cast(frag, pw[tt]), o_acc[db]);
-      }
-      if constexpr (DO_S)
-        s[g & 1] = M::mma(__builtin_bit_cast(frag, kfr[g]), qf[g >> 1], g < 2 ? s_init : s[g & 1]);
-      if (g % 4 == 1 && g / 4 < 2 * RPW) load_entry(t, g / 4);
-      __builtin_amdgcn_sched_barrier(0);  // keep reads kPrefetch jobs ahead
-    }
-  };
-
-  // A(t): masked softmax of S_t -> P_t.  key = kb + 32 mb + 8 (r/4) + 4 h + r % 4.
-  auto a_phase = [&](int t) {
-    const int kb = t * BN;
-    const bool need_mask = (kb + BN > p.seq_k) || (CAUSAL && kb + BN - 1 > q0 + off);
-    if (need_mask) {
-      int lim = p.seq_k - 1 - kb - 4 * h;
-      if (CAUSAL) lim = min(lim, qi + off - kb - 4 * h);
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int kl = 32 * mb + 8 * (r >> 2) + (r & 3);
-          s[mb][r] = kl <= lim ? s[mb][r] : -INFINITY;
-        }
-    }
-    // row max: four independent chains of 8, then a lane-pair exchange
-    float mq[4];
-#pragma unroll
-    for (int c4 = 0; c4 < 4; ++c4) {
-      const f32x16& v = s[c4 >> 1];
-      const int o = 8 * (c4 & 1);
-      mq[c4] = fmaxf(fmaxf(fmaxf(v[o], v[o + 1]), v[o + 2]), fmaxf(fmaxf(v[o + 3], v[o + 4]), v[o + 5]));
-      mq[c4] = fmaxf(mq[c4], fmaxf(v[o + 6], v[o + 7]));
-    }
-    const float mx = max_xor32(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3])));
-    const bool grow = fresh ? (mx != -INFINITY) : (mx > kRescaleLog2);
-    if (__any(grow)) {
-      // delta >= 0 unless fresh (then o_acc and l are still zero)
-      const float delta = fresh ? (mx == -INFINITY ? 0.f : mx) : fmaxf(mx, 0.f);
-      const float alpha = fresh ? 1.f : fast_exp2(-delta);  // fresh: nothing to scale, 2^-mx may overflow
-      m_run += delta;
-      fresh = fresh && (mx == -INFINITY);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) l4[k] *= alpha;
-#pragma unroll
-      for (int i = 0; i < NDB; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o_acc[i][r] *= alpha;
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[mb][r] -= delta;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s_init[r] = -m_run;
-    }
-    // P = exp2(S): P chunk tt (keys 16 tt..) = s[tt / 2][8 (tt % 2) + 0..7]
-#pragma unroll
-    for (int tt = 0; tt < BN / 16; ++tt)
-#pragma unroll
-      for (int j2 = 0; j2 < 4; ++j2) {
-        float pr2[2] = {fast_exp2(s[tt >> 1][8 * (tt & 1) + 2 * j2]),
-                        fast_exp2(s[tt >> 1][8 * (tt & 1) + 2 * j2 + 1])};
-        pw[tt][j2] = pack2<T>(pr2);
-        // fp32 adds, not v_dot2 on the packed pair: on gfx950 the dot2
-        // instructions do not co-execute with the partner wave's MFMAs
-        // (measured: a dot2 stream runs 2.6x slower beside an MFMA stream,
-        // an add stream ~10%).
-        l4[j2] += pr2[0] + pr2[1];
-      }
-  };
-
-  // ---- prologue: K_0, K_1, V^T_0 ------------------------------------------
-  if (n_kt > 0) {
-    // Q is in registers before any DMA is issued (the compiler's own wait for
-    // Q must not cover loads it cannot see).
-    wait_vmcnt<0>();
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) load_k(0, i);
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) load_k(1, i);
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) load_v(0, i);
-    wait_vmcnt<2 * RPW>();  // K_0 landed; K_1, V^T_0 may be in flight
-    lds_barrier();
-  }
-  const int n_phase = n_kt > 0 ? 2 * n_kt + 2 : 0;
-  for (int ph = 0; ph < n_phase; ++ph) {
-    const int t = ph >> 1;
-    if ((ph & 1) == group) {
-      __builtin_amdgcn_s_setprio(1);
-      const bool a1 = tile_active(t - 1), a0 = tile_active(t);
-      if (a1 && a0) {
-        g_phase(t, std::true_type{}, std::true_type{});
-      } else if (a1) {
-        g_phase(t, std::true_type{}, std::false_type{});
-      } else if (a0) {
-        g_phase(t, std::false_type{}, std::true_type{});
-      } else {
-#pragma unroll
-        for (int e = 0; e < 2 * RPW; ++e) load_entry(t, e);
-      }
-      __builtin_amdgcn_s_setprio(0);
-    } else {
-      const int ta = group == 0 ? t : t - 1;
-      if (tile_active(ta)) a_phase(ta);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    if (ph & 1) {
-      // Phase 2t+2 reads K_{t+1} and V^T_t, issued in this wave's G phase for
-      // tile t-1 (or the prologue); only its 2 RPW loads for tile t may still
-      // be in flight.
-      wait_vmcnt<2 * RPW>();
-    }
-    lds_barrier();
-  }
-  // No LDS-DMA may land after the workgroup has left its LDS.
-  wait_vmcnt<0>();
-
-  // Epilogue: O[qi][d] = O^T[d][qi] / l.
-  const float inv = 1.f / sum_xor32((l4[0] + l4[1]) + (l4[2] + l4[3]));
-  if (qi < p.seq_q) {
-    Bits* orow = (Bits*)p.o + b * p.o_sb + hq * p.o_sh + (int64_t)qi * p.o_ss;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const int d0 = 32 * db + 8 * rq + 4 * h;
-        uint32_t w0 = (uint32_t)from_f32<T>(o_acc[db][4 * rq + 0] * inv) |
-                      ((uint32_t)from_f32<T>(o_acc[db][4 * rq + 1] * inv) << 16);
-        uint32_t w1 = (uint32_t)from_f32<T>(o_acc[db][4 * rq + 2] * inv) |
-                      ((uint32_t)from_f32<T>(o_acc[db][4 * rq + 3] * inv) << 16);
-        *(u32x2*)(orow + d0) = u32x2{w0, w1};
-      }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// 16-bit (f16 / bf16) kernel: ping-pong over 128-key tiles.
-//
-// Same scheme as flash_fwd_pp2 (two groups of four waves alternating a G
-// phase -- PV of tile t-1 and S of tile t, now 2 x 32 MFMAs -- with an A
-// phase, the softmax of tile t) but with 128-key tiles, so every phase does
-// twice the work for the same fixed costs (the phase barrier, the LDS
-// latency before a G phase's first MFMA, the loop).  Registers: O^T 64, S
-// 64, P 32, Q 32, s_init 16 per lane.  LDS: two 32 KiB buffers each for K
-// and V^T (d_k 128).  Group 0 issues all loads of tile t+1 (K) and t (V^T)
-// early in its G phase for tile t, so they have the rest of that phase and
-// the next to land.
-// ---------------------------------------------------------------------------
-constexpr int P3_BM = 256;
-constexpr int P3_BN = 128;
-constexpr int P3_THREADS = 512;
-
-template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp3(FlashParams p) {
-  using M = Mfma<T>;
-  using frag = typename M::frag;
-  using Bits = typename T::bits;
-  constexpr int BN = P3_BN;
-  constexpr int ROWB = D * 2;          // bytes per K row in LDS
-  constexpr int VROWB = BN * 2;        // bytes per V^T row in LDS (256)
-  constexpr int TILEB = BN * ROWB;     // bytes per K or V^T tile
-  constexpr int NSL = ROWB / 16;       // 16-byte slots per K row
-  constexpr int RPR = 1024 / ROWB;     // K rows per 1 KiB region
-  constexpr int NREG = TILEB / 1024;   // 1 KiB regions per tile
-  constexpr int RPW = NREG / 4;        // regions per group-0 wave per tile (K or V^T)
-  constexpr int NDB = D / 32;          // 32-row blocks of O^T
-  constexpr int NKS = D / 16;          // k-steps of S^T
-  constexpr int NMB = BN / 32;         // 32-key blocks of S^T
-  constexpr int NG = NMB * NKS;        // MFMA jobs per product
-  static_assert(BN / 16 * NDB == NG, "S and PV job counts must match");
-  static_assert(2 * RPW <= NG / 2, "every tile load needs an issue slot");
-
-  __shared__ __attribute__((aligned(1024))) char smem[4 * TILEB];  // K0 K1 V0 V1
-
-  int b, hq, qt;
-  decode_block(p, b, hq, qt);
-  const int hkv = hq / p.group;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: phase branches are scalar
-  const int group = wave >> 2;
-  const int lq = lane & 31;
-  const int h = lane >> 5;
-  const int off = p.seq_k - p.seq_q;  // bottom-right causal offset
-
-  const int q_first = qt * P3_BM;
-  const int q_last = min(p.seq_q, q_first + P3_BM) - 1;
-  int k_end = p.seq_k;
-  if (CAUSAL) k_end = max(0, min(p.seq_k, q_last + off + 1));
-  const int n_kt = (k_end + BN - 1) / BN;  // tiles the workgroup loads
-
-  const int q0 = q_first + 128 * group + 32 * (wave & 3);  // first row of this wave
-  const int qi = q0 + lq;                                  // this lane's query row
-  int wave_k_end = p.seq_k;
-  if (CAUSAL) wave_k_end = max(0, min(p.seq_k, min(q0 + 31, p.seq_q - 1) + off + 1));
-  if (q0 >= p.seq_q) wave_k_end = 0;  // no rows: no compute
-
-  // Q pre-scaled by sm_scale * log2 e (see flash_fwd_pp2).
-  frag qf[NKS];
-  {
-    const Bits* qrow = (const Bits*)p.q + b * p.q_sb + hq * p.q_sh + (int64_t)qi * p.q_ss;
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      u32x4 raw = {0u, 0u, 0u, 0u};
-      if (qi < p.seq_q) raw = *(const u32x4*)(qrow + 16 * ks + 8 * h);
-      uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float lo, hi;
-        unpack2<T>(w[i], lo, hi);
-        w[i] = (uint32_t)from_f32<T>(lo * p.scale_log2) | ((uint32_t)from_f32<T>(hi * p.scale_log2) << 16);
-      }
-      qf[ks] = __builtin_bit_cast(frag, u32x4{w[0], w[1], w[2], w[3]});
-    }
-  }
-
-  f32x16 o_acc[NDB];
-#pragma unroll
-  for (int i = 0; i < NDB; ++i)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o_acc[i][r] = 0.f;
-  float m_run = 0.f;  // offset of the relative scores (see flash_fwd_pp2)
-  bool fresh = true;
-  float l4[4] = {0.f, 0.f, 0.f, 0.f};
-  f32x16 s_init;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) s_init[r] = 0.f;
-  f32x16 s[NMB];      // S_t (relative scores)
-  u32x4 pw[BN / 16];  // P_t packed 16-bit
-
-  // ---- tile loads (group 0 only, scalar-base LDS-DMA) ------------------------
-  // K: region R holds rows R * RPR + l / NSL, slot l % NSL = chunk (l % NSL) ^
-  // swz(row).  V^T: region R holds rows 4 R + l / 16 (256-byte rows), slot
-  // l % 16 = chunk (l % 16) ^ swz128(row).  Wave w of group 0 fills regions
-  // w + 4 i; the swizzle term does not depend on i, so one lane offset per
-  // tensor serves every region and the region step goes into the scalar base.
-  // K is read through a buffer resource whose size stops at the last key the
-  // workgroup uses: rows past it read as zeros (and are masked), with no
-  // per-lane clamp.  V^T tiles always lie inside the padded workspace.
-  const char* kg = (const char*)((const Bits*)p.k + b * p.k_sb + hkv * p.k_sh);
-  const char* vg = (const char*)((const Bits*)p.vt + ((int64_t)b * p.n_kv + hkv) * D * p.sk_pad);
-  const int wq = wave & 3;
-  const int k_row0 = wq * RPR + lane / NSL;  // row of region wq; region wq + 4 i adds 4 i RPR
-  const uint32_t k_voff = (uint32_t)(((int64_t)k_row0 * p.k_ss + ((lane % NSL) ^ lds_swz<D>(k_row0)) * 8) * 2);
-  const int v_row0 = 4 * wq + lane / 16;
-  const uint32_t v_voff =
-      (uint32_t)(((int64_t)v_row0 * p.sk_pad + ((lane % 16) ^ lds_swz<128>(v_row0)) * 8) * 2);
-  const uint32_t wave_lds = __builtin_amdgcn_readfirstlane((uint32_t)wq * 1024u);
-  const uint32_t lds_k0 = (uint32_t)(size_t)(__attribute__((address_space(3))) char*)smem;
-  const uint32_t lds_v0 = lds_k0 + 2 * TILEB;
-  const int k_rows = min(p.seq_k, n_kt * BN);  // keys the workgroup reads
-  const uint32_t k_ss2 = (uint32_t)p.k_ss * 2u;
-  const uint32_t k_step = 4u * RPR * k_ss2;                // bytes of 4 regions of K rows
-  const uint32_t v_step = 16u * (uint32_t)p.sk_pad * 2u;  // bytes of 16 V^T rows
-  auto dma = [&](const i32x4& rsrc, uint32_t voff, uint32_t la) __attribute__((always_inline)) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(la), "v"(voff), "s"(rsrc)
-                 : "memory");
-  };
-  auto rsrc_of = [&](const char* base, uint32_t bytes) __attribute__((always_inline)) {
-    const uint64_t a = (uint64_t)(uintptr_t)base;
-    // every word wave-uniform, so the resource stays in SGPRs
-    return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
-                 __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu)),
-                 __builtin_amdgcn_readfirstlane((int)bytes), kBufRsrcWord3};
-  };
-  // One resource per tile, built once per phase; the region offset goes into
-  // the (range-checked) lane offset.  K rows past k_rows read as zeros and
-  // cost no traffic; nothing is read for V^T tiles past the last one.
-  auto k_rsrc = [&](int tk) __attribute__((always_inline)) {
-    const int rows = min(max(k_rows - tk * BN, 0), BN);
-    return rsrc_of(kg + (int64_t)tk * BN * k_ss2, (uint32_t)rows * k_ss2);
-  };
-  auto v_rsrc = [&](int tv) __attribute__((always_inline)) {
-    return rsrc_of(vg + (int64_t)tv * BN * 2, tv < n_kt ? (uint32_t)D * (uint32_t)p.sk_pad * 2u : 0u);
-  };
-  // Regions wq + 4 i of a K tile (tile rows 4 i RPR ..) into K buffer `buf`.
-  auto load_k = [&](const i32x4& rs, int buf, int i) __attribute__((always_inline)) {
-    dma(rs, k_voff + (uint32_t)i * k_step, lds_k0 + buf * TILEB + i * 4096 + wave_lds);
-  };
-  // Regions wq + 4 i of a V^T tile (rows 16 i ..) into V^T buffer `buf`.
-  auto load_v = [&](const i32x4& rs, int buf, int i) __attribute__((always_inline)) {
-    dma(rs, v_voff + (uint32_t)i * v_step, lds_v0 + buf * TILEB + i * 4096 + wave_lds);
-  };
-
-  // ---- LDS operand addresses -------------------------------------------------
-  const int k_lane = lq * ROWB + ((h ^ lds_swz<D>(lq)) << 4);
-  const int v_lane = lq * VROWB + ((h ^ lds_swz<128>(lq)) << 4);
-  constexpr int kPrefetch = 2;
-  static_assert(NMB == 4, "S jobs are ordered for four key blocks");
-  constexpr auto s_mb = [](int g) { return 2 * (g / (2 * NKS)) + (g & 1); };
-  constexpr auto s_ks = [](int g) { return (g % (2 * NKS)) >> 1; };
-
-  // G(t): job g = PV job g of tile t-1 (keys 16 (g / NDB).., d-block g % NDB)
-  // and S job g of tile t.  S jobs fill key blocks in pairs (0 1, then 2 3),
-  // alternating the pair, so only half of S is live while the first half of
-  // P is consumed.  Every G phase runs both products: the P of a tile a wave
-  // does not use is zero (its PV adds nothing) and the S of such a tile is
-  // never read, which keeps one straight-line MFMA stream per group.  Group 0
-  // issues, one every other job, the loads of K_{t+1} and then V^T_t.
-  auto g_phase = [&](int t, auto dma_tag) __attribute__((always_inline)) {
-    constexpr bool DO_DMA = decltype(dma_tag)::value;
-    i32x4 rk = {0, 0, 0, 0}, rv = {0, 0, 0, 0};
-    if constexpr (DO_DMA) {
-      rk = k_rsrc(t + 1);
-      rv = v_rsrc(t);
-    }
-    int kb_lane = k_lane + (t & 1) * TILEB;               // K_t
-    int vb_lane = v_lane + (2 + ((t + 1) & 1)) * TILEB;  // V^T_{t-1}
-    // Opaque per phase, so the per-job addresses are formed in the job that
-    // uses them instead of being hoisted and kept live across the loop.
-    asm volatile("" : "+v"(kb_lane), "+v"(vb_lane));
-    u32x4 kfr[NG], vfr[NG];
-    auto fetch = [&](int g) __attribute__((always_inline)) {
-      const int tt = g / NDB, db = g % NDB;
-      vfr[g] = *(const u32x4*)(smem + (vb_lane ^ (tt << 5)) + 32 * db * VROWB);
-      const int ks = s_ks(g), mb = s_mb(g);
-      kfr[g] = *(const u32x4*)(smem + (kb_lane ^ (ks << 5)) + 32 * mb * ROWB);
-    };
-    __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-    for (int g = 0; g < kPrefetch; ++g) fetch(g);
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      if (g + kPrefetch < NG) fetch(g + kPrefetch);
-      {
-        const int tt = g / NDB, db = g % NDB;
-        o_acc[db] = M::mma(__builtin_bit_cast(frag, vfr[g]), __builtin_bit_cast(frag, pw[tt]), o_acc[db]);
-      }
-      {
-        const int ks = s_ks(g), mb = s_mb(g);
-        s[mb] = M::mma(__builtin_bit_cast(frag, kfr[g]), qf[ks], ks == 0 ? s_init : s[mb]);
-      }
-      if constexpr (DO_DMA) {
-        if (g % 2 == 1 && g / 2 < RPW) load_k(rk, (t + 1) & 1, g / 2);
-        if (g % 2 == 1 && g / 2 >= RPW && g / 2 < 2 * RPW) load_v(rv, t & 1, g / 2 - RPW);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    __builtin_amdgcn_s_setprio(0);
-    __builtin_amdgcn_sched_barrier(0);
-  };
-
-  // A(t): masked softmax of S_t -> P_t.  key = kb + 32 mb + 8 (r/4) + 4 h + r % 4.
-  // A tile the wave does not use yields P = 0.
-  auto a_phase = [&](int t) __attribute__((always_inline)) {
-    const int kb = t * BN;
-    if (t >= n_kt || kb >= wave_k_end) {
-#pragma unroll
-      for (int tt = 0; tt < BN / 16; ++tt) pw[tt] = u32x4{0u, 0u, 0u, 0u};
-      __builtin_amdgcn_sched_barrier(0);
-      return;
-    }
-    const bool need_mask = (kb + BN > p.seq_k) || (CAUSAL && kb + BN - 1 > q0 + off);
-    if (need_mask) {
-      int lim = p.seq_k - 1 - kb - 4 * h;
-      if (CAUSAL) lim = min(lim, qi + off - kb - 4 * h);
-#pragma unroll
-      for (int mb = 0; mb < NMB; ++mb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int kl = 32 * mb + 8 * (r >> 2) + (r & 3);
-          s[mb][r] = kl <= lim ? s[mb][r] : -INFINITY;
-        }
-    }
-    float mq[NMB];
-#pragma unroll
-    for (int mb = 0; mb < NMB; ++mb) {
-      const f32x16& v = s[mb];
-      float a = fmaxf(fmaxf(fmaxf(v[0], v[1]), v[2]), fmaxf(fmaxf(v[3], v[4]), v[5]));
-      float c2 = fmaxf(fmaxf(fmaxf(v[8], v[9]), v[10]), fmaxf(fmaxf(v[11], v[12]), v[13]));
-      a = fmaxf(a, fmaxf(v[6], v[7]));
-      c2 = fmaxf(c2, fmaxf(v[14], v[15]));
-      mq[mb] = fmaxf(a, c2);
-    }
-    float mxl = mq[0];
-#pragma unroll
-    for (int mb = 1; mb < NMB; ++mb) mxl = fmaxf(mxl, mq[mb]);
-    const float mx = max_xor32(mxl);
-    const bool grow = fresh ? (mx != -INFINITY) : (mx > kRescaleLog2);
-    if (__any(grow)) {
-      const float delta = fresh ? (mx == -INFINITY ? 0.f : mx) : fmaxf(mx, 0.f);
-      const float alpha = fresh ? 1.f : fast_exp2(-delta);  // fresh: nothing to scale, 2^-mx may overflow
-      m_run += delta;
-      fresh = fresh && (mx == -INFINITY);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) l4[k] *= alpha;
-#pragma unroll
-      for (int i = 0; i < NDB; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o_acc[i][r] *= alpha;
-#pragma unroll
-      for (int mb = 0; mb < NMB; ++mb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[mb][r] -= delta;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s_init[r] = -m_run;
-    }
-    // P chunk tt (keys 16 tt..) = s[tt / 2][8 (tt % 2) + 0..7]; fp32 row sums
-    // (v_dot2 does not co-execute with the partner's MFMAs).
-#pragma unroll
-    for (int tt = 0; tt < BN / 16; ++tt)
-#pragma unroll
-      for (int j2 = 0; j2 < 4; ++j2) {
-        float pr2[2] = {fast_exp2(s[tt >> 1][8 * (tt & 1) + 2 * j2]),
-                        fast_exp2(s[tt >> 1][8 * (tt & 1) + 2 * j2 + 1])};
-        pw[tt][j2] = pack2<T>(pr2);
-        l4[j2] += pr2[0] + pr2[1];
-      }
-    __builtin_amdgcn_sched_barrier(0);
-  };
-
-  // ---- prologue ----------------------------------------------------------------
-  // K_0 by all eight waves.  P and the V^T buffer the first PV products (of
-  // tile -1) read start as zeros, so those products add nothing.
-#pragma unroll
-  for (int tt = 0; tt < BN / 16; ++tt) pw[tt] = u32x4{0u, 0u, 0u, 0u};
-  if (n_kt > 0) {
-#pragma unroll
-    for (int i = tid; i < TILEB / 16; i += P3_THREADS) *(u32x4*)(smem + 3 * TILEB + 16 * i) = u32x4{0u, 0u, 0u, 0u};
-    wait_vmcnt<0>();  // Q is in registers before any DMA is issued
-#pragma unroll
-    for (int i = group; i < RPW; i += 2) load_k(k_rsrc(0), 0, i);  // regions wq + 4 i, split by group
-    wait_vmcnt<0>();
-    lds_barrier();
-  }
-  // Phases 2t (group 0: G(t), group 1: A(t-1)) and 2t+1 (group 0: A(t),
-  // group 1: G(t)) for t = 0 .. n_kt.  One loop per group keeps S and P
-  // from both being live across the loop edge.  Phase 2t+2 reads K_{t+1} and
-  // V^T_t, which group 0 issued during phase 2t and waits for at the end of
-  // phase 2t+1.
-  if (n_kt > 0) {
-    if (group == 0) {
-      for (int t = 0; t <= n_kt; ++t) {
-        g_phase(t, std::true_type{});
-        lds_barrier();
-        a_phase(t);
-        wait_vmcnt<0>();
-        lds_barrier();
-      }
-    } else {
-      lds_barrier();  // phase 0: nothing to do (A of tile -1)
-      g_phase(0, std::false_type{});
-      lds_barrier();
-      for (int t = 1; t <= n_kt; ++t) {
-        a_phase(t - 1);
-        lds_barrier();
-        g_phase(t, std::false_type{});
-        lds_barrier();
-      }
-    }
-  }
-  wait_vmcnt<0>();  // no LDS-DMA may land after the workgroup has left its LDS
-
-  // Epilogue: O[qi][d] = O^T[d][qi] / l.
-  const float inv = 1.f / sum_xor32((l4[0] + l4[1]) + (l4[2] + l4[3]));
-  if (qi < p.seq_q) {
-    Bits* orow = (Bits*)p.o + b * p.o_sb + hq * p.o_sh + (int64_t)qi * p.o_ss;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const int d0 = 32 * db + 8 * rq + 4 * h;
-        uint32_t w0 = (uint32_t)from_f32<T>(o_acc[db][4 * rq + 0] * inv) |
-                      ((uint32_t)from_f32<T>(o_acc[db][4 * rq + 1] * inv) << 16);
-        uint32_t w1 = (uint32_t)from_f32<T>(o_acc[db][4 * rq + 2] * inv) |
-                      ((uint32_t)from_f32<T>(o_acc[db][4 * rq + 3] * inv) << 16);
-        *(u32x2*)(orow + d0) = u32x2{w0, w1};
-      }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// 16-bit kernel, persistent: flash_fwd_pp3's phases, one workgroup per CU
-// walking a static list of query tiles.
+// Persistence: one workgroup per CU walks a static list of query tiles.
 //
 // Tiles (b, hq, qt) form n_queues lists -- one per XCD when the (batch, kv
 // head) units divide by 8, so that the K/V tiles a list reads stay in one
@@ -1652,11 +258,11 @@ __device__ __forceinline__ int sched_rank(const FlashParams& p, int j, int r) {
 }
 
 template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp4(FlashParams p) {
+__global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
   using M = Mfma<T>;
   using frag = typename M::frag;
   using Bits = typename T::bits;
-  constexpr int BN = P3_BN;
+  constexpr int BN = K16_BN;
   constexpr int ROWB = D * 2;          // bytes per K / Q row in LDS
   constexpr int VROWB = BN * 2;        // bytes per V^T row in LDS (256)
   constexpr int TILEB = BN * ROWB;     // bytes per K, V^T or 128-row Q tile
@@ -1670,7 +276,7 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp4(FlashParams p) {
   constexpr int NG = NMB * NKS;        // MFMA jobs per product
   static_assert(BN / 16 * NDB == NG, "S and PV job counts must match");
   static_assert(2 * RPW <= NG / 2, "every tile load needs an issue slot");
-  static_assert(BN == 128 && P3_BM == 256, "a group's 128 Q rows fill one K-sized buffer");
+  static_assert(BN == 128 && K16_BM == 256, "a group's 128 Q rows fill one K-sized buffer");
 
   // K0 K1 V0 V1 Qn (group 0's next Q rows)
   __shared__ __attribute__((aligned(1024))) char smem[5 * TILEB];
@@ -1725,7 +331,7 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp4(FlashParams p) {
   auto make_tile = [&](int rank) __attribute__((always_inline)) {
     Tile tl;
     decode_tile(p, queue, rank, tl.b, tl.hq, tl.qt);
-    const int q_last = min(p.seq_q, tl.qt * P3_BM + P3_BM) - 1;
+    const int q_last = min(p.seq_q, tl.qt * K16_BM + K16_BM) - 1;
     int k_end = p.seq_k;
     if (CAUSAL) k_end = max(0, min(p.seq_k, q_last + off + 1));
     tl.n_kt = (k_end + BN - 1) / BN;             // K tiles the workgroup loads
@@ -1757,7 +363,7 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp4(FlashParams p) {
   };
   // Q rows [128 g, 128 g + 128) of a tile (rows past seq_q read as zeros).
   auto q_rsrc = [&](const Tile& tl, int g) __attribute__((always_inline)) {
-    const int r0 = tl.qt * P3_BM + 128 * g;
+    const int r0 = tl.qt * K16_BM + 128 * g;
     const int rows = min(max(p.seq_q - r0, 0), 128);
     const char* qg = (const char*)((const Bits*)p.q + tl.b * p.q_sb + tl.hq * p.q_sh + (int64_t)r0 * p.q_ss);
     return rsrc_of(qg, (uint32_t)rows * q_ss2);
@@ -1796,7 +402,7 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp4(FlashParams p) {
     const uint32_t kvo = kq_off(ln, p.k_ss);
 #pragma unroll
     for (int i = group; i < RPW; i += 2) dma(rk, kvo + (uint32_t)i * k_step, lds_k0 + kb * TILEB + i * 4096 + wave_lds);
-    const int qi = tl.qt * P3_BM + 128 * group + 32 * wq + (ln & 31);
+    const int qi = tl.qt * K16_BM + 128 * group + 32 * wq + (ln & 31);
     const Bits* qrow = (const Bits*)p.q + tl.b * p.q_sb + tl.hq * p.q_sh + (int64_t)min(qi, p.seq_q - 1) * p.q_ss;
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
@@ -1825,7 +431,7 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp4(FlashParams p) {
     const int nrank = sched_rank(p, mach, r + 1);
     const bool has_next = nrank < p.q_tiles;
     const int n_kt = cur.n_kt;
-    const int q0 = cur.qt * P3_BM + 128 * group + 32 * wq;  // first row of this wave
+    const int q0 = cur.qt * K16_BM + 128 * group + 32 * wq;  // first row of this wave
     int wave_k_end = p.seq_k;
     if (CAUSAL) wave_k_end = max(0, min(p.seq_k, min(q0 + 31, p.seq_q - 1) + off + 1));
     if (q0 >= p.seq_q) wave_k_end = 0;  // no rows: no compute
@@ -1841,9 +447,15 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp4(FlashParams p) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) l4[k] = 0.f;
 
-    // G(t): PV job g of tile t-1 (none for t = 0) and S job g of tile t, as
-    // flash_fwd_pp3.  Group 0 loads, one every other job, K_{t+1} then V^T_t
-    // -- for t = n_kt the next tile's K_0 and group 1's next Q rows instead.
+    // G(t): job g = PV job g of tile t-1 (keys 16 (g / NDB).., d-block
+    // g % NDB; none for t = 0) and S job g of tile t.  S jobs fill key blocks
+    // in pairs (0 1, then 2 3), alternating the pair, so only half of S is
+    // live while the first half of P is consumed.  Every G phase runs both
+    // products: the P of a tile a wave does not use is zero (its PV adds
+    // nothing) and the S of such a tile is never read, which keeps one
+    // straight-line MFMA stream per group.  Group 0 loads, one every other
+    // job, K_{t+1} then V^T_t -- for t = n_kt the next tile's K_0 and group
+    // 1's next Q rows instead.
     auto g_phase = [&](int t, auto dma_tag, auto pv_tag) __attribute__((always_inline)) {
       constexpr bool DO_DMA = decltype(dma_tag)::value;
       constexpr bool DO_PV = decltype(pv_tag)::value;
@@ -1907,7 +519,8 @@ __global__ __launch_bounds__(P3_THREADS, 2) void flash_fwd_pp4(FlashParams p) {
       __builtin_amdgcn_sched_barrier(0);
     };
 
-    // A(t): masked softmax of S_t -> P_t, as flash_fwd_pp3.
+    // A(t): masked softmax of S_t -> P_t.  key = kb + 32 mb + 8 (r/4) + 4 h + r % 4;
+    // a tile the wave does not use yields P = 0.
     auto a_phase = [&](int t) __attribute__((always_inline)) {
       const int kb = t * BN;
       if (t >= n_kt || kb >= wave_k_end) {
@@ -2393,7 +1006,7 @@ int device_cus() {
 template <typename T, int D>
 int launch_flash_16(FlashParams& p, void* ws, bool causal, hipStream_t st) {
   p.vt = ws;
-  p.n_qt = (p.seq_q + P3_BM - 1) / P3_BM;
+  p.n_qt = (p.seq_q + K16_BM - 1) / K16_BM;
   // Tile lists: one per XCD when the (batch, kv head) units split evenly.
   const int units = p.batch * p.n_kv;
   p.n_queues = units % 8 == 0 ? 8 : 1;
@@ -2409,9 +1022,9 @@ int launch_flash_16(FlashParams& p, void* ws, bool causal, hipStream_t st) {
   if (e) return e;
   dim3 grid((unsigned)(p.q_machines * p.n_queues));
   if (causal)
-    hipLaunchKernelGGL((flash_fwd_pp4<T, D, true>), grid, dim3(P3_THREADS), 0, st, p);
+    hipLaunchKernelGGL((flash_fwd_16<T, D, true>), grid, dim3(K16_THREADS), 0, st, p);
   else
-    hipLaunchKernelGGL((flash_fwd_pp4<T, D, false>), grid, dim3(P3_THREADS), 0, st, p);
+    hipLaunchKernelGGL((flash_fwd_16<T, D, false>), grid, dim3(K16_THREADS), 0, st, p);
   return tl_launch_status();
 }
 
