@@ -217,12 +217,13 @@ __device__ __forceinline__ void lds_barrier() {
 // number of rounds the first three use a balanced-triple order whose rank
 // sums differ by at most one.
 //
-// Tile switches do not wait for memory: during a tile's last G phase group 0
-// loads the next tile's first K tile (into the K buffer the next tile starts
-// from) and group 1's next Q rows (into the V^T buffer no later phase reads);
-// group 1 loads group 0's next Q rows into a fifth LDS buffer early in the
-// tile.  At the switch each wave copies its next Q from LDS, while the
-// finished tile's output stores drain in the background.
+// Tile switches do not wait for memory.  The last G step, G(n_kt), only
+// finishes the PV of the last key tile (no S), so K_{n_kt} is never loaded:
+// in G(n_kt - 1) group 0 loads its own next Q rows into that K buffer, and
+// in G(n_kt) the next tile's first K tile (into the K buffer the next tile
+// starts from) and group 1's next Q rows (into the V^T buffer no later step
+// reads).  At the switch each wave copies its next Q from LDS, then stages
+// its output in the same buffer; the output stores drain in the background.
 // ---------------------------------------------------------------------------
 // The lane index, read afresh at each use (an opaque read that cannot be
 // hoisted), so that lane-derived offsets are recomputed where they are used
@@ -278,8 +279,8 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
   static_assert(2 * RPW <= NG / 2, "every tile load needs an issue slot");
   static_assert(BN == 128 && K16_BM == 256, "a group's 128 Q rows fill one K-sized buffer");
 
-  // K0 K1 V0 V1 Qn (group 0's next Q rows)
-  __shared__ __attribute__((aligned(1024))) char smem[5 * TILEB];
+  // K0 K1 V0 V1 (128 KiB at d_k 128)
+  __shared__ __attribute__((aligned(1024))) char smem[4 * TILEB];
 
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);  // wave-uniform: phase branches are scalar
   const int group = wave >> 2;
@@ -316,7 +317,6 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
   const uint32_t wave_lds = __builtin_amdgcn_readfirstlane((uint32_t)wq * 1024u);
   const uint32_t lds_k0 = (uint32_t)(size_t)(__attribute__((address_space(3))) char*)smem;
   const uint32_t lds_v0 = lds_k0 + 2 * TILEB;
-  const uint32_t lds_qn = lds_k0 + 4 * TILEB;
   const uint32_t k_ss2 = (uint32_t)p.k_ss * 2u;
   const uint32_t q_ss2 = (uint32_t)p.q_ss * 2u;
   const uint32_t k_step = 4u * RPR * k_ss2;                // bytes of 4 regions of K rows
@@ -456,27 +456,40 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
     // straight-line MFMA stream per group.  Group 0 loads, one every other
     // job, K_{t+1} then V^T_t -- for t = n_kt the next tile's K_0 and group
     // 1's next Q rows instead.
-    auto g_phase = [&](int t, auto dma_tag, auto pv_tag) __attribute__((always_inline)) {
+    auto g_phase = [&](int t, auto dma_tag, auto pv_tag, auto s_tag) __attribute__((always_inline)) {
       constexpr bool DO_DMA = decltype(dma_tag)::value;
       constexpr bool DO_PV = decltype(pv_tag)::value;
+      constexpr bool DO_S = decltype(s_tag)::value;
       const int ln = fresh_lane();
       i32x4 rk = {0, 0, 0, 0}, rv = {0, 0, 0, 0};
-      uint32_t kvo = 0, vvo = 0, vstep = v_step;
+      uint32_t kvo = 0, vvo = 0, kstep = k_step, vstep = v_step;
       if constexpr (DO_DMA) {
-        kvo = kq_off(ln, p.k_ss);
-        if (t < n_kt) {
+        // K slot: K_{t+1}; at t = n_kt - 1 group 0's next Q rows (K_{n_kt}
+        // is never used: G(n_kt) computes no S); at t = n_kt the next K_0.
+        // V slot: V^T_t; at t = n_kt group 1's next Q rows.
+        const Tile nxt = make_tile(has_next ? nrank : rank);
+        const i32x4 none = rsrc_of(cur.kg, 0u);
+        if (t < n_kt - 1) {
           rk = k_rsrc(cur, t + 1);
+          kvo = kq_off(ln, p.k_ss);
+        } else if (t == n_kt - 1) {
+          rk = has_next ? q_rsrc(nxt, 0) : none;
+          kvo = kq_off(ln, p.q_ss);
+          kstep = q_step;
+        } else {
+          rk = has_next ? k_rsrc(nxt, 0) : none;
+          kvo = kq_off(ln, p.k_ss);
+        }
+        if (t < n_kt) {
           rv = v_rsrc(cur, t);
           vvo = v_off(ln);
         } else {
-          const Tile nxt = make_tile(has_next ? nrank : rank);
-          rk = has_next ? k_rsrc(nxt, 0) : rsrc_of(cur.kg, 0u);
-          rv = has_next ? q_rsrc(nxt, 1) : rsrc_of(cur.kg, 0u);
+          rv = has_next ? q_rsrc(nxt, 1) : none;
           vvo = kq_off(ln, p.q_ss);
           vstep = q_step;
         }
       }
-      const int kbuf = (tb + t + 1) & 1;  // K_{t+1} (or the next K_0)
+      const int kbuf = (tb + t + 1) & 1;  // K_{t+1} (or a next Q / K_0)
       const int vbuf = (tb + t) & 1;      // V^T_t (or group 1's next Q)
       int kb_lane = k_lane_of(ln) + ((tb + t) & 1) * TILEB;              // K_t
       int vb_lane = v_lane_of(ln) + (2 + ((tb + t + 1) & 1)) * TILEB;   // V^T_{t-1}
@@ -486,8 +499,10 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
           const int tt = g / NDB, db = g % NDB;
           vfr[g] = *(const u32x4*)(smem + (vb_lane ^ (tt << 5)) + 32 * db * VROWB);
         }
-        const int ks = s_ks(g), mb = s_mb(g);
-        kfr[g] = *(const u32x4*)(smem + (kb_lane ^ (ks << 5)) + 32 * mb * ROWB);
+        if constexpr (DO_S) {
+          const int ks = s_ks(g), mb = s_mb(g);
+          kfr[g] = *(const u32x4*)(smem + (kb_lane ^ (ks << 5)) + 32 * mb * ROWB);
+        }
       };
       __builtin_amdgcn_s_setprio(1);
 #pragma unroll
@@ -499,14 +514,14 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
           const int tt = g / NDB, db = g % NDB;
           o_acc[db] = M::mma(__builtin_bit_cast(frag, vfr[g]), __builtin_bit_cast(frag, pw[tt]), o_acc[db]);
         }
-        {
+        if constexpr (DO_S) {
           const int ks = s_ks(g), mb = s_mb(g);
           s[mb] = M::mma(__builtin_bit_cast(frag, kfr[g]), qf[ks], ks == 0 ? s_init : s[mb]);
         }
         if constexpr (DO_DMA) {
           if (g % 2 == 1 && g / 2 < RPW) {
             const int i = g / 2;
-            dma(rk, kvo + (uint32_t)i * k_step, lds_k0 + kbuf * TILEB + i * 4096 + wave_lds);
+            dma(rk, kvo + (uint32_t)i * kstep, lds_k0 + kbuf * TILEB + i * 4096 + wave_lds);
           }
           if (g % 2 == 1 && g / 2 >= RPW && g / 2 < 2 * RPW) {
             const int i = g / 2 - RPW;
@@ -597,33 +612,33 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
     // not forced to alternate; G phases run at raised priority, so the MFMA
     // work of one group overlaps the other's softmax. -------------------------------
     if (n_kt > 0) {
+      using Y = std::true_type;
+      using N = std::false_type;
       if (group == 0) {
-        g_phase(0, std::true_type{}, std::false_type{});
+        g_phase(0, Y{}, N{}, Y{});
         a_phase(0);
         wait_vmcnt<0>();
         lds_barrier();
-        for (int t = 1; t <= n_kt; ++t) {
-          g_phase(t, std::true_type{}, std::true_type{});
+        for (int t = 1; t < n_kt; ++t) {
+          g_phase(t, Y{}, Y{}, Y{});
           a_phase(t);
           wait_vmcnt<0>();
           lds_barrier();
         }
-      } else {
-        g_phase(0, std::false_type{}, std::false_type{});
+        g_phase(n_kt, Y{}, Y{}, N{});  // PV of the last tile; no S
+        wait_vmcnt<0>();
         lds_barrier();
-        // Group 0's next Q rows into the fifth buffer (read only at the switch).
-        if (has_next) {
-          const i32x4 rq = q_rsrc(make_tile(nrank), 0);
-          const uint32_t qvo = kq_off(fresh_lane(), p.q_ss);
-#pragma unroll
-          for (int i = 0; i < RPW; ++i) dma(rq, qvo + (uint32_t)i * q_step, lds_qn + i * 4096 + wave_lds);
-        }
-        for (int t = 1; t <= n_kt; ++t) {
+      } else {
+        g_phase(0, N{}, N{}, Y{});
+        lds_barrier();
+        for (int t = 1; t < n_kt; ++t) {
           a_phase(t - 1);
-          g_phase(t, std::false_type{}, std::true_type{});
-          if (t == n_kt) wait_vmcnt<0>();
+          g_phase(t, N{}, Y{}, Y{});
           lds_barrier();
         }
+        a_phase(n_kt - 1);
+        g_phase(n_kt, N{}, Y{}, N{});
+        lds_barrier();
       }
     }
 
@@ -638,8 +653,9 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
     const float inv = 1.f / sum_xor32((l4[0] + l4[1]) + (l4[2] + l4[3]));
     const int ntb = (tb + n_kt + 1) & 1;  // where the next K_0 went
     const Tile nxt = make_tile(has_next ? nrank : rank);
-    // group 0's next Q rows are in the fifth buffer, group 1's in V^T buffer (tb + n_kt) & 1
-    const int qbuf = group == 0 ? 4 * TILEB : (2 + ((tb + n_kt) & 1)) * TILEB;
+    // the next Q rows: group 0's in K buffer (tb + n_kt) & 1, group 1's in
+    // V^T buffer (tb + n_kt) & 1; each group stages its output there too
+    const int qbuf = (group == 0 ? 0 : 2 * TILEB) + ((tb + n_kt) & 1) * TILEB;
     if (has_next) {
       if (n_kt > 0) {
         const int ql = qbuf + 32 * wq * ROWB + k_lane_of(fresh_lane());
@@ -674,6 +690,7 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
         if (q0 + rr < p.seq_q) *(u32x4*)(obase + (int64_t)(q0 + rr) * p.o_ss + 8 * cc) = val;
       }
     }
+    lds_barrier();  // the staging buffers are reused by the next tile's first loads
     if (!has_next) break;
     cur = nxt;
     rank = nrank;
