@@ -40,9 +40,11 @@ def test_workspace_queries():
     assert lib.tl_attention_fwd_workspace_bytes(2, 3, 100, 64, _lib.DTYPE_F16) == 2 * 3 * 64 * 128 * 2
     assert lib.tl_attention_fwd_workspace_bytes(1, 1, 100, 32, _lib.DTYPE_BF16) == 0  # generic path
     split = lib.tl_decode_split_size(64, 8, 16384)
-    assert split % 16 == 0 and 64 <= split <= 2048
+    assert split % 16 == 0 and 64 <= split <= 4096
+    assert lib.tl_decode_split_size(8, 12, 1024) == 64  # short caches: one-iteration floor
     ws = lib.tl_attention_decode_workspace_bytes(64, 24, 16384, 128, split)
-    rows = 64 * 24 * ((16384 + split - 1) // split)
+    # A (sequence, head) spans at most ceil(max_ctx / split) + 1 workgroup shares.
+    rows = 64 * 24 * ((16384 + split - 1) // split + 1)
     assert ws >= rows * (128 + 2) * 4
     assert lib.tl_attention_decode_workspace_bytes(0, 24, 16384, 128, split) == 0
 

@@ -115,3 +115,19 @@ def test_decode_split_sizes_agree(split):
     data = oi.make_decode(cfg, fill="nan")
     got, exp, _, _ = run_decode_step(cfg, data, split=split)
     compare(f"split{split}", got, exp, TOL[cfg.dtype])
+
+
+@pytest.mark.parametrize("cus,batch", [(1, 70), (3, 9), (7, 66)])
+def test_decode_few_workgroups_span_many_sequences(monkeypatch, cus, batch):
+    """Capping the device at a few compute units leaves a handful of
+    workgroups, so each share crosses many (sequence, head) pairs and most
+    pairs are split between two shares; batches above 64 take the lengths
+    scan in several chunks.  Some sequences hold only the appended token, one
+    fills the cache."""
+    monkeypatch.setenv("TRITON_LLM_HIP_MAX_CUS", str(cus))
+    cfg = oi.scaled(oi.CONFIGS["4"], batch=batch, max_ctx=640, lo=0, hi=639)
+    lens = oi.draw_lens(cfg)
+    lens[: min(4, batch)] = [0, 639, 1, 0][: min(4, batch)]
+    data = oi.make_decode(cfg, fill="nan", lens=lens)
+    got, exp, _, _ = run_decode_step(cfg, data, split=16)
+    compare(f"cus{cus} b{batch}", got, exp, TOL[cfg.dtype])

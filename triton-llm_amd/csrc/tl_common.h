@@ -127,3 +127,8 @@ static inline int tl_launch_status() { return (int)hipGetLastError(); }
 
 // Resolve the stream argument of an entry point: NULL means the library stream.
 hipStream_t tl_resolve_stream(void* stream);
+
+// Compute units of the current device (cached per device), capped by the
+// environment variable TRITON_LLM_HIP_MAX_CUS when set (tests use it to force
+// multi-round schedules on small problems).
+int tl_device_cus();

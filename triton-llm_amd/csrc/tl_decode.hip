@@ -4,9 +4,20 @@
 // Reference behaviour being replaced: per decode step the reference runs
 // attention_gqa(q, K[:L], V[:L], causal=False) (smollm2_triton/model.py:310-314)
 // whose kernel (attention_gqa.py:21-146) launches one program per query head,
-// re-reading each KV head once per query head of its group.  Here one
-// workgroup owns (sequence b, KV head, split of the positions) and serves all
-// G query heads of that KV head from a single pass over K/V.
+// re-reading each KV head once per query head of its group.  Here a
+// workgroup streams K/V rows of one KV head and serves all G query heads of
+// it (up to 8; larger groups run as several pairs of the same KV head), so
+// each K/V byte is read once.
+//
+// Work partition.  The cached positions of every (sequence, pair) stream are
+// laid end to end and cut into equal shares, one per workgroup, with exactly
+// as many workgroups as the device holds at once.  Every workgroup therefore
+// streams the same number of bytes whatever the sequence lengths are, and no
+// second round of workgroups is left to straggle.  (A grid of one workgroup
+// per (sequence, head, fixed-size split) leaves the late splits of long
+// sequences running alone, and measured 6.1 TB/s where the equal shares
+// reach 6.5 TB/s.)  A share may end inside one pair and continue into the
+// next; each piece is a segment with its own softmax state.
 //
 // The pass is HBM-bound (every K/V byte is read exactly once), so the design
 // goal is to keep the VALU work per byte well under the issue budget:
@@ -23,14 +34,14 @@
 //     2^kRescaleLog2 (exact either way -- the max only bounds exponent range);
 //   * full 64-key iterations run without masks; one masked iteration takes
 //     the remainder.
-// At the end the 16 streams are merged (lane shuffles, then LDS).  A sequence
-// that fits one split writes its normalised output directly; otherwise each
-// split stores (m, l, acc[d_k]) to the workspace and a second, small kernel
-// merges the splits and normalises (attention_gqa.py:143 acc / row_sum).
-// The merge is a separate launch on purpose: on MI355X each XCD has its own
-// L2, so a device-scope fence inside the split kernel (to let the last
-// workgroup combine) writes back and invalidates the whole L2 per workgroup,
-// which costs far more than one extra launch.
+// At the end of a segment the 16 streams are merged (lane shuffles, then
+// LDS).  A pair inside one share is normalised and written directly;
+// otherwise each share's segment stores (m, l, acc[d_k]) to the workspace and
+// a second, small kernel merges them and normalises (attention_gqa.py:143
+// acc / row_sum).  The merge is a separate launch on purpose: on MI355X each
+// XCD has its own L2, so a device-scope fence inside the split kernel (to let
+// the last workgroup combine) writes back and invalidates the whole L2 per
+// workgroup, which costs far more than one extra launch.
 #include "tl_common.h"
 
 #include <math.h>
@@ -112,6 +123,9 @@ struct DecodeParams {
   void* o;
   int len_add;
   int batch, n_head, n_kv, group, max_ctx, split, max_splits;
+  int heads_per_pair;  // query heads of one (kv head, chunk) pair: min(group, 8)
+  int n_pairs;         // (kv head, chunk) pairs per sequence
+  int n_blocks;        // workgroups launched by the split kernel
   int64_t q_sb, q_sh;
   int64_t k_sb, k_sh;
   int64_t v_sb, v_sh;
@@ -127,6 +141,104 @@ __device__ __forceinline__ int ctx_len(const DecodeParams& p, int b) {
   return c > p.max_ctx ? p.max_ctx : c;
 }
 
+// ---- Equal-work partition ------------------------------------------------
+// The cached positions of all (sequence, pair) streams are laid end to end in
+// the order (b, pair, position): pair q of sequence b occupies rows
+// [S_b + q*ctx_b, S_b + (q+1)*ctx_b), S_b = n_pairs * sum_{b' < b} ctx_b'.
+// Workgroup i takes rows [i*rpb, (i+1)*rpb), so every workgroup streams the
+// same number of K/V bytes whatever the sequence lengths, and a workgroup
+// may cover the end of one pair and the start of the next.
+template <typename I>
+__device__ __forceinline__ I wave_incl_scan(I x, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const I y = __shfl_up(x, d);
+    if (lane >= d) x += y;
+  }
+  return x;
+}
+
+__device__ __forceinline__ int64_t wave_sum64(int64_t x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+  return x;
+}
+
+// Values equal on every lane, moved to scalar registers (the compiler cannot
+// see through the lane shuffles that produced them).
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ int64_t uniform(int64_t x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)x >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// Rows in the flattened order (uniform across the wave).
+__device__ __forceinline__ int64_t total_rows(const DecodeParams& p, int lane) {
+  int64_t t = 0;
+  for (int b0 = 0; b0 < p.batch; b0 += 64)
+    t += wave_sum64(b0 + lane < p.batch ? (int64_t)ctx_len(p, b0 + lane) : 0);
+  return uniform(t) * p.n_pairs;
+}
+
+// Rows per workgroup: an even share of the rows, at least `split`, rounded up
+// to whole 64-position iterations.
+__device__ __forceinline__ int64_t rows_per_block(const DecodeParams& p, int64_t rows) {
+  int64_t r = (rows + p.n_blocks - 1) / p.n_blocks;
+  r = r < p.split ? p.split : r;
+  return (r + 63) & ~(int64_t)63;
+}
+
+// The sequence owning flattened row r (r < total rows): b, S_b and ctx_b.
+struct SeqPos {
+  int b;
+  int ctx;
+  int64_t start;
+};
+
+// Lane b's view of sequences 0..63: ctx_b and the flattened rows of
+// sequences 0..b.  With batch <= 64 one load of the lengths serves the whole
+// workgroup life (every dependent load costs microseconds under full HBM
+// load).
+struct SeqScan {
+  int c;
+  int64_t incl;
+};
+__device__ __forceinline__ SeqScan scan_first64(const DecodeParams& p, int lane) {
+  SeqScan s;
+  s.c = lane < p.batch ? ctx_len(p, lane) : 0;
+  s.incl = wave_incl_scan((int64_t)s.c * p.n_pairs, lane);
+  return s;
+}
+__device__ __forceinline__ SeqPos locate_in(const SeqScan& s, int64_t r, int n_pairs) {
+  const uint64_t hit = __ballot(s.incl > r);
+  const int l = __ffsll((unsigned long long)hit) - 1;
+  SeqPos q;
+  q.b = uniform(l);
+  q.ctx = uniform(__shfl(s.c, l));
+  q.start = uniform(__shfl(s.incl - (int64_t)s.c * n_pairs, l));
+  return q;
+}
+__device__ __forceinline__ SeqPos locate_row(const DecodeParams& p, int64_t r, int lane) {
+  int64_t base = 0;
+  for (int b0 = 0; b0 < p.batch; b0 += 64) {
+    const int c = b0 + lane < p.batch ? ctx_len(p, b0 + lane) : 0;
+    const int64_t rows = (int64_t)c * p.n_pairs;
+    const int64_t incl = base + wave_incl_scan(rows, lane);
+    const uint64_t hit = __ballot(incl > r);
+    if (hit) {
+      const int l = __ffsll((unsigned long long)hit) - 1;
+      SeqPos s;
+      s.b = uniform(b0 + l);
+      s.ctx = uniform(__shfl(c, l));
+      s.start = uniform(__shfl(incl - rows, l));
+      return s;
+    }
+    base = uniform(__shfl(incl, 63));
+  }
+  return SeqPos{p.batch, 0, base};  // not reached for r < total rows
+}
+
 // Weights that merge two log2-domain (max, sum) states into max mn.
 __device__ __forceinline__ void merge_weights(float m, float m2, float& w1, float& w2, float& mn) {
   mn = fmaxf(m, m2);
@@ -140,253 +252,329 @@ __device__ __forceinline__ void store_out(void* base, int64_t idx, float x) {
   ((typename T::bits*)base)[idx] = from_f32<T>(x);
 }
 
-// G: query heads handled by this workgroup (<= group); blockIdx.y encodes
-// (kv head, head chunk).
+// G: query heads of one (kv head, chunk) pair (<= group).
 template <typename T, int D, int G>
 __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p) {
   constexpr int EPL = D / 16;           // elements per lane per row
   constexpr int W = EPL * T::size / 4;  // 32-bit words per lane per row
   using Bits = typename T::bits;
 
-  const int split = blockIdx.x;
-  const int b = blockIdx.z;
-  const int n_chunks = (p.group + G - 1) / G;
-  const int hkv = blockIdx.y / n_chunks;
-  const int hq0 = hkv * p.group + (blockIdx.y - hkv * n_chunks) * G;
-  const int n_g = min(G, hkv * p.group + p.group - hq0);  // heads valid in this chunk
-
   const int tid = threadIdx.x;
-  const int ctx = ctx_len(p, b);
-  if (ctx == 0) {
-    // Nothing to attend to: zeros, the reference's empty-KV result
-    // (tests/test_attention_gqa.py:297).
-    if (split == 0)
-      for (int idx = tid; idx < n_g * D; idx += kThreads)
-        store_out<T>(p.o, b * p.o_sb + (int64_t)(hq0 + idx / D) * p.o_sh + idx % D, 0.f);
-    return;
-  }
-  const int start = split * p.split;
-  if (start >= ctx) return;  // this split is past the sequence end
-  const int end = min(ctx, start + p.split);
-  const int n_split = (ctx + p.split - 1) / p.split;
-
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int sub = lane & 15;
   const int stream = wave * 4 + (lane >> 4);
+  const int n_chunks = p.n_pairs / p.n_kv;
 
-  // Query slices of the G heads, kept in storage format.
-  Slice<W> qs[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const uint32_t* src = (const uint32_t*)((const Bits*)p.q + b * p.q_sb +
-                                            (int64_t)min(hq0 + g, hq0 + n_g - 1) * p.q_sh + sub * EPL);
-#pragma unroll
-    for (int i = 0; i < W; ++i) qs[g].w[i] = (g < n_g) ? src[i] : 0u;
-  }
+  const SeqScan scan = scan_first64(p, lane);
+  const bool in_regs = p.batch <= 64;
+  const int64_t total = in_regs ? uniform(__shfl(scan.incl, 63)) : total_rows(p, lane);
+  const int64_t rpb = uniform(rows_per_block(p, total));
+  const int64_t r0 = (int64_t)blockIdx.x * rpb;
+  if (r0 >= total) return;
+  const int64_t r1 = r0 + rpb < total ? r0 + rpb : total;
 
-  float m[G], l[G], acc[G][EPL];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m[g] = -INFINITY;
-    l[g] = 0.f;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
-  }
-
-  const __amdgpu_buffer_rsrc_t krs = make_rsrc((const Bits*)p.k + b * p.k_sb + hkv * p.k_sh, p.k_region_bytes);
-  const __amdgpu_buffer_rsrc_t vrs = make_rsrc((const Bits*)p.v + b * p.v_sb + hkv * p.v_sh, p.v_region_bytes);
+  __shared__ float s_m[4][G], s_l[4][G];
+  __shared__ float s_acc[4][G][D];
   const uint32_t lane_bytes = sub * (EPL * T::size);
   const float c = p.scale_log2;
 
-  // One iteration: kUnroll keys per stream, 64 per workgroup.
-  auto iteration = [&](int key0, auto masked) {
-    constexpr bool kMasked = decltype(masked)::value;
-    Slice<W> kr[kUnroll], vr[kUnroll];
-    bool valid[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int key = key0 + u * kStreams;
-      if constexpr (kMasked) {
-        // Out-of-range keys re-read this split's first row (always inside
-        // the sequence) and are masked out of the softmax below.
-        valid[u] = key < end;
-        const uint32_t row = valid[u] ? key : start;
-        load_slice(kr[u], krs, row * p.k_row_bytes + lane_bytes, 0);
-        load_slice(vr[u], vrs, row * p.v_row_bytes + lane_bytes, 0);
-      } else {
-        valid[u] = true;
-        load_slice(kr[u], krs, (uint32_t)key0 * p.k_row_bytes + lane_bytes, u * kStreams * p.k_row_bytes);
-        load_slice(vr[u], vrs, (uint32_t)key0 * p.v_row_bytes + lane_bytes, u * kStreams * p.v_row_bytes);
-      }
-    }
-    float s[G][kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float d = row16_sum(dot_slice<T>(qs[g], kr[u])) * c;
-        s[g][u] = (!kMasked || valid[u]) ? d : -INFINITY;
-      }
-    }
-    // Lazy rescale: move the running max only when a score would exceed it
-    // by more than 2^kRescaleLog2.
-    bool grow = false;
-    float mb[G];
+  for (int64_t r = r0; r < r1;) {
+    // The segment [r, seg_end) of this workgroup's rows lies in one pair.
+    const SeqPos sp = in_regs ? locate_in(scan, r, p.n_pairs) : locate_row(p, r, lane);
+    const int b = sp.b;
+    const int pair = uniform((int)((r - sp.start) / sp.ctx));
+    const int64_t pair_row0 = sp.start + (int64_t)pair * sp.ctx;
+    const int start = (int)(r - pair_row0);
+    const int end = (int)((r1 - pair_row0) < sp.ctx ? (r1 - pair_row0) : sp.ctx);
+    r = pair_row0 + end;
+    const int hkv = pair / n_chunks;
+    const int hq0 = hkv * p.group + (pair - hkv * n_chunks) * G;
+    const int n_g = min(G, hkv * p.group + p.group - hq0);  // heads valid in this pair
+    // Workgroups covering this pair: the partial of this one goes to slot
+    // blockIdx.x - first; a pair inside one workgroup is finished here.
+    const int64_t first = uniform((int64_t)(pair_row0 / rpb));
+    const bool whole = uniform((int)((pair_row0 + sp.ctx - 1) / rpb - first)) == 0;
+    const int slot = (int)(blockIdx.x - first);
+
+    // Query slices of the G heads, kept in storage format.
+    Slice<W> qs[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      mb[g] = s[g][0];
+      const uint32_t* src = (const uint32_t*)((const Bits*)p.q + b * p.q_sb +
+                                              (int64_t)min(hq0 + g, hq0 + n_g - 1) * p.q_sh + sub * EPL);
 #pragma unroll
-      for (int u = 1; u < kUnroll; ++u) mb[g] = fmaxf(mb[g], s[g][u]);
-      grow |= mb[g] > m[g] + kRescaleLog2;
+      for (int i = 0; i < W; ++i) qs[g].w[i] = (g < n_g) ? src[i] : 0u;
     }
-    if (__any(grow)) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float mn = fmaxf(m[g], mb[g]);
-        const float alpha = fast_exp2(m[g] - ((mn == -INFINITY) ? 0.f : mn));
-        m[g] = mn;
-        l[g] *= alpha;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[g][e] *= alpha;
-      }
-    }
-    float pu[G][kUnroll];
+
+    float m[G], l[G], acc[G][EPL];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float base = (m[g] == -INFINITY) ? 0.f : m[g];
+      m[g] = -INFINITY;
+      l[g] = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
+    }
+
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc((const Bits*)p.k + b * p.k_sb + hkv * p.k_sh, p.k_region_bytes);
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc((const Bits*)p.v + b * p.v_sb + hkv * p.v_sh, p.v_region_bytes);
+
+    // One iteration: kUnroll keys per stream, 64 per workgroup.
+    auto iteration = [&](int key0, auto masked) {
+      constexpr bool kMasked = decltype(masked)::value;
+      Slice<W> kr[kUnroll], vr[kUnroll];
+      bool valid[kUnroll];
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        pu[g][u] = fast_exp2(s[g][u] - base);
-        l[g] += pu[g][u];
+        const int key = key0 + u * kStreams;
+        if constexpr (kMasked) {
+          // Out-of-range keys re-read this segment's first row (always
+          // inside the sequence) and are masked out of the softmax below.
+          valid[u] = key < end;
+          const uint32_t row = valid[u] ? key : start;
+          load_slice(kr[u], krs, row * p.k_row_bytes + lane_bytes, 0);
+          load_slice(vr[u], vrs, row * p.v_row_bytes + lane_bytes, 0);
+        } else {
+          valid[u] = true;
+          load_slice(kr[u], krs, (uint32_t)key0 * p.k_row_bytes + lane_bytes, u * kStreams * p.k_row_bytes);
+          load_slice(vr[u], vrs, (uint32_t)key0 * p.v_row_bytes + lane_bytes, u * kStreams * p.v_row_bytes);
+        }
+      }
+      float s[G][kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float d = row16_sum(dot_slice<T>(qs[g], kr[u])) * c;
+          s[g][u] = (!kMasked || valid[u]) ? d : -INFINITY;
+        }
+      }
+      // Lazy rescale: move the running max only when a score would exceed
+      // it by more than 2^kRescaleLog2.
+      bool grow = false;
+      float mb[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        mb[g] = s[g][0];
+#pragma unroll
+        for (int u = 1; u < kUnroll; ++u) mb[g] = fmaxf(mb[g], s[g][u]);
+        grow |= mb[g] > m[g] + kRescaleLog2;
+      }
+      if (__any(grow)) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float mn = fmaxf(m[g], mb[g]);
+          const float alpha = fast_exp2(m[g] - ((mn == -INFINITY) ? 0.f : mn));
+          m[g] = mn;
+          l[g] *= alpha;
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) acc[g][e] *= alpha;
+        }
+      }
+      float pu[G][kUnroll];
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float base = (m[g] == -INFINITY) ? 0.f : m[g];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+          pu[g][u] = fast_exp2(s[g][u] - base);
+          l[g] += pu[g][u];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        float vf[EPL];
+        slice_to_float<T>(vr[u], vf);
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(pu[g][u], vf[e], acc[g][e]);
+      }
+    };
+
+    const int n_full = (end - start) / kKeysPerIter;
+    int key0 = start + stream;
+    for (int it = 0; it < n_full; ++it, key0 += kKeysPerIter) iteration(key0, std::false_type{});
+    if (start + n_full * kKeysPerIter < end) iteration(key0, std::true_type{});
+
+    // Merge the 4 streams of this wave (lane groups 16 apart).
+#pragma unroll
+    for (int off = 16; off <= 32; off <<= 1) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float m2 = __shfl_xor(m[g], off);
+        const float l2 = __shfl_xor(l[g], off);
+        float w1, w2, mn;
+        merge_weights(m[g], m2, w1, w2, mn);
+        m[g] = mn;
+        l[g] = l[g] * w1 + l2 * w2;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+          const float a2 = __shfl_xor(acc[g][e], off);
+          acc[g][e] = acc[g][e] * w1 + a2 * w2;
+        }
       }
     }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      float vf[EPL];
-      slice_to_float<T>(vr[u], vf);
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(pu[g][u], vf[e], acc[g][e]);
-    }
-  };
 
-  const int n_full = (end - start) / kKeysPerIter;
-  int key0 = start + stream;
-  for (int it = 0; it < n_full; ++it, key0 += kKeysPerIter) iteration(key0, std::false_type{});
-  if (start + n_full * kKeysPerIter < end) iteration(key0, std::true_type{});
-
-  // Merge the 4 streams of this wave (lane groups 16 apart).
+    // Merge the 4 waves through LDS (the barrier in front protects the
+    // previous segment's reads of the same arrays).
+    __syncthreads();
+    if (lane < 16) {
 #pragma unroll
-  for (int off = 16; off <= 32; off <<= 1) {
+      for (int g = 0; g < G; ++g) {
+        if (lane == 0) {
+          s_m[wave][g] = m[g];
+          s_l[wave][g] = l[g];
+        }
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float m2 = __shfl_xor(m[g], off);
-      const float l2 = __shfl_xor(l[g], off);
-      float w1, w2, mn;
-      merge_weights(m[g], m2, w1, w2, mn);
-      m[g] = mn;
-      l[g] = l[g] * w1 + l2 * w2;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) {
-        const float a2 = __shfl_xor(acc[g][e], off);
-        acc[g][e] = acc[g][e] * w1 + a2 * w2;
+        for (int e = 0; e < EPL; ++e) s_acc[wave][g][sub * EPL + e] = acc[g][e];
       }
     }
-  }
-
-  // Merge the 4 waves through LDS.
-  __shared__ float s_m[4][G], s_l[4][G];
-  __shared__ float s_acc[4][G][D];
-  if (lane < 16) {
+    __syncthreads();
+    const int64_t row_base = ((int64_t)b * p.n_head + hq0) * p.max_splits;
+    for (int idx = tid; idx < n_g * D; idx += kThreads) {
+      const int g = idx / D;
+      const int d = idx - g * D;
+      float mx = -INFINITY;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      if (lane == 0) {
-        s_m[wave][g] = m[g];
-        s_l[wave][g] = l[g];
+      for (int w = 0; w < 4; ++w) mx = fmaxf(mx, s_m[w][g]);
+      const float base = (mx == -INFINITY) ? 0.f : mx;
+      float a = 0.f, lsum = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float wt = fast_exp2(s_m[w][g] - base);
+        a += s_acc[w][g][d] * wt;
+        lsum += s_l[w][g] * wt;
       }
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) s_acc[wave][g][sub * EPL + e] = acc[g][e];
-    }
-  }
-  __syncthreads();
-  const int64_t row_base = ((int64_t)b * p.n_head + hq0) * p.max_splits;
-  for (int idx = tid; idx < n_g * D; idx += kThreads) {
-    const int g = idx / D;
-    const int d = idx - g * D;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) mx = fmaxf(mx, s_m[w][g]);
-    const float base = (mx == -INFINITY) ? 0.f : mx;
-    float a = 0.f, lsum = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float wt = fast_exp2(s_m[w][g] - base);
-      a += s_acc[w][g][d] * wt;
-      lsum += s_l[w][g] * wt;
-    }
-    if (n_split == 1) {
-      store_out<T>(p.o, b * p.o_sb + (int64_t)(hq0 + g) * p.o_sh + d, a / lsum);
-    } else {
-      const int64_t row = row_base + (int64_t)g * p.max_splits + split;
-      p.ws_acc[row * D + d] = a;
-      if (d == 0) {
-        p.ws_ml[row * 2 + 0] = mx;
-        p.ws_ml[row * 2 + 1] = lsum;
+      if (whole) {
+        store_out<T>(p.o, b * p.o_sb + (int64_t)(hq0 + g) * p.o_sh + d, a / lsum);
+      } else {
+        const int64_t row = row_base + (int64_t)g * p.max_splits + slot;
+        p.ws_acc[row * D + d] = a;
+        if (d == 0) {
+          p.ws_ml[row * 2 + 0] = mx;
+          p.ws_ml[row * 2 + 1] = lsum;
+        }
       }
     }
   }
 }
 
-// One workgroup per (b, query head): merge the splits and normalise.
-// Sequences that fit one split (or are empty) were finished by the split
-// kernel.
+// One wave per (b, query head): merge the partials of the workgroups that
+// covered this head's pair and normalise.  A pair inside one workgroup was
+// finished by the split kernel; an empty sequence gets zeros here (the
+// reference's empty-KV result, tests/test_attention_gqa.py:297).  The kernel is latency-bound (a few KiB per head), so every load
+// it can issue early is issued early: lane s holds split s's (m, l) pair,
+// the accumulator rows are read eight splits at a time, the next eight in
+// flight while the current ones are summed, and a split's weight reaches
+// the other lanes with v_readlane.
 template <typename T, int D>
 __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
+  constexpr int NJ = (D + 63) / 64;
+  constexpr int R = 8;
   const int hq = blockIdx.x;
   const int b = blockIdx.y;
+  const int lane = threadIdx.x;
   const int ctx = ctx_len(p, b);
-  const int n_split = (ctx + p.split - 1) / p.split;
+  if (ctx == 0) {
+    for (int d = lane; d < D; d += 64) store_out<T>(p.o, b * p.o_sb + (int64_t)hq * p.o_sh + d, 0.f);
+    return;
+  }
+  int64_t total = 0, before = 0;
+  for (int b0 = 0; b0 < p.batch; b0 += 64) {
+    const int bb = b0 + lane;
+    const int64_t cb = bb < p.batch ? ctx_len(p, bb) : 0;
+    total += wave_sum64(cb);
+    before += wave_sum64(bb < b ? cb : 0);
+  }
+  total = uniform(total);
+  before = uniform(before);
+  const int64_t rpb = rows_per_block(p, total * p.n_pairs);
+  const int hkv = hq / p.group;
+  const int pair = hkv * (p.n_pairs / p.n_kv) + (hq - hkv * p.group) / p.heads_per_pair;
+  const int64_t pair_row0 = before * p.n_pairs + (int64_t)pair * ctx;
+  const int64_t first = pair_row0 / rpb;
+  const int n_split = (int)((pair_row0 + ctx - 1) / rpb - first) + 1;
   if (n_split <= 1) return;
   const int64_t row0 = ((int64_t)b * p.n_head + hq) * p.max_splits;
-  float mx = -INFINITY;
-  for (int s = 0; s < n_split; ++s) mx = fmaxf(mx, p.ws_ml[(row0 + s) * 2]);
+  const float2* ml = (const float2*)p.ws_ml + row0;
+  const float* acc = p.ws_acc + row0 * D;
+  auto load_rows = [&](int s0, float (&r)[R][NJ]) {
+#pragma unroll
+    for (int k = 0; k < R; ++k)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int d = lane + 64 * j;
+        r[k][j] = (s0 + k < n_split && d < D) ? acc[(int64_t)(s0 + k) * D + d] : 0.f;
+      }
+  };
+  float r[R][NJ];
+  load_rows(0, r);
+  const float2 e0 = lane < n_split ? ml[lane] : make_float2(-INFINITY, 0.f);
+  float mx = e0.x;
+  for (int s = lane + 64; s < n_split; s += 64) mx = fmaxf(mx, ml[s].x);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
   const float base = (mx == -INFINITY) ? 0.f : mx;
-  float lsum = 0.f;
-  float a[(D + 63) / 64];
+  float lsum = 0.f, a[NJ];
 #pragma unroll
-  for (int j = 0; j < (D + 63) / 64; ++j) a[j] = 0.f;
-  for (int s = 0; s < n_split; ++s) {
-    const float wt = fast_exp2(p.ws_ml[(row0 + s) * 2] - base);
-    lsum += p.ws_ml[(row0 + s) * 2 + 1] * wt;
-#pragma unroll
-    for (int j = 0; j < (D + 63) / 64; ++j) {
-      const int d = threadIdx.x + 64 * j;
-      if (d < D) a[j] += p.ws_acc[(row0 + s) * D + d] * wt;
+  for (int j = 0; j < NJ; ++j) a[j] = 0.f;
+  float wl = 0.f;  // weight of split (s0 & ~63) + lane
+  for (int s0 = 0; s0 < n_split; s0 += R) {
+    if ((s0 & 63) == 0) {
+      const int s = s0 + lane;
+      const float2 e = s0 == 0 ? e0 : (s < n_split ? ml[s] : make_float2(-INFINITY, 0.f));
+      wl = s < n_split ? fast_exp2(e.x - base) : 0.f;
+      lsum += e.y * wl;
     }
+    float rn[R][NJ];
+    if (s0 + R < n_split) load_rows(s0 + R, rn);
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), (s0 + k) & 63));
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) a[j] = fmaf(r[k][j], w, a[j]);
+    }
+#pragma unroll
+    for (int k = 0; k < R; ++k)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) r[k][j] = rn[k][j];
   }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) lsum += __shfl_xor(lsum, off);
   const float inv = 1.f / lsum;
 #pragma unroll
-  for (int j = 0; j < (D + 63) / 64; ++j) {
-    const int d = threadIdx.x + 64 * j;
+  for (int j = 0; j < NJ; ++j) {
+    const int d = lane + 64 * j;
     if (d < D) store_out<T>(p.o, b * p.o_sb + (int64_t)hq * p.o_sh + d, a[j] * inv);
   }
 }
 
 template <typename T, int D, int G>
-int launch_decode_g(const DecodeParams& p, hipStream_t st) {
-  const int n_chunks = (p.group + G - 1) / G;
-  dim3 grid(p.max_splits, p.n_kv * n_chunks, p.batch);
-  hipLaunchKernelGGL((decode_split_kernel<T, D, G>), grid, dim3(kThreads), 0, st, p);
+int launch_decode_g(DecodeParams& p, hipStream_t st) {
+  // One workgroup per resident slot (occupancy x compute units), never more
+  // than the shares of `split` positions a full cache would hold.
+  static int per_cu = 0;
+  if (per_cu == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_split_kernel<T, D, G>, kThreads, 0) !=
+            hipSuccess ||
+        n <= 0)
+      n = 1;
+    per_cu = n;
+  }
+  const int64_t most = ((int64_t)p.batch * p.n_pairs * p.max_ctx + p.split - 1) / p.split;
+  const int64_t slots = (int64_t)per_cu * tl_device_cus();
+  p.n_blocks = (int)(most < slots ? most : slots);
+  hipLaunchKernelGGL((decode_split_kernel<T, D, G>), dim3(p.n_blocks), dim3(kThreads), 0, st, p);
   int e = tl_launch_status();
-  if (e || p.max_splits == 1) return e;
+  if (e) return e;
   hipLaunchKernelGGL((decode_combine_kernel<T, D>), dim3(p.n_head, p.batch), dim3(64), 0, st, p);
   return tl_launch_status();
 }
 
 template <typename T, int D>
-int launch_decode_d(const DecodeParams& p, hipStream_t st) {
+int launch_decode_d(DecodeParams& p, hipStream_t st) {
   switch (p.group) {
     case 1: return launch_decode_g<T, D, 1>(p, st);
     case 2: return launch_decode_g<T, D, 2>(p, st);
@@ -400,7 +588,7 @@ int launch_decode_d(const DecodeParams& p, hipStream_t st) {
 }
 
 template <typename T>
-int launch_decode_t(const DecodeParams& p, int d_k, hipStream_t st) {
+int launch_decode_t(DecodeParams& p, int d_k, hipStream_t st) {
   switch (d_k) {
     case 64: return launch_decode_d<T, 64>(p, st);
     case 128: return launch_decode_d<T, 128>(p, st);
@@ -415,20 +603,23 @@ size_t round256(size_t x) { return (x + 255) & ~(size_t)255; }
 extern "C" {
 
 int tl_decode_split_size(int batch, int n_kv_head, int max_ctx) {
-  // Aim for several thousand workgroups over the longest sequence: enough to
-  // fill 256 CUs several times over, while keeping each split at up to 1024
-  // positions (512 KiB of K+V at d_k 128 bf16) so its partial write stays
-  // negligible.
-  const int64_t heads = (int64_t)batch * (n_kv_head > 0 ? n_kv_head : 1);
+  // Minimum positions per workgroup share.  The split kernel shares the
+  // cached positions evenly over the resident workgroups; this floor keeps a
+  // share at least one 64-position iteration when the caches are short, and
+  // bounds the partial slots one (sequence, head) can need, hence the
+  // workspace.  Picked so a full-length cache would give about 16384 shares.
+  const int64_t rows = (int64_t)(batch > 0 ? batch : 1) * (n_kv_head > 0 ? n_kv_head : 1) * (max_ctx > 0 ? max_ctx : 1);
   int split = 64;
-  while (split < 1024 && heads * ((max_ctx + 2 * split - 1) / (2 * split)) >= 8192) split *= 2;
+  while (split < 4096 && rows > (int64_t)split * 16384) split *= 2;
   return split;
 }
 
 size_t tl_attention_decode_workspace_bytes(int batch, int n_head, int max_ctx,
                                            int d_k, int split_size) {
   if (batch <= 0 || n_head <= 0 || max_ctx <= 0 || d_k <= 0 || split_size <= 0) return 0;
-  const size_t splits = (size_t)((max_ctx + split_size - 1) / split_size);
+  // A (sequence, head) covers at most ceil(max_ctx / split) + 1 workgroup
+  // shares (every share holds at least split positions).
+  const size_t splits = (size_t)((max_ctx + split_size - 1) / split_size) + 1;
   const size_t rows = (size_t)batch * n_head * splits;
   // (m, l) pairs, then accumulators (256-byte aligned).
   return round256(rows * 2 * sizeof(float)) + rows * (size_t)d_k * sizeof(float);
@@ -466,7 +657,10 @@ int tl_attention_decode(const void* q, const void* k_cache, const void* v_cache,
   p.group = n_head / n_kv_head;
   p.max_ctx = max_ctx;
   p.split = split_size;
-  p.max_splits = (max_ctx + split_size - 1) / split_size;
+  p.max_splits = (max_ctx + split_size - 1) / split_size + 1;
+  p.heads_per_pair = p.group < 8 ? p.group : 8;
+  p.n_pairs = n_kv_head * ((p.group + p.heads_per_pair - 1) / p.heads_per_pair);
+
   const size_t rows = (size_t)batch * n_head * p.max_splits;
   char* ws = (char*)workspace;
   p.ws_ml = (float*)ws;

@@ -998,28 +998,6 @@ size_t vt_bytes(int batch, int n_kv, int seq_k, int d_k) {
   return (size_t)batch * n_kv * d_k * sk_pad * 2;
 }
 
-// Compute units of the current device (cached per device), capped by
-// TRITON_LLM_HIP_MAX_CUS when set (tests use it to force multi-round tile
-// schedules on small shapes).
-int device_cus() {
-  static int cus[64] = {0};
-  int dev = 0;
-  int n = 256;
-  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
-    if (cus[dev] == 0) {
-      int c = 0;
-      if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
-      cus[dev] = c;
-    }
-    n = cus[dev];
-  }
-  if (const char* cap = getenv("TRITON_LLM_HIP_MAX_CUS")) {
-    const int c = atoi(cap);
-    if (c > 0 && c < n) n = c;
-  }
-  return n;
-}
-
 template <typename T, int D>
 int launch_flash_16(FlashParams& p, void* ws, bool causal, hipStream_t st) {
   p.vt = ws;
@@ -1029,7 +1007,7 @@ int launch_flash_16(FlashParams& p, void* ws, bool causal, hipStream_t st) {
   p.n_queues = units % 8 == 0 ? 8 : 1;
   p.q_units = units / p.n_queues;
   p.q_tiles = p.q_units * p.n_qt * p.group;
-  p.q_machines = min((device_cus() + p.n_queues - 1) / p.n_queues, p.q_tiles);
+  p.q_machines = min((tl_device_cus() + p.n_queues - 1) / p.n_queues, p.q_tiles);
   const int rounds = p.q_tiles / p.q_machines;
   p.q_triple = (p.q_tiles % p.q_machines == 0 && rounds % 2 == 1 && rounds >= 3 && p.q_machines % 2 == 0) ? 1 : 0;
   dim3 tg(p.sk_pad / 64, p.n_kv, p.batch);

@@ -4,6 +4,8 @@
 // kernel launch shares one in-order HIP stream.
 #include "tl_common.h"
 
+#include <stdlib.h>
+
 namespace {
 hipStream_t g_stream = nullptr;
 int g_device = -1;
@@ -11,6 +13,25 @@ int g_device = -1;
 
 hipStream_t tl_resolve_stream(void* stream) {
   return stream ? (hipStream_t)stream : g_stream;
+}
+
+int tl_device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  int n = 256;
+  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
+    if (cus[dev] == 0) {
+      int c = 0;
+      if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+      cus[dev] = c;
+    }
+    n = cus[dev];
+  }
+  if (const char* cap = getenv("TRITON_LLM_HIP_MAX_CUS")) {
+    const int c = atoi(cap);
+    if (c > 0 && c < n) n = c;
+  }
+  return n;
 }
 
 extern "C" {
