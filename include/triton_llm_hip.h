@@ -113,10 +113,14 @@ int tl_attention_fwd(const void* q, const void* k, const void* v, void* o,
  * Q/O: (batch, n_head, d_k) with {batch, head} strides.  Caches:
  * (batch, n_kv_head, max_ctx, d_k) with {batch, head, seq} strides.
  * Sequence b attends to positions [0, min(cache_lens[b] + len_add, max_ctx)).
- * split_size: positions per split (multiple of 16); 0 picks a default.
- * Launches the split pass and, when any sequence spans more than one split,
- * a combine pass; the workspace holds the per-split partials and may be
- * reused by consecutive calls on one stream.
+ * The cached positions of all sequences and KV heads are cut into equal
+ * shares, one per resident workgroup of the device; split_size (multiple of
+ * 16; 0 picks tl_decode_split_size) is the smallest share, which bounds the
+ * partials one (sequence, head) can produce: ceil(max_ctx / split_size) + 1.
+ * Launches the split pass, then a combine pass that merges the partials of
+ * heads whose positions were shared by several workgroups and writes zeros
+ * for empty sequences.  The workspace holds the partials and may be reused
+ * by consecutive calls on one stream.
  * ------------------------------------------------------------------------- */
 int tl_decode_split_size(int batch, int n_kv_head, int max_ctx);
 size_t tl_attention_decode_workspace_bytes(int batch, int n_head, int max_ctx,
