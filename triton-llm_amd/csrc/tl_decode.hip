@@ -252,6 +252,19 @@ __device__ __forceinline__ void store_out(void* base, int64_t idx, float x) {
   ((typename T::bits*)base)[idx] = from_f32<T>(x);
 }
 
+// Wave priority from the share's progress: a wave with less of its share
+// done wins instruction issue (and so memory issue) over waves that are
+// further along.  Without it the hardware's age order lets the oldest
+// workgroup of a CU run ahead while the youngest starves, so the equal
+// shares finish up to 140 us apart; with it, within 50 us.
+__device__ __forceinline__ void set_progress_priority(int64_t done, int64_t share) {
+  const int64_t q = done * 4 / share;
+  if (q <= 0) __builtin_amdgcn_s_setprio(3);
+  else if (q == 1) __builtin_amdgcn_s_setprio(2);
+  else if (q == 2) __builtin_amdgcn_s_setprio(1);
+  else __builtin_amdgcn_s_setprio(0);
+}
+
 // G: query heads of one (kv head, chunk) pair (<= group).
 template <typename T, int D, int G>
 __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p) {
@@ -394,7 +407,11 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p) 
 
     const int n_full = (end - start) / kKeysPerIter;
     int key0 = start + stream;
-    for (int it = 0; it < n_full; ++it, key0 += kKeysPerIter) iteration(key0, std::false_type{});
+    const int64_t seg_done0 = pair_row0 + start - r0;  // positions of the share already done
+    for (int it = 0; it < n_full; ++it, key0 += kKeysPerIter) {
+      if ((it & 3) == 0) set_progress_priority(seg_done0 + (int64_t)it * kKeysPerIter, r1 - r0);
+      iteration(key0, std::false_type{});
+    }
     if (start + n_full * kKeysPerIter < end) iteration(key0, std::true_type{});
 
     // Merge the 4 streams of this wave (lane groups 16 apart).
@@ -463,10 +480,11 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p) 
 // One wave per (b, query head): merge the partials of the workgroups that
 // covered this head's pair and normalise.  A pair inside one workgroup was
 // finished by the split kernel; an empty sequence gets zeros here (the
-// reference's empty-KV result, tests/test_attention_gqa.py:297).  The kernel is latency-bound (a few KiB per head), so every load
-// it can issue early is issued early: lane s holds split s's (m, l) pair,
-// the accumulator rows are read eight splits at a time, the next eight in
-// flight while the current ones are summed, and a split's weight reaches
+// reference's empty-KV result, tests/test_attention_gqa.py:297).
+// The kernel is latency-bound (a few KiB per head), so every load it can
+// issue early is issued early: lane s holds partial s's (m, l) pair, the
+// accumulator rows are read eight partials at a time, the next eight in
+// flight while the current ones are summed, and a partial's weight reaches
 // the other lanes with v_readlane.
 template <typename T, int D>
 __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
