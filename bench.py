@@ -89,6 +89,24 @@ def cpu_threads():
         return os.cpu_count() or 1
 
 
+def cpu_host():
+    """What the CPU baseline ran on: cores the process may use, the thread
+    settings and NumPy's BLAS."""
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except Exception:
+        affinity = os.cpu_count()
+    blas = None
+    try:
+        cfg = np.show_config(mode="dicts")
+        b = cfg.get("Build Dependencies", {}).get("blas", {})
+        blas = f"{b.get('name')} {b.get('version')}".strip()
+    except Exception:
+        pass
+    return {"affinity_cores": affinity, "blas": blas,
+            "threads_env": {k: os.environ.get(k) for k in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS")}}
+
+
 # ---------------------------------------------------------------------------
 # decode
 # ---------------------------------------------------------------------------
@@ -202,6 +220,7 @@ def cpu_decode_baseline(cfg, data, oa, on, budget_s=10.0):
         "value": nbytes / t / 1e9,
         "unit": "GB/s",
         "cores": cpu_threads(),
+        "host": cpu_host(),
         "kind": "port",
         "sample": f"the whole workload ({B} sequences, {int(np.sum(lens))} positions), NumPy fp32 "
                   f"oracle decode, median of {len(passes)} passes ({t_total:.1f}s); bytes counted as "
@@ -213,7 +232,7 @@ def cpu_decode_baseline(cfg, data, oa, on, budget_s=10.0):
 # prefill
 # ---------------------------------------------------------------------------
 
-def bench_prefill(cfg, steps, warmup, cpu=True):
+def bench_prefill(cfg, steps, warmup, replicas=1, cpu=True):
     from oracle import attention as oa
     from oracle import inputs as oi
     from oracle import numerics as on
@@ -225,26 +244,34 @@ def bench_prefill(cfg, steps, warmup, cpu=True):
     gdt = {"bfloat16": gpu.bfloat16, "float16": np.float16, "float32": np.float32}[dt]
     raw = oi.make_prefill_raw(cfg)
     B, Hq, Hkv, S, D = cfg.batch, cfg.n_head, cfg.n_kv_head, cfg.seq, cfg.d_k
-    q = gpu.to_device(raw["q"], gdt)
-    k = gpu.to_device(raw["k"], gdt)
-    v = gpu.to_device(raw["v"], gdt)
     if cfg.rope_theta is not None:
         cos, sin = precompute_cos_sin(S, D, cfg.rope_theta)
         cd, sd = gpu.to_device(cos), gpu.to_device(sin)
-        apply_rope(gpu.view(q, (B * Hq * S, D)), cd, sd, seq_len=S)
-        apply_rope(gpu.view(k, (B * Hkv * S, D)), cd, sd, seq_len=S)
-    out = gpu.allocate(q.shape, gdt)
+    sets = []  # rotate replicas so a step's inputs are not served from MALL
+    for _ in range(replicas):
+        q = gpu.to_device(raw["q"], gdt)
+        k = gpu.to_device(raw["k"], gdt)
+        v = gpu.to_device(raw["v"], gdt)
+        if cfg.rope_theta is not None:
+            apply_rope(gpu.view(q, (B * Hq * S, D)), cd, sd, seq_len=S)
+            apply_rope(gpu.view(k, (B * Hkv * S, D)), cd, sd, seq_len=S)
+        sets.append((q, k, v, gpu.allocate(q.shape, gdt)))
     wsb = flash_workspace_bytes(B, Hkv, S, D, gdt)
     ws = gpu.allocate((max(wsb, 1),), np.uint8)
     lib = gpu.runtime()
     ev = Events(lib, 2 * max(steps, warmup) + 2)
-    for i in range(warmup):
+
+    def step(i):
+        q, k, v, out = sets[i % replicas]
         flash_attention(q, k, v, causal=True, sm_scale=cfg.scale, out=out, workspace=ws)
+
+    for i in range(warmup):
+        step(i)
     gpu.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
         ev.record(2 * i)
-        flash_attention(q, k, v, causal=True, sm_scale=cfg.scale, out=out, workspace=ws)
+        step(i)
         ev.record(2 * i + 1)
     gpu.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
@@ -299,6 +326,7 @@ def cpu_prefill_baseline(cfg, raw, oa, on, oi, budget_s=10.0):
         "value": flops / t / 1e12,
         "unit": "TFLOP/s",
         "cores": cpu_threads(),
+        "host": cpu_host(),
         "kind": "port",
         "sample": f"the whole workload ({B * Hkv} KV groups of {g} heads x {S} rows, 512-row "
                   f"query tiles), NumPy fp32 oracle, median of {len(passes)} passes ({t_total:.1f}s)",
@@ -362,7 +390,11 @@ def main():
             results[name] = bench_decode(cfg, args.steps, args.warmup, replicas=replicas, cpu=cpu,
                                          split=args.decode_split)
         else:
-            results[name] = bench_prefill(cfg, args.steps, args.warmup, cpu=cpu)
+            # Q, K, V and O of one step; replicas so that >= 1 GB of other
+            # inputs passes between two uses of one set (MALL is 256 MB).
+            set_mb = (2 * cfg.n_head + 2 * cfg.n_kv_head) * cfg.batch * cfg.seq * cfg.d_k * (4 if cfg.dtype == "float32" else 2) / 1e6
+            replicas = max(1, int(np.ceil(1024 / set_mb))) if set_mb < 1024 else 1
+            results[name] = bench_prefill(cfg, args.steps, args.warmup, replicas=replicas, cpu=cpu)
         log(f"config {name}: {results[name]['value']:.1f} {results[name]['unit']} "
             f"({results[name]['roofline']['frac'] * 100:.1f}% of roofline)")
 
