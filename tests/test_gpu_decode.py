@@ -131,3 +131,17 @@ def test_decode_few_workgroups_span_many_sequences(monkeypatch, cus, batch):
     data = oi.make_decode(cfg, fill="nan", lens=lens)
     got, exp, _, _ = run_decode_step(cfg, data, split=16)
     compare(f"cus{cus} b{batch}", got, exp, TOL[cfg.dtype])
+
+
+def test_decode_all_sequences_empty_over_64():
+    """Every length 0 (no append): the split kernel finds no positions and
+    exits; the combine writes zeros for all heads.  70 sequences take the
+    lengths scan in two chunks."""
+    dt = "bfloat16"
+    cfg = oi.Config("decode-empty", "decode", dt, 70, 6, 2, 64, 5, 0.125, max_ctx=64, lo=0, hi=0)
+    lens = np.zeros(70, np.int32)
+    data = oi.make_decode(cfg, fill="nan", lens=lens)
+    out = attention_decode(H.upload(data["q"], dt), H.upload(data["k_cache"], dt), H.upload(data["v_cache"], dt),
+                           gpu.to_device(lens), 6, 2, sm_scale=0.125, len_add=0)
+    got = on.from_storage(H.download(out), dt)
+    assert np.all(got == 0)
