@@ -118,11 +118,13 @@ struct DecodeParams {
   const void* k;
   const void* v;
   const int32_t* lens;
-  float* ws_ml;   // [B][Hq][max_splits][2]  (m in log2 domain, l)
-  float* ws_acc;  // [B][Hq][max_splits][D]  unnormalised
+  float* ws_ml;   // [B][Hq][max_slots][2]  (m in log2 domain, l) of partial shares
+  float* ws_acc;  // [B][Hq][max_slots][D]  unnormalised
   void* o;
   int len_add;
-  int batch, n_head, n_kv, group, max_ctx, split, max_splits;
+  int batch, n_head, n_kv, group, max_ctx;
+  int min_share;  // fewest positions in a workgroup share (the split_size argument)
+  int max_slots;  // partial slots per (b, query head): ceil(max_ctx / min_share) + 1
   int heads_per_pair;  // query heads of one (kv head, chunk) pair: min(group, 8)
   int n_pairs;         // (kv head, chunk) pairs per sequence
   int n_blocks;        // workgroups launched by the split kernel
@@ -181,11 +183,11 @@ __device__ __forceinline__ int64_t total_rows(const DecodeParams& p, int lane) {
   return uniform(t) * p.n_pairs;
 }
 
-// Rows per workgroup: an even share of the rows, at least `split`, rounded up
+// Rows per workgroup: an even share of the rows, at least min_share, rounded up
 // to whole 64-position iterations.
 __device__ __forceinline__ int64_t rows_per_block(const DecodeParams& p, int64_t rows) {
   int64_t r = (rows + p.n_blocks - 1) / p.n_blocks;
-  r = r < p.split ? p.split : r;
+  r = r < p.min_share ? p.min_share : r;
   return (r + 63) & ~(int64_t)63;
 }
 
@@ -448,7 +450,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p) 
       }
     }
     __syncthreads();
-    const int64_t row_base = ((int64_t)b * p.n_head + hq0) * p.max_splits;
+    const int64_t row_base = ((int64_t)b * p.n_head + hq0) * p.max_slots;
     for (int idx = tid; idx < n_g * D; idx += kThreads) {
       const int g = idx / D;
       const int d = idx - g * D;
@@ -466,7 +468,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p) 
       if (whole) {
         store_out<T>(p.o, b * p.o_sb + (int64_t)(hq0 + g) * p.o_sh + d, a / lsum);
       } else {
-        const int64_t row = row_base + (int64_t)g * p.max_splits + slot;
+        const int64_t row = row_base + (int64_t)g * p.max_slots + slot;
         p.ws_acc[row * D + d] = a;
         if (d == 0) {
           p.ws_ml[row * 2 + 0] = mx;
@@ -512,9 +514,9 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
   const int pair = hkv * (p.n_pairs / p.n_kv) + (hq - hkv * p.group) / p.heads_per_pair;
   const int64_t pair_row0 = before * p.n_pairs + (int64_t)pair * ctx;
   const int64_t first = pair_row0 / rpb;
-  const int n_split = (int)((pair_row0 + ctx - 1) / rpb - first) + 1;
-  if (n_split <= 1) return;
-  const int64_t row0 = ((int64_t)b * p.n_head + hq) * p.max_splits;
+  const int n_parts = (int)((pair_row0 + ctx - 1) / rpb - first) + 1;
+  if (n_parts <= 1) return;
+  const int64_t row0 = ((int64_t)b * p.n_head + hq) * p.max_slots;
   const float2* ml = (const float2*)p.ws_ml + row0;
   const float* acc = p.ws_acc + row0 * D;
   auto load_rows = [&](int s0, float (&r)[R][NJ]) {
@@ -523,30 +525,30 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
         const int d = lane + 64 * j;
-        r[k][j] = (s0 + k < n_split && d < D) ? acc[(int64_t)(s0 + k) * D + d] : 0.f;
+        r[k][j] = (s0 + k < n_parts && d < D) ? acc[(int64_t)(s0 + k) * D + d] : 0.f;
       }
   };
   float r[R][NJ];
   load_rows(0, r);
-  const float2 e0 = lane < n_split ? ml[lane] : make_float2(-INFINITY, 0.f);
+  const float2 e0 = lane < n_parts ? ml[lane] : make_float2(-INFINITY, 0.f);
   float mx = e0.x;
-  for (int s = lane + 64; s < n_split; s += 64) mx = fmaxf(mx, ml[s].x);
+  for (int s = lane + 64; s < n_parts; s += 64) mx = fmaxf(mx, ml[s].x);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
   const float base = (mx == -INFINITY) ? 0.f : mx;
   float lsum = 0.f, a[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) a[j] = 0.f;
-  float wl = 0.f;  // weight of split (s0 & ~63) + lane
-  for (int s0 = 0; s0 < n_split; s0 += R) {
+  float wl = 0.f;  // weight of partial (s0 & ~63) + lane
+  for (int s0 = 0; s0 < n_parts; s0 += R) {
     if ((s0 & 63) == 0) {
       const int s = s0 + lane;
-      const float2 e = s0 == 0 ? e0 : (s < n_split ? ml[s] : make_float2(-INFINITY, 0.f));
-      wl = s < n_split ? fast_exp2(e.x - base) : 0.f;
+      const float2 e = s0 == 0 ? e0 : (s < n_parts ? ml[s] : make_float2(-INFINITY, 0.f));
+      wl = s < n_parts ? fast_exp2(e.x - base) : 0.f;
       lsum += e.y * wl;
     }
     float rn[R][NJ];
-    if (s0 + R < n_split) load_rows(s0 + R, rn);
+    if (s0 + R < n_parts) load_rows(s0 + R, rn);
 #pragma unroll
     for (int k = 0; k < R; ++k) {
       const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), (s0 + k) & 63));
@@ -571,7 +573,7 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
 template <typename T, int D, int G>
 int launch_decode_g(DecodeParams& p, hipStream_t st) {
   // One workgroup per resident slot (occupancy x compute units), never more
-  // than the shares of `split` positions a full cache would hold.
+  // than the shares of min_share positions a full cache would hold.
   static int per_cu = 0;
   if (per_cu == 0) {
     int n = 0;
@@ -581,7 +583,7 @@ int launch_decode_g(DecodeParams& p, hipStream_t st) {
       n = 1;
     per_cu = n;
   }
-  const int64_t most = ((int64_t)p.batch * p.n_pairs * p.max_ctx + p.split - 1) / p.split;
+  const int64_t most = ((int64_t)p.batch * p.n_pairs * p.max_ctx + p.min_share - 1) / p.min_share;
   const int64_t slots = (int64_t)per_cu * tl_device_cus();
   p.n_blocks = (int)(most < slots ? most : slots);
   hipLaunchKernelGGL((decode_split_kernel<T, D, G>), dim3(p.n_blocks), dim3(kThreads), 0, st, p);
@@ -674,12 +676,12 @@ int tl_attention_decode(const void* q, const void* k_cache, const void* v_cache,
   p.n_kv = n_kv_head;
   p.group = n_head / n_kv_head;
   p.max_ctx = max_ctx;
-  p.split = split_size;
-  p.max_splits = (max_ctx + split_size - 1) / split_size + 1;
+  p.min_share = split_size;
+  p.max_slots = (max_ctx + split_size - 1) / split_size + 1;
   p.heads_per_pair = p.group < 8 ? p.group : 8;
   p.n_pairs = n_kv_head * ((p.group + p.heads_per_pair - 1) / p.heads_per_pair);
 
-  const size_t rows = (size_t)batch * n_head * p.max_splits;
+  const size_t rows = (size_t)batch * n_head * p.max_slots;
   char* ws = (char*)workspace;
   p.ws_ml = (float*)ws;
   ws += round256(rows * 2 * sizeof(float));
