@@ -193,6 +193,97 @@ def bench_decode(cfg, steps, warmup, replicas=1, cpu=True, split=0):
     return res
 
 
+# ---------------------------------------------------------------------------
+# projections (tl_gemm): the model step's plain GEMMs
+# ---------------------------------------------------------------------------
+
+GEMM_MODELS = {
+    # name: (n_embd, q, kv, intermediate) -- projection widths of the model
+    "smollm2-360m": (960, 960, 320, 2560),
+    "llama3.2-3b": (3072, 3072, 1024, 8192),
+}
+FP32_PEAK_TFLOPS = 157.3
+
+
+def bench_gemm(steps, warmup, cpu=True, models=("llama3.2-3b", "smollm2-360m"), prompt=2048):
+    """Time every projection of one layer (q, k, v, o, gate, up, down) of
+    each model for one decoded token (M = 1, weight-bandwidth bound) and for
+    a prompt (M = prompt, MFMA bound), fp32 as the reference runs them and
+    bf16.  Weights rotate over replicas totalling >= 1 GB so each call reads
+    them from HBM, not MALL.  The CPU baseline is NumPy float32 matmul on
+    the host (a bounded sample: one pass per shape, M = 1 and 128)."""
+    from triton_llm import gpu
+    from triton_llm.kernels import gemm
+
+    lib = gpu.runtime()
+    rows = []
+    for model in models:
+        e, q, kv, inter = GEMM_MODELS[model]
+        shapes = [("q", e, q), ("k", e, kv), ("v", e, kv), ("o", q, e), ("gate", e, inter), ("up", e, inter), ("down", inter, e)]
+        for dt, gdt, esz, peak in (("float32", np.float32, 4, FP32_PEAK_TFLOPS), ("bfloat16", gpu.bfloat16, 2, PEAK_TFLOPS["bfloat16"])):
+            acc = {M: [0.0, 0, 0] for M in (1, prompt)}  # ms, flops, bytes per layer
+            for name, K, N in shapes:
+                wbytes = K * N * esz
+                rng = np.random.default_rng(K + N)
+                wh = rng.standard_normal((K, N), dtype=np.float32)
+                if dt == "bfloat16":
+                    wh = (wh.view(np.uint32) >> 16).astype(np.uint16)
+                w0 = gpu.to_device(wh, gdt)
+                for M in (1, prompt):
+                    # one token reads the whole weight: rotate copies past MALL
+                    reps = max(1, int(np.ceil(1e9 / wbytes))) if M == 1 else 1
+                    ws = [w0]
+                    for _ in range(reps - 1):
+                        w = gpu.allocate((K, N), gdt)
+                        gpu.copy_(w, w0)
+                        ws.append(w)
+                    hh = rng.standard_normal((M, K), dtype=np.float32)
+                    if dt == "bfloat16":
+                        hh = (hh.view(np.uint32) >> 16).astype(np.uint16)
+                    h = gpu.to_device(hh, gdt)
+                    out = gpu.allocate((M, N), gdt)
+                    for i in range(warmup):
+                        gemm(h, ws[i % reps], out_dev=out)
+                    ev = Events(lib, 2)
+                    ev.record(0)
+                    for i in range(steps):
+                        gemm(h, ws[i % reps], out_dev=out)
+                    ev.record(1)
+                    ms = ev.ms(0, 1) / steps
+                    ev.close()
+                    acc[M][0] += ms
+                    acc[M][1] += 2 * M * K * N
+                    acc[M][2] += wbytes + (M * K + M * N) * esz
+                    del ws
+            for M, (tot_ms, tot_flops, tot_bytes) in acc.items():
+                rows.append({
+                    "model": model, "dtype": dt, "M": M, "ms_per_layer": tot_ms,
+                    "tflops": tot_flops / (tot_ms * 1e-3) / 1e12, "frac_mfma": tot_flops / (tot_ms * 1e-3) / 1e12 / peak,
+                    "gbs": tot_bytes / (tot_ms * 1e-3) / 1e9, "frac_hbm": tot_bytes / (tot_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                })
+                log(f"gemm {model} {dt} M={M}: {tot_ms*1e3:.1f} us/layer, {rows[-1]['tflops']:.1f} TFLOP/s, {rows[-1]['gbs']:.0f} GB/s")
+    res = {"metric": "projection GEMMs per layer (tl_gemm, rocBLAS)", "rows": rows}
+    if cpu:
+        cpu_rows = []
+        for model in models:
+            e, q, kv, inter = GEMM_MODELS[model]
+            shapes = [(e, q), (e, kv), (e, kv), (q, e), (e, inter), (e, inter), (inter, e)]
+            for M in (1, 128):
+                t = 0.0
+                flops = 0
+                for K, N in shapes:
+                    a = np.random.standard_normal((M, K)).astype(np.float32)
+                    b = np.random.standard_normal((K, N)).astype(np.float32)
+                    t0 = time.perf_counter()
+                    a @ b
+                    t += time.perf_counter() - t0
+                    flops += 2 * M * K * N
+                cpu_rows.append({"model": model, "dtype": "float32", "M": M, "ms_per_layer": t * 1e3, "tflops": flops / t / 1e12})
+        res["cpu_baseline"] = {"rows": cpu_rows, "cores": cpu_threads(), "host": cpu_host(), "kind": "numpy",
+                               "sample": "one pass per projection shape, M = 1 and 128"}
+    return res
+
+
 def cpu_decode_baseline(cfg, data, oa, on, budget_s=10.0):
     """NumPy fp32 decode attention over every sequence of the workload,
     repeated until ``budget_s`` of CPU time; the median pass is reported."""
@@ -359,6 +450,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--config", default="5")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--gemm", action="store_true",
+                    help="time the model's projection GEMMs (tl_gemm) instead of attention")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="only run 5 device-to-device copies of this many MiB (the known-size "
                          "reference for calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -379,6 +472,9 @@ def main():
         copy_probe(args.copy_probe_mb)
         return
     cpu = not args.no_cpu
+    if args.gemm:
+        print(json.dumps(bench_gemm(min(args.steps, 20), min(args.warmup, 5), cpu=cpu)))
+        return
     sel = {"5": ["5a", "5b"], "all": ["1", "2", "3", "4", "5a", "5b"]}.get(args.config, [args.config])
     results = {}
     for name in sel:

@@ -156,6 +156,24 @@ int tl_rope_kv_append(void* q, const void* k_new, const void* v_new,
                       const int64_t* k_cache_strides,
                       const int64_t* v_cache_strides, int dtype, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Dense projection GEMM of the model step (the row SURVEY lists after the
+ * attention path): C = A . B, row-major, A (m, k) with row stride lda, B
+ * (k, n) with ldb, C (m, n) with ldc, all of one dtype, fp32 accumulation.
+ * Replaces the Triton GEMM gemm(h_dev, w_dev, out_dev)
+ * (triton_llm/kernels/gemm.py:53-108) used for every projection in
+ * gpt2_triton/model.py and smollm2_triton/model.py (e.g. :285-287, :351,
+ * :360-363, :375).  k = 0 writes zeros; m = 0 or n = 0 does nothing.
+ * m <= 8 (a decoded token) runs a hand-written HBM-streaming kernel whose
+ * K-slice partial sums need tl_gemm_workspace_bytes(m, n, k, dtype) bytes of
+ * workspace (0 otherwise); larger m goes to rocBLAS (one handle per device,
+ * created on first use, which holds rocBLAS's own workspace).
+ * ------------------------------------------------------------------------- */
+size_t tl_gemm_workspace_bytes(int m, int n, int k, int dtype);
+int tl_gemm(const void* a, const void* b, void* c, int m, int n, int k, int64_t lda,
+            int64_t ldb, int64_t ldc, void* workspace, size_t workspace_bytes, int dtype,
+            void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,99 @@
+"""The model's projection GEMM against the oracle (oracle/gemm.py), on the
+reference's own cases (tests/test_gemm.py of the reference: seeded shapes,
+non-block-aligned shapes, empty dimensions, mismatched K) and on the
+projection shapes of SmolLM2-360M and Llama-3.2-3B for one decoded token,
+a few tokens (the hand-written streaming kernel, up to 8 rows) and a short
+prompt (rocBLAS).  Tolerances: fp32 2e-3 max-abs (the reference's own
+bar is allclose(rtol 1e-2, atol 5e-2)); 16-bit outputs within their
+rounding, rtol 8e-3 + atol 1e-2.
+"""
+
+import time
+
+import numpy as np
+import pytest
+
+from oracle import numerics as on
+from oracle.gemm import gemm_ref
+from tests import _helpers as H
+from triton_llm import gpu
+from triton_llm.kernels import gemm
+
+pytestmark = pytest.mark.gpu
+
+
+def gemm_cpu(a, b, dtype="float32"):
+    return H.download(gemm(H.upload(a, dtype), H.upload(b, dtype)))
+
+
+@pytest.mark.parametrize("M,K,N", [(64, 128, 32), (128, 256, 128), (256, 512, 256), (65, 130, 33), (100, 200, 150)])
+def test_gemm_reference_cases(M, K, N):
+    np.random.seed(42)
+    a = np.random.randn(M, K).astype(np.float32)
+    b = np.random.randn(K, N).astype(np.float32)
+    out = gemm_cpu(a, b)
+    assert np.allclose(out, a @ b, rtol=1e-2, atol=5e-2)
+    err = H.max_abs(out, gemm_ref(a, b))
+    H.report(f"gemm {M}x{K}@{K}x{N}", err, 2e-3)
+    assert err <= 2e-3
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
+@pytest.mark.parametrize("M", [1, 3, 8, 37])
+@pytest.mark.parametrize("K,N", [(960, 960), (960, 320), (960, 2560), (2560, 960), (3072, 1024), (8192, 3072)])
+def test_gemm_projection_shapes(dtype, M, K, N):
+    rng = np.random.default_rng(K * 7 + N + M)
+    a = on.to_storage(rng.standard_normal((M, K), dtype=np.float32), dtype)
+    b = on.to_storage(rng.standard_normal((K, N), dtype=np.float32) / np.sqrt(K), dtype)
+    got = on.from_storage(gemm_cpu(a, b, dtype), dtype)
+    exp = gemm_ref(on.from_storage(a, dtype), on.from_storage(b, dtype))
+    if dtype == "float32":
+        err = H.max_abs(got, exp)
+        H.report(f"{dtype} {M}x{K}@{K}x{N}", err, 2e-3)
+        assert err <= 2e-3
+    else:
+        np.testing.assert_allclose(got, exp, rtol=8e-3, atol=1e-2)
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 130, 33), (2, 7, 40), (5, 1000, 100), (8, 4100, 260)])
+def test_gemm_few_rows_odd_shapes(M, K, N):
+    """Few-row products on shapes the streaming kernel handles partly (a
+    ragged last K-slice or column tile) or not at all (N not a multiple of
+    the 16-byte chunk: rocBLAS), against the oracle."""
+    rng = np.random.default_rng(M * 1000 + K + N)
+    a = rng.standard_normal((M, K), dtype=np.float32)
+    b = rng.standard_normal((K, N), dtype=np.float32)
+    err = H.max_abs(gemm_cpu(a, b), gemm_ref(a, b))
+    H.report(f"few rows {M}x{K}@{K}x{N}", err, 2e-3)
+    assert err <= 2e-3
+
+
+def test_gemm_edge_cases():
+    # K = 0: zeros of shape (M, N) (the reference only checks the shape)
+    out = gemm_cpu(np.zeros((10, 0), np.float32), np.zeros((0, 10), np.float32))
+    assert out.shape == (10, 10) and not out.any()
+    assert gemm_cpu(np.zeros((0, 20), np.float32), np.ones((20, 10), np.float32)).shape == (0, 10)
+    assert gemm_cpu(np.ones((10, 20), np.float32), np.zeros((20, 0), np.float32)).shape == (10, 0)
+    with pytest.raises(AssertionError):
+        gemm(gpu.to_device(np.ones((10, 20), np.float32)), gpu.to_device(np.ones((30, 10), np.float32)))
+    with pytest.raises(AssertionError):
+        gemm(gpu.to_device(np.ones((10, 20), np.float32)), gpu.to_device(np.ones((20, 10), np.float32)),
+             out_dev=gpu.allocate((10, 11), np.float32))
+    # a given output is written in place
+    a, b = np.random.randn(33, 17).astype(np.float32), np.random.randn(17, 5).astype(np.float32)
+    out = gpu.allocate((33, 5), np.float32)
+    assert gemm(gpu.to_device(a), gpu.to_device(b), out_dev=out) is out
+    assert H.max_abs(H.download(out), gemm_ref(a, b)) <= 2e-3
+
+
+def test_gemm_reference_performance_bound():
+    """The reference's performance test: 512x1024 @ 1024x512 under 50 ms
+    per call including the copies."""
+    a = np.random.randn(512, 1024).astype(np.float32)
+    b = np.random.randn(1024, 512).astype(np.float32)
+    for _ in range(3):
+        gemm_cpu(a, b)
+    t0 = time.perf_counter()
+    for _ in range(10):
+        gemm_cpu(a, b)
+    assert (time.perf_counter() - t0) / 10 * 1e3 < 50

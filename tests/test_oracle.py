@@ -321,3 +321,20 @@ def test_small_decode_inputs_shapes_and_poison():
         L = d["lens"][b]
         assert np.all(d["k_cache"][b, :, L:] == 0x7FC0)
         assert not np.any(d["k_cache"][b, :, :L] == 0x7FC0)
+
+
+def test_gemm_ref_pins():
+    """gemm_ref against facts a transposed operand or dropped term would break."""
+    from oracle.gemm import gemm_ref
+
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal((7, 5)).astype(np.float32)
+    b = rng.standard_normal((5, 9)).astype(np.float32)
+    np.testing.assert_array_equal(gemm_ref(np.eye(7, dtype=np.float32), a), a)
+    np.testing.assert_array_equal(gemm_ref(a, np.eye(5, dtype=np.float32)), a)
+    u, v = rng.standard_normal((6, 1)), rng.standard_normal((1, 4))
+    np.testing.assert_allclose(gemm_ref(u, v), u * v, rtol=1e-6)  # rank one: outer product
+    x = rng.standard_normal(9)
+    np.testing.assert_allclose(gemm_ref(a, b) @ x, a.astype(np.float64) @ (b.astype(np.float64) @ x), rtol=1e-5, atol=1e-5)
+    assert gemm_ref(np.zeros((3, 0)), np.zeros((0, 4))).shape == (3, 4)
+    assert not gemm_ref(np.zeros((3, 0)), np.zeros((0, 4))).any()

@@ -40,6 +40,11 @@ HIPCC_FLAGS = [
 ]
 
 
+# rocBLAS carries the model's plain projection GEMMs (tl_gemm.hip).
+ROCM_LIB = "/opt/rocm/lib"
+LINK_LIBS = [f"-L{ROCM_LIB}", "-lrocblas", f"-Wl,-rpath,{ROCM_LIB}"]
+
+
 def _hipcc() -> str:
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not os.path.exists(path):
@@ -78,7 +83,8 @@ def build(verbose: bool = True, jobs: int | None = None) -> str:
             for f in futs:
                 f.result()
         tmp_lib = LIB_PATH + ".tmp"
-        cmd = [_hipcc(), f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC", *objs, "-o", tmp_lib]
+        cmd = [_hipcc(), f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC", *objs, "-o", tmp_lib,
+               *LINK_LIBS]
         res = subprocess.run(cmd, capture_output=True, text=True)
         if res.returncode != 0:
             raise RuntimeError(f"link failed:\n{res.stderr}")

@@ -70,6 +70,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
          _i64p, _i64p, _i64p, _i64p, _i64p, _c_int, _vp],
     ),
+    "tl_gemm_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
+    "tl_gemm": (
+        _c_int,
+        [_vp, _vp, _vp, _c_int, _c_int, _c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+         _vp, _c_size, _c_int, _vp],
+    ),
 }
 
 _lib: ctypes.CDLL | None = None
