@@ -263,6 +263,7 @@ def bench_gemm(steps, warmup, cpu=True, models=("llama3.2-3b", "smollm2-360m"), 
                 })
                 log(f"gemm {model} {dt} M={M}: {tot_ms*1e3:.1f} us/layer, {rows[-1]['tflops']:.1f} TFLOP/s, {rows[-1]['gbs']:.0f} GB/s")
     res = {"metric": "projection GEMMs per layer (tl_gemm, rocBLAS)", "rows": rows}
+    res["layers"] = bench_layers(steps, warmup)
     if cpu:
         cpu_rows = []
         for model in models:
@@ -282,6 +283,41 @@ def bench_gemm(steps, warmup, cpu=True, models=("llama3.2-3b", "smollm2-360m"), 
         res["cpu_baseline"] = {"rows": cpu_rows, "cores": cpu_threads(), "host": cpu_host(), "kind": "numpy",
                                "sample": "one pass per projection shape, M = 1 and 128"}
     return res
+
+
+def bench_layers(steps, warmup, rows=2048, e=3072, inter=8192):
+    """RMSNorm, fused add + RMSNorm, SwiGLU and add at a Llama-3.2-3B prompt's
+    size (fp32): algorithmic bytes (every input read once, every output
+    written once) per event-timed call, against 8 TB/s."""
+    from triton_llm import gpu
+    from triton_llm.kernels import add, add_rms_norm, rms_norm, swiglu
+
+    lib = gpu.runtime()
+    rng = np.random.default_rng(0)
+    dev = lambda *shape: gpu.to_device(rng.standard_normal(shape, dtype=np.float32))  # noqa: E731
+    a, b, w = dev(rows, e), dev(rows, e), dev(e)
+    h, y = gpu.allocate((rows, e), np.float32), gpu.allocate((rows, e), np.float32)
+    g, u, o = dev(rows, inter), dev(rows, inter), gpu.allocate((rows, inter), np.float32)
+    n, ni = rows * e * 4, rows * inter * 4
+    cases = [("rms_norm", lambda: rms_norm(a, w, y), 2 * n),
+             ("add_rms_norm", lambda: add_rms_norm(a, b, h, w, y), 4 * n),
+             ("swiglu", lambda: swiglu(g, u, o), 3 * ni),
+             ("add", lambda: add(a, b, h), 3 * n)]
+    out = []
+    for name, fn, nbytes in cases:
+        for _ in range(warmup):
+            fn()
+        ev = Events(lib, 2)
+        ev.record(0)
+        for _ in range(steps):
+            fn()
+        ev.record(1)
+        ms = ev.ms(0, 1) / steps
+        ev.close()
+        out.append({"op": name, "shape": [rows, inter if name == "swiglu" else e], "us": ms * 1e3,
+                    "gbs": nbytes / (ms * 1e-3) / 1e9, "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS})
+        log(f"{name}: {ms * 1e3:.1f} us, {out[-1]['gbs']:.0f} GB/s")
+    return out
 
 
 def cpu_decode_baseline(cfg, data, oa, on, budget_s=10.0):

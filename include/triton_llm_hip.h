@@ -174,6 +174,28 @@ int tl_gemm(const void* a, const void* b, void* c, int m, int n, int k, int64_t 
             int64_t ldb, int64_t ldc, void* workspace, size_t workspace_bytes, int dtype,
             void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Layers around the projections, contiguous rows, fp32 math in any dtype.
+ *   tl_rms_norm: y = (x / sqrt(mean(x^2) + eps)) * w per row of n; replaces
+ *     rms_norm(x_dev, w_dev, out_dev, eps) (triton_llm/kernels/rms_norm.py:68-116).
+ *   tl_add_rms_norm: h = a + b, then y = rms_norm(h) (the residual add and
+ *     the next RMSNorm of smollm2_triton/model.py:352-357 / :279-280 in one
+ *     pass; h is written, and normalised as stored).  No reference
+ *     counterpart as one call: it fuses add.py:54-104 with rms_norm.py.
+ *   tl_swiglu: out = silu(gate) * up, count elements; replaces
+ *     swiglu(gate_dev, up_dev, out_dev) (triton_llm/kernels/swiglu.py:70-125).
+ *   tl_add: z = x + y, count elements; replaces add(x_dev, y_dev, out_dev)
+ *     (triton_llm/kernels/add.py:54-104).
+ * m = 0 or count = 0 does nothing; n = 0 rows are an error, as in rms_norm.py:96-97.
+ * ------------------------------------------------------------------------- */
+int tl_rms_norm(const void* x, const void* w, void* y, int m, int n, float eps, int dtype,
+                void* stream);
+int tl_add_rms_norm(const void* a, const void* b, void* h, const void* w, void* y, int m,
+                    int n, float eps, int dtype, void* stream);
+int tl_swiglu(const void* gate, const void* up, void* out, int64_t count, int dtype,
+              void* stream);
+int tl_add(const void* x, const void* y, void* z, int64_t count, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -338,3 +338,32 @@ def test_gemm_ref_pins():
     np.testing.assert_allclose(gemm_ref(a, b) @ x, a.astype(np.float64) @ (b.astype(np.float64) @ x), rtol=1e-5, atol=1e-5)
     assert gemm_ref(np.zeros((3, 0)), np.zeros((0, 4))).shape == (3, 4)
     assert not gemm_ref(np.zeros((3, 0)), np.zeros((0, 4))).any()
+
+
+def test_layers_ref_pins():
+    """rms_norm_ref / swiglu_ref / decoder_layer_ref against invariants a wrong
+    axis, a dropped term or a sign slip would break."""
+    from oracle import layers as ol
+
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((5, 96)).astype(np.float32)
+    w = rng.standard_normal(96).astype(np.float32)
+    y1 = ol.rms_norm_ref(x, w, eps=0.0)
+    np.testing.assert_allclose(ol.rms_norm_ref(7.5 * x, w, eps=0.0), y1, rtol=1e-5, atol=1e-6)  # scale invariant
+    unit = ol.rms_norm_ref(x, np.ones(96), eps=0.0).astype(np.float64)
+    np.testing.assert_allclose(np.sqrt(np.mean(unit * unit, axis=-1)), 1.0, rtol=1e-6)  # unit RMS per row
+    assert not ol.rms_norm_ref(np.zeros((2, 8)), np.ones(8)).any()  # zeros stay zero (eps > 0)
+    g = np.array([0.0, 40.0, -40.0, 1.0], np.float32)
+    u = np.array([3.0, 2.0, 5.0, 1.0], np.float32)
+    s = ol.swiglu_ref(g, u)
+    assert s[0] == 0.0 and abs(s[1] - 80.0) < 1e-4 and abs(s[2]) < 1e-12
+    np.testing.assert_allclose(s[3], 1.0 / (1.0 + np.exp(-1.0)), rtol=1e-6)  # silu(1) = sigmoid(1)
+    # Zero weights: attention and MLP add nothing, the layer returns its input.
+    E, H, Hkv, D, I, S = 32, 4, 2, 8, 48, 6
+    zw = {"ln1": np.ones(E, np.float32), "ln2": np.ones(E, np.float32), "q": np.zeros((E, H * D)), "k": np.zeros((E, Hkv * D)),
+          "v": np.zeros((E, Hkv * D)), "o": np.zeros((H * D, E)), "gate": np.zeros((E, I)), "up": np.zeros((E, I)),
+          "down": np.zeros((I, E))}
+    cache = {"k": np.zeros((Hkv, 16, D), np.float32), "v": np.zeros((Hkv, 16, D), np.float32)}
+    cos, sin = orope.precompute_cos_sin(16, D, 1e4)
+    h = rng.standard_normal((S, E)).astype(np.float32)
+    np.testing.assert_array_equal(ol.decoder_layer_ref(h, zw, cache, 0, cos, sin, H, Hkv), h)

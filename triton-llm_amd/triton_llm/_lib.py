@@ -70,6 +70,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
          _i64p, _i64p, _i64p, _i64p, _i64p, _c_int, _vp],
     ),
+    "tl_rms_norm": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_float, _c_int, _vp]),
+    "tl_add_rms_norm": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_float, _c_int, _vp]),
+    "tl_swiglu": (_c_int, [_vp, _vp, _vp, ctypes.c_int64, _c_int, _vp]),
+    "tl_add": (_c_int, [_vp, _vp, _vp, ctypes.c_int64, _c_int, _vp]),
     "tl_gemm_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
     "tl_gemm": (
         _c_int,

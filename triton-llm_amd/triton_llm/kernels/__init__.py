@@ -3,10 +3,11 @@
 Exports the reference's hot-path names (triton_llm/kernels/__init__.py:6-31 of
 ziliangpeng/triton-llm: ``attention``, ``attention_gqa``, ``precompute_cos_sin``,
 ``apply_rope``) plus the additive batched entry points of this build
-(flash prefill, KV-cache append, split-K decode) and the model's projection
-``gemm`` (rocBLAS-backed).  The reference's other kernels (add, gelu,
-layer_norm, rms_norm, softmax, swiglu, embedding) are outside this library's
-scope.
+(flash prefill, KV-cache append, split-K decode) and the model step's other
+layers: the projection ``gemm``, ``rms_norm`` (plus the fused
+``add_rms_norm``), ``swiglu`` and ``add``.  The reference's gelu,
+layer_norm, softmax and embedding kernels (GPT-2 and host-side pieces) are
+outside this library's scope.
 """
 
 from .attention import attention
@@ -14,6 +15,9 @@ from .attention_gqa import attention_gqa
 from .rope import apply_rope, precompute_cos_sin, precompute_cos_sin_device
 from .flash import flash_attention, flash_attention_strided
 from .gemm import gemm
+from .rms_norm import add_rms_norm, rms_norm
+from .swiglu import swiglu
+from .add import add
 from .decode import (
     allocate_kv_cache,
     attention_decode,
@@ -36,4 +40,8 @@ __all__ = [
     "decode_step",
     "decode_workspace",
     "gemm",
+    "rms_norm",
+    "add_rms_norm",
+    "swiglu",
+    "add",
 ]
