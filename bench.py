@@ -264,6 +264,7 @@ def bench_gemm(steps, warmup, cpu=True, models=("llama3.2-3b", "smollm2-360m"), 
                 log(f"gemm {model} {dt} M={M}: {tot_ms*1e3:.1f} us/layer, {rows[-1]['tflops']:.1f} TFLOP/s, {rows[-1]['gbs']:.0f} GB/s")
     res = {"metric": "projection GEMMs per layer (tl_gemm, rocBLAS)", "rows": rows}
     res["layers"] = bench_layers(steps, warmup)
+    res["sample"] = bench_sample(steps, warmup, cpu=cpu)
     if cpu:
         cpu_rows = []
         for model in models:
@@ -474,6 +475,70 @@ def copy_probe(mib):
         assert lib.tl_memcpy_dtod(dst.ptr, src.ptr, n) == 0
     gpu.synchronize()
     print(json.dumps({"copy_probe_bytes": n, "copies": 5}))
+
+
+def bench_sample(steps, warmup, cpu=True, vocabs=(49152, 128256)):
+    """Next-token sampling (tl_sample) on fp32 logits at SmolLM2's and
+    Llama-3.2's vocabularies: event-timed kernel time per call for 1 and 64
+    rows, greedy / temperature 0.8 / temperature 0.8 with top_k 50, and the
+    wall time of one ``sample()`` per token from Python (draw upload, kernel,
+    token download).  Algorithmic bytes: the logits read once.  The CPU
+    baseline is the reference's host ``_sample`` (NumPy) on one row, without
+    the logits download it also needs."""
+    from oracle import sample as osm
+    from triton_llm import gpu
+    from triton_llm.kernels import sample, sample_rows
+
+    lib = gpu.runtime()
+    rng = np.random.default_rng(0)
+    modes = (("greedy", 0.0, 0), ("t0.8", 0.8, 0), ("t0.8_k50", 0.8, 50))
+    out = []
+    for V in vocabs:
+        for rows in (1, 64):
+            x = gpu.to_device((3.0 * rng.standard_normal((rows, V))).astype(np.float32))
+            u = gpu.to_device(rng.random(rows))
+            tok = gpu.allocate((rows,), np.int32)
+            for name, T, k in modes:
+                for _ in range(warmup):
+                    sample_rows(x, T, k, uniforms=u, out_dev=tok)
+                ev = Events(lib, 2)
+                ev.record(0)
+                for _ in range(steps):
+                    sample_rows(x, T, k, uniforms=u, out_dev=tok)
+                ev.record(1)
+                ms = ev.ms(0, 1) / steps
+                ev.close()
+                nbytes = rows * V * 4
+                out.append({"vocab": V, "rows": rows, "mode": name, "us": ms * 1e3,
+                            "gbs": nbytes / (ms * 1e-3) / 1e9})
+                log(f"sample V={V} rows={rows} {name}: {ms * 1e3:.1f} us")
+        x1 = gpu.to_device((3.0 * rng.standard_normal((1, V))).astype(np.float32))
+        for name, T, k in modes:
+            for _ in range(5):
+                sample(x1, T, k)
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                sample(x1, T, k)
+            us = (time.perf_counter() - t0) / steps * 1e6
+            out.append({"vocab": V, "rows": 1, "mode": name, "python_call_us": us})
+            log(f"sample() V={V} {name}: {us:.1f} us per token from Python")
+    res = {"metric": "next-token sampling (tl_sample)", "rows": out}
+    if cpu:
+        cpu_rows = []
+        for V in vocabs:
+            row = (3.0 * rng.standard_normal(V)).astype(np.float32)
+            for name, T, k in modes:
+                n = 50
+                t0 = time.perf_counter()
+                for _ in range(n):
+                    if T > 0:
+                        np.random.choice(V, p=osm.probs_ref(row, T, k))
+                    else:
+                        np.argmax(row)
+                cpu_rows.append({"vocab": V, "mode": name, "us": (time.perf_counter() - t0) / n * 1e6})
+        res["cpu_baseline"] = {"rows": cpu_rows, "cores": 1, "kind": "port",
+                               "sample": "the reference's _sample on one host row, 50 calls per case"}
+    return res
 
 
 def main():

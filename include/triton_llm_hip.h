@@ -196,6 +196,27 @@ int tl_swiglu(const void* gate, const void* up, void* out, int64_t count, int dt
               void* stream);
 int tl_add(const void* x, const void* y, void* z, int64_t count, int dtype, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Next-token sampling, one token per row of logits [rows][row_stride]
+ * (vocab valid entries per row); replaces SmolLM2._sample
+ * (smollm2_triton/model.py:566-584; GPT-2: gpt2_triton/model.py:424-438),
+ * which runs on the host after downloading the logits.
+ *   temperature <= 0: tokens[r] = first index of the row's maximum (np.argmax;
+ *     a NaN counts as the maximum).  uniforms may be NULL.
+ *   temperature > 0: p = exp(x / T - max / T); 0 < top_k < vocab keeps every
+ *     entry >= the top_k-th largest logit (ties with it all kept); tokens[r] =
+ *     first index whose cumulative kept mass exceeds uniforms[r] * total, the
+ *     inverse CDF np.random.choice applies to its uniform draw.  A row whose
+ *     mass is not a positive finite number (NaN / +inf logits, all -inf) gets
+ *     -1, where the reference's np.random.choice raises ValueError.
+ * The reference's 1e-6 greedy cut-off is the caller's (compare in double,
+ * pass 0 for greedy).  1 <= vocab <= tl_sample_max_vocab(), row_stride >=
+ * vocab, top_k >= 0 (0 keeps all); rows = 0 does nothing.
+ * ------------------------------------------------------------------------- */
+int tl_sample_max_vocab(void);
+int tl_sample(const void* logits, int rows, int vocab, int64_t row_stride, float temperature,
+              int top_k, const double* uniforms, int32_t* tokens, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,229 @@
+"""On-device next-token sampling (tl_sample) against the oracle's restatement
+of the reference's ``_sample`` (oracle/sample.py).
+
+* greedy: bit-exact ``np.argmax`` (first maximum, NaN first) for fp32, fp16
+  and bf16 storage, vocabularies 1 .. the maximum, ties, -inf rows;
+* sampled: for every row the token equals ``sample_ref``'s for the same
+  uniform draw.  A row may differ only where the draw sits within 1e-5 of a
+  step of the CDF (the device's fp32 exp and NumPy's differ by an ulp, which
+  moves a step by ~1e-7); such rows are counted and must be rare;
+* 16-bit logits tie often: checked against ``sample_kept_ref`` (every logit
+  >= the k-th kept), the device's documented tie rule;
+* the reference's own cases (tests/test_smollm2_model.py:194-218,
+  test_gpt2_kv_cache.py:79-90, test_gpt2_support_matrix.py:149-156): vocab
+  100 / top_k 50 gives valid ids, an oversized top_k is accepted, greedy
+  decoding is deterministic; ``np.random.seed`` repeats a sampled run and
+  gives the reference's own tokens;
+* rows whose probabilities are undefined (NaN, +inf, all -inf) give -1 and
+  ``sample`` raises ValueError as ``np.random.choice`` does.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import numerics as on
+from oracle import sample as osm
+from tests import _helpers as H
+from triton_llm import gpu
+from triton_llm.kernels import sample, sample_rows
+from triton_llm.kernels.sample import max_vocab
+
+pytestmark = pytest.mark.gpu
+
+STEP_MARGIN = 1e-5
+
+
+def run_rows(x_store, dtype, T, k, u):
+    """tokens for host logits storage (rows, V) with draws u."""
+    dev = H.upload(x_store, dtype)
+    out = sample_rows(dev, T, k, uniforms=u)
+    gpu.synchronize()
+    return out.to_numpy()
+
+
+def logits_f32(x_store, dtype):
+    return on.from_storage(x_store, dtype).astype(np.float32)
+
+
+def compare(x, T, k, u, got, keep_ties=False):
+    """count real mismatches and draws on a CDF step."""
+    ref = osm.sample_kept_ref if keep_ties else osm.sample_ref
+    bad, near = [], 0
+    for r in range(x.shape[0]):
+        want = ref(x[r], T, k, u[r])
+        if got[r] != want:
+            if osm.crossing_margin(x[r], T, k, u[r], keep_ties) < STEP_MARGIN:
+                near += 1
+            else:
+                bad.append((r, int(got[r]), want))
+    return bad, near
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+@pytest.mark.parametrize("V", [1, 2, 100, 1023, 1024, 1025, 4097, 49152, 128256])
+def test_greedy_is_argmax(dtype, V):
+    rng = np.random.default_rng(V)
+    rows = 16 if V < 100000 else 4
+    x = (4.0 * rng.standard_normal((rows, V))).astype(np.float32)
+    if V > 2:
+        x[1, :] = 0.5                     # all equal: index 0
+        x[2, V // 3] = x[2, V - 1] = 99.0  # repeated maximum: the first
+        x[3, V - 1] = 99.0                 # maximum at the end
+    store = on.to_storage(x, dtype)
+    got = run_rows(store, dtype, 0.0, 0, None)
+    want = np.argmax(logits_f32(store, dtype), axis=1)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_greedy_nan_inf_rows():
+    V = 3000
+    x = np.random.default_rng(1).standard_normal((5, V)).astype(np.float32)
+    x[0, 17] = x[0, 2000] = np.nan      # first NaN
+    x[1, :] = -np.inf                   # all -inf: 0
+    x[2, 5] = np.inf                    # +inf wins
+    x[3, 9] = np.inf
+    x[3, 4] = np.nan                    # NaN beats +inf
+    got = run_rows(x, "float32", 0.0, 0, None)
+    np.testing.assert_array_equal(got, [np.argmax(r) for r in x])
+    assert got.tolist()[:4] == [17, 0, 5, 4]
+
+
+@pytest.mark.parametrize("V", [2, 100, 1000, 1025, 49152, 128256])
+@pytest.mark.parametrize("T", [0.5, 1.0, 1.7])
+@pytest.mark.parametrize("k", [0, 1, 5, 50, 999999])
+def test_sampled_matches_reference(V, T, k):
+    rng = np.random.default_rng(1000 * V + int(10 * T) + k)
+    rows = 24 if V <= 49152 else 6
+    x = (3.0 * rng.standard_normal((rows, V))).astype(np.float32)
+    u = rng.random(rows)
+    u[0], u[1] = 0.0, 1.0 - 2.0 ** -53
+    got = run_rows(x, "float32", T, k, u)
+    bad, near = compare(x, T, k, u, got)
+    assert not bad, f"V={V} T={T} k={k} mismatches (row, got, want): {bad[:5]}"
+    assert near <= 2
+
+
+def test_top_k_one_is_argmax_and_vocab_edge_k():
+    rng = np.random.default_rng(7)
+    V = 5000
+    x = rng.standard_normal((32, V)).astype(np.float32)
+    got = run_rows(x, "float32", 1.3, 1, rng.random(32))
+    np.testing.assert_array_equal(got, np.argmax(x, axis=1))
+    for k in (V - 1, V, V + 1):
+        u = rng.random(32)
+        bad, near = compare(x, 0.9, k, u, run_rows(x, "float32", 0.9, k, u))
+        assert not bad and near <= 2
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("k", [0, 3, 50, 700])
+def test_sixteen_bit_logits_with_ties(dtype, k):
+    rng = np.random.default_rng(len(dtype) + k)
+    rows, V = 32, 49152
+    store = on.to_storage((2.0 * rng.standard_normal((rows, V))).astype(np.float32), dtype)
+    x = logits_f32(store, dtype)
+    u = rng.random(rows)
+    got = run_rows(store, dtype, 0.8, k, u)
+    for r in range(rows):
+        assert osm.kept_mask(x[r], k)[got[r]]
+    bad, near = compare(x, 0.8, k, u, got, keep_ties=True)
+    assert not bad, f"{dtype} k={k}: {bad[:5]}"
+    assert near <= 2
+
+
+def test_max_vocab_and_strided_rows():
+    V = max_vocab()
+    assert V >= 256000  # the largest vocabularies in use (Gemma: 256000)
+    rng = np.random.default_rng(3)
+    x = (2.0 * rng.standard_normal((3, V))).astype(np.float32)
+    u = rng.random(3)
+    for k in (0, 40):
+        bad, near = compare(x, 1.0, k, u, run_rows(x, "float32", 1.0, k, u))
+        assert not bad and near <= 1
+    # rows padded to a stride above the vocabulary, through the C ABI
+    Vp, stride, rows = 1000, 1024, 8
+    xp = np.full((rows, stride), 1e9, np.float32)  # padding would win if read
+    xp[:, :Vp] = rng.standard_normal((rows, Vp))
+    dev = gpu.to_device(xp)
+    u = rng.random(rows)
+    u_dev = gpu.to_device(u)
+    out = gpu.allocate((rows,), np.int32)
+    lib = gpu.runtime()
+    assert lib.tl_sample(dev.ptr, rows, Vp, stride, 0.0, 0, None, out.ptr, 0, None) == 0
+    gpu.synchronize()
+    np.testing.assert_array_equal(out.to_numpy(), np.argmax(xp[:, :Vp], axis=1))
+    assert lib.tl_sample(dev.ptr, rows, Vp, stride, 1.0, 10, u_dev.ptr, out.ptr, 0, None) == 0
+    gpu.synchronize()
+    bad, near = compare(xp[:, :Vp], 1.0, 10, u, out.to_numpy())
+    assert not bad and near <= 1
+
+
+def test_undefined_probabilities():
+    V = 2000
+    x = np.random.default_rng(5).standard_normal((4, V)).astype(np.float32)
+    x[0, 10] = np.nan
+    x[1, 20] = np.inf
+    x[2, :] = -np.inf
+    got = run_rows(x, "float32", 1.0, 0, np.full(4, 0.5))
+    assert got[:3].tolist() == [-1, -1, -1] and 0 <= got[3] < V
+    for r in range(3):
+        with pytest.raises(ValueError, match="NaN"):
+            sample(gpu.to_device(x[r]), 1.0, 0)
+        with pytest.raises(ValueError):  # the reference raises on the same rows
+            np.random.choice(V, p=osm.probs_ref(x[r], 1.0, 0))
+
+
+def test_reference_model_sampling_contract():
+    """vocab 100, temperature 1, top_k 50 / oversized top_k: valid ids;
+    greedy twice: identical; seeded runs repeat and match the reference."""
+    rng = np.random.default_rng(42)
+    V = 100
+    x = rng.standard_normal((1, 3, V)).astype(np.float32)  # (batch, seq, vocab) logits
+    dev = gpu.to_device(x)
+    for k in (50, 999999, 0):
+        toks = [sample(dev, 1.0, k) for _ in range(200)]
+        assert all(0 <= t < V for t in toks)
+    assert sample(dev, 0.0, 0) == sample(dev, 0.0, 0) == int(np.argmax(x[0, -1]))
+    assert sample(dev, 0.0, 0, row=0) == int(np.argmax(x[0, 0]))
+    for seed in (0, 1, 2, 123):
+        np.random.seed(seed)
+        got = [sample(dev, 0.8, 20) for _ in range(40)]
+        np.random.seed(seed)
+        again = [sample(dev, 0.8, 20) for _ in range(40)]
+        assert got == again
+        np.random.seed(seed)  # the reference's own draws: np.random.choice
+        want = [int(np.random.choice(V, p=osm.probs_ref(x[0, -1], 0.8, 20))) for _ in range(40)]
+        assert sum(g != w for g, w in zip(got, want)) <= 1
+    # greedy consumes no draw, as in the reference
+    np.random.seed(9)
+    sample(dev, 0.0, 5)
+    assert np.random.random_sample() == np.random.RandomState(9).random_sample()
+
+
+def test_distribution_of_many_draws():
+    rng = np.random.default_rng(8)
+    V, rows = 10, 8192
+    x = np.tile(rng.standard_normal(V).astype(np.float32), (rows, 1))
+    got = run_rows(x, "float32", 0.7, 6, rng.random(rows))
+    freq = np.bincount(got, minlength=V) / rows
+    np.testing.assert_allclose(freq, osm.probs_ref(x[0], 0.7, 6), atol=0.02)
+
+
+def test_argument_errors():
+    lib = gpu.runtime()
+    dev = gpu.to_device(np.zeros((2, 8), np.float32))
+    out = gpu.allocate((2,), np.int32)
+    u = gpu.to_device(np.zeros(2))
+    assert lib.tl_sample(dev.ptr, 2, 0, 8, 1.0, 0, u.ptr, out.ptr, 0, None) != 0          # vocab 0
+    assert lib.tl_sample(dev.ptr, 2, 8, 4, 1.0, 0, u.ptr, out.ptr, 0, None) != 0          # stride < vocab
+    assert lib.tl_sample(dev.ptr, 2, 8, 8, 1.0, -1, u.ptr, out.ptr, 0, None) != 0         # top_k < 0
+    assert lib.tl_sample(dev.ptr, 2, 8, 8, 1.0, 0, ctypes.c_void_p(None), out.ptr, 0, None) != 0  # no draws
+    assert lib.tl_sample(dev.ptr, 2, max_vocab() + 1, max_vocab() + 1, 0.0, 0, None, out.ptr, 0, None) != 0
+    assert lib.tl_sample(dev.ptr, 2, 8, 8, 1.0, 0, u.ptr, out.ptr, 7, None) != 0          # dtype
+    assert lib.tl_sample(dev.ptr, 0, 8, 8, 1.0, 0, u.ptr, out.ptr, 0, None) == 0          # no rows
+    with pytest.raises(ValueError):
+        sample_rows(dev, 1.0, 0, uniforms=np.zeros(3))
+    with pytest.raises(IndexError):
+        sample(dev, 1.0, 0, row=2)

@@ -367,3 +367,55 @@ def test_layers_ref_pins():
     cos, sin = orope.precompute_cos_sin(16, D, 1e4)
     h = rng.standard_normal((S, E)).astype(np.float32)
     np.testing.assert_array_equal(ol.decoder_layer_ref(h, zw, cache, 0, cos, sin, H, Hkv), h)
+
+
+def test_sample_ref_pins():
+    """sample_ref against np.random.choice / np.argmax themselves, plus the
+    softmax closed form and the empirical distribution of many draws."""
+    from scipy.special import softmax
+
+    from oracle import sample as osm
+
+    rng = np.random.default_rng(11)
+    for V in (1, 2, 100, 5000):
+        x = (3.0 * rng.standard_normal(V)).astype(np.float32)
+        for T in (0.5, 1.0, 1.7):
+            # probabilities: softmax(x / T) from the library
+            np.testing.assert_allclose(osm.probs_ref(x, T, 0), softmax(x.astype(np.float64) / np.float32(T)),
+                                       rtol=1e-5, atol=1e-12)
+            for k in (0, 1, 3, 50, V, 999999):
+                p = osm.probs_ref(x, T, k)
+                for seed in range(6):
+                    np.random.seed(seed)
+                    want = int(np.random.choice(V, p=p))  # the reference's call
+                    np.random.seed(seed)
+                    assert osm.sample_ref(x, T, k, np.random.random_sample()) == want
+                if 0 < k < V:  # the k largest logits survive, renormalised
+                    top = np.argsort(x)[::-1][:k]
+                    assert set(np.nonzero(p)[0]) == set(top)
+                    np.testing.assert_allclose(p[top], softmax(x[top].astype(np.float64) / np.float32(T)), rtol=1e-5)
+                    assert osm.kept_mask(x, k).sum() == k
+    # greedy: first maximum, NaN first, exactly np.argmax
+    y = np.array([1.0, 5.0, 5.0, -2.0], np.float32)
+    assert osm.sample_ref(y, 0.0, 0, 0.3) == 1 == np.argmax(y)
+    assert osm.sample_ref(y, 1e-6, 3, 0.9) == 1  # the cut-off itself is greedy
+    assert osm.sample_ref(np.array([1.0, np.nan, 3.0, np.nan], np.float32), 0.0, 0, 0.5) == 1
+    # ties at the k-th: the device keeps all of them; without ties its rule
+    # is the reference's
+    z = np.array([0.0, 2.0, 1.0, 2.0, 1.0, 1.0], np.float32)
+    assert osm.kept_mask(z, 3).tolist() == [False, True, True, True, True, True]
+    # p = [0, e^2, e, e^2, e, e] / (2 e^2 + 3 e): steps at .322 .441 .763 .882 1
+    assert [osm.sample_kept_ref(z, 1.0, 3, u) for u in (0.1, 0.4, 0.7, 0.9, 0.99)] == [1, 2, 3, 5, 5]
+    x = (2.0 * rng.standard_normal(3000)).astype(np.float32)
+    for k in (0, 1, 7, 64, 2999, 5000):
+        for u in rng.random(50):
+            assert osm.sample_kept_ref(x, 0.9, k, u) == osm.sample_ref(x, 0.9, k, u)
+    # u = 0 picks the first entry with mass; u -> 1 the last
+    w = np.array([-np.inf, 0.0, 0.0, -np.inf], np.float32)
+    assert osm.sample_ref(w, 1.0, 0, 0.0) == 1 and osm.sample_ref(w, 1.0, 0, 1 - 2.0 ** -53) == 2
+    # many draws follow p
+    x = rng.standard_normal(8).astype(np.float32)
+    p = osm.probs_ref(x, 0.8, 5)
+    u = rng.random(40000)
+    counts = np.bincount([osm.sample_ref(x, 0.8, 5, ui) for ui in u], minlength=8) / u.size
+    np.testing.assert_allclose(counts, p, atol=0.012)

@@ -5,7 +5,8 @@ ziliangpeng/triton-llm: ``attention``, ``attention_gqa``, ``precompute_cos_sin``
 ``apply_rope``) plus the additive batched entry points of this build
 (flash prefill, KV-cache append, split-K decode) and the model step's other
 layers: the projection ``gemm``, ``rms_norm`` (plus the fused
-``add_rms_norm``), ``swiglu`` and ``add``.  The reference's gelu,
+``add_rms_norm``), ``swiglu`` and ``add``, and on-device next-token
+``sample`` / ``sample_rows`` (the models' ``_sample``).  The reference's gelu,
 layer_norm, softmax and embedding kernels (GPT-2 and host-side pieces) are
 outside this library's scope.
 """
@@ -18,6 +19,7 @@ from .gemm import gemm
 from .rms_norm import add_rms_norm, rms_norm
 from .swiglu import swiglu
 from .add import add
+from .sample import sample, sample_rows
 from .decode import (
     allocate_kv_cache,
     attention_decode,
@@ -44,4 +46,6 @@ __all__ = [
     "add_rms_norm",
     "swiglu",
     "add",
+    "sample",
+    "sample_rows",
 ]
