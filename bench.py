@@ -477,6 +477,26 @@ def copy_probe(mib):
     print(json.dumps({"copy_probe_bytes": n, "copies": 5}))
 
 
+SAMPLE_MODES = {"greedy": (0.0, 0), "t0.8": (0.8, 0), "t0.8_k50": (0.8, 50)}
+
+
+def bench_sample_case(vocab, rows, mode, steps):
+    """One sampling case only, for rocprofv3: ``steps`` calls of
+    sample_rows on fp32 logits (rows, vocab)."""
+    from triton_llm import gpu
+    from triton_llm.kernels import sample_rows
+
+    rng = np.random.default_rng(0)
+    T, k = SAMPLE_MODES[mode]
+    x = gpu.to_device((3.0 * rng.standard_normal((rows, vocab))).astype(np.float32))
+    u = gpu.to_device(rng.random(rows))
+    tok = gpu.allocate((rows,), np.int32)
+    for _ in range(steps):
+        sample_rows(x, T, k, uniforms=u, out_dev=tok)
+    gpu.synchronize()
+    log(f"sample case vocab={vocab} rows={rows} {mode}: {steps} calls")
+
+
 def bench_sample(steps, warmup, cpu=True, vocabs=(49152, 128256)):
     """Next-token sampling (tl_sample) on fp32 logits at SmolLM2's and
     Llama-3.2's vocabularies: event-timed kernel time per call for 1 and 64
@@ -491,7 +511,7 @@ def bench_sample(steps, warmup, cpu=True, vocabs=(49152, 128256)):
 
     lib = gpu.runtime()
     rng = np.random.default_rng(0)
-    modes = (("greedy", 0.0, 0), ("t0.8", 0.8, 0), ("t0.8_k50", 0.8, 50))
+    modes = tuple((name, T, k) for name, (T, k) in SAMPLE_MODES.items())
     out = []
     for V in vocabs:
         for rows in (1, 64):
@@ -553,6 +573,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gemm", action="store_true",
                     help="time the model's projection GEMMs (tl_gemm) instead of attention")
+    ap.add_argument("--sample", action="store_true",
+                    help="time next-token sampling (tl_sample) instead of attention")
+    ap.add_argument("--sample-case", default="",
+                    help="VOCAB,ROWS,MODE (mode: greedy, t0.8, t0.8_k50): run only --steps calls "
+                         "of that sampling case (for rocprofv3) and exit")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="only run 5 device-to-device copies of this many MiB (the known-size "
                          "reference for calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -573,6 +598,13 @@ def main():
         copy_probe(args.copy_probe_mb)
         return
     cpu = not args.no_cpu
+    if args.sample_case:
+        vocab, rows, mode = args.sample_case.split(",")
+        bench_sample_case(int(vocab), int(rows), mode, args.steps)
+        return
+    if args.sample:
+        print(json.dumps(bench_sample(min(args.steps, 50), min(args.warmup, 5), cpu=cpu)))
+        return
     if args.gemm:
         print(json.dumps(bench_gemm(min(args.steps, 20), min(args.warmup, 5), cpu=cpu)))
         return

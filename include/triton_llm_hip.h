@@ -207,15 +207,20 @@ int tl_add(const void* x, const void* y, void* z, int64_t count, int dtype, void
  *     entry >= the top_k-th largest logit (ties with it all kept); tokens[r] =
  *     first index whose cumulative kept mass exceeds uniforms[r] * total, the
  *     inverse CDF np.random.choice applies to its uniform draw.  A row whose
- *     mass is not a positive finite number (NaN / +inf logits, all -inf) gets
- *     -1, where the reference's np.random.choice raises ValueError.
+ *     maximum is not finite (NaN / +inf logits, all -inf) gets -1, where the
+ *     reference's np.random.choice raises ValueError.
  * The reference's 1e-6 greedy cut-off is the caller's (compare in double,
  * pass 0 for greedy).  1 <= vocab <= tl_sample_max_vocab(), row_stride >=
- * vocab, top_k >= 0 (0 keeps all); rows = 0 does nothing.
+ * vocab, top_k >= 0 (0 keeps all), rows <= 65535; rows = 0 does nothing.
+ * workspace: tl_sample_workspace_bytes(rows, vocab) bytes (segment results
+ * and candidates; no initial contents needed).  Two kernels on `stream`:
+ * one workgroup per 2048-entry segment of every row, then one per row.
  * ------------------------------------------------------------------------- */
 int tl_sample_max_vocab(void);
+size_t tl_sample_workspace_bytes(int rows, int vocab);
 int tl_sample(const void* logits, int rows, int vocab, int64_t row_stride, float temperature,
-              int top_k, const double* uniforms, int32_t* tokens, int dtype, void* stream);
+              int top_k, const double* uniforms, int32_t* tokens, void* workspace,
+              size_t workspace_bytes, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -151,10 +151,12 @@ def test_max_vocab_and_strided_rows():
     u_dev = gpu.to_device(u)
     out = gpu.allocate((rows,), np.int32)
     lib = gpu.runtime()
-    assert lib.tl_sample(dev.ptr, rows, Vp, stride, 0.0, 0, None, out.ptr, 0, None) == 0
+    nws = lib.tl_sample_workspace_bytes(rows, Vp)
+    ws = gpu.allocate((nws,), np.uint8)
+    assert lib.tl_sample(dev.ptr, rows, Vp, stride, 0.0, 0, None, out.ptr, ws.ptr, nws, 0, None) == 0
     gpu.synchronize()
     np.testing.assert_array_equal(out.to_numpy(), np.argmax(xp[:, :Vp], axis=1))
-    assert lib.tl_sample(dev.ptr, rows, Vp, stride, 1.0, 10, u_dev.ptr, out.ptr, 0, None) == 0
+    assert lib.tl_sample(dev.ptr, rows, Vp, stride, 1.0, 10, u_dev.ptr, out.ptr, ws.ptr, nws, 0, None) == 0
     gpu.synchronize()
     bad, near = compare(xp[:, :Vp], 1.0, 10, u, out.to_numpy())
     assert not bad and near <= 1
@@ -216,14 +218,39 @@ def test_argument_errors():
     dev = gpu.to_device(np.zeros((2, 8), np.float32))
     out = gpu.allocate((2,), np.int32)
     u = gpu.to_device(np.zeros(2))
-    assert lib.tl_sample(dev.ptr, 2, 0, 8, 1.0, 0, u.ptr, out.ptr, 0, None) != 0          # vocab 0
-    assert lib.tl_sample(dev.ptr, 2, 8, 4, 1.0, 0, u.ptr, out.ptr, 0, None) != 0          # stride < vocab
-    assert lib.tl_sample(dev.ptr, 2, 8, 8, 1.0, -1, u.ptr, out.ptr, 0, None) != 0         # top_k < 0
-    assert lib.tl_sample(dev.ptr, 2, 8, 8, 1.0, 0, ctypes.c_void_p(None), out.ptr, 0, None) != 0  # no draws
-    assert lib.tl_sample(dev.ptr, 2, max_vocab() + 1, max_vocab() + 1, 0.0, 0, None, out.ptr, 0, None) != 0
-    assert lib.tl_sample(dev.ptr, 2, 8, 8, 1.0, 0, u.ptr, out.ptr, 7, None) != 0          # dtype
-    assert lib.tl_sample(dev.ptr, 0, 8, 8, 1.0, 0, u.ptr, out.ptr, 0, None) == 0          # no rows
+    nws = lib.tl_sample_workspace_bytes(2, 8)
+    ws = gpu.allocate((nws,), np.uint8)
+    null = ctypes.c_void_p(None)
+
+    def call(rows=2, vocab=8, stride=8, t=1.0, k=0, uu=u.ptr, w=ws.ptr, wb=nws, dtype=0):
+        return lib.tl_sample(dev.ptr, rows, vocab, stride, t, k, uu, out.ptr, w, wb, dtype, None)
+
+    assert call(vocab=0) != 0                    # vocab 0
+    assert call(stride=4) != 0                   # stride < vocab
+    assert call(k=-1) != 0                       # top_k < 0
+    assert call(uu=null) != 0                    # sampling without draws
+    assert call(w=null) != 0                     # no workspace
+    assert call(wb=nws - 1) != 0                 # workspace too small
+    assert call(vocab=max_vocab() + 1, stride=max_vocab() + 1, t=0.0) != 0
+    assert lib.tl_sample_workspace_bytes(2, max_vocab() + 1) == 0
+    assert lib.tl_sample_workspace_bytes(65536, 8) == 0
+    assert call(dtype=7) != 0                    # dtype
+    assert call(rows=0) == 0                     # no rows
+    assert call() == 0
+    gpu.synchronize()
     with pytest.raises(ValueError):
         sample_rows(dev, 1.0, 0, uniforms=np.zeros(3))
     with pytest.raises(IndexError):
         sample(dev, 1.0, 0, row=2)
+
+
+def test_workspace_reuse_across_layouts():
+    """One cached workspace serving alternating (rows, vocab, top_k) layouts
+    keeps giving the oracle's tokens."""
+    rng = np.random.default_rng(21)
+    for rows, V, k in ((3, 5000, 0), (40, 300, 7), (1, 49152, 50), (40, 300, 7), (7, 70000, 0), (3, 5000, 3)):
+        x = rng.standard_normal((rows, V)).astype(np.float32)
+        u = rng.random(rows)
+        bad, near = compare(x, 1.1, k, u, run_rows(x, "float32", 1.1, k, u))
+        assert not bad and near <= 1
+        np.testing.assert_array_equal(run_rows(x, "float32", 0.0, 0, None), np.argmax(x, axis=1))

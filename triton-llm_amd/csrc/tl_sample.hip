@@ -14,24 +14,32 @@
 // np.random.choice would.  The C entry point takes temperature <= 0 as greedy
 // (the wrapper applies the reference's 1e-6 cut-off in double precision).
 //
-// One workgroup of 1024 threads per row; every pass over the row is a
-// coalesced strided sweep with 16 loads in flight per thread (the row stays
-// in L2 after the first):
-//   1. row maximum and its first index (and the first radix digits);
-//   2. top_k: radix select of the k-th largest logit on an order-preserving
-//      32-bit key, 4 bits per pass from the top.  Each thread counts digits
-//      in packed 8-bit fields (two 64-bit words), a wave sums them as 16-bit
-//      fields, wave 0 picks the digit.  The select stops early once the
-//      chosen digit's bin holds exactly the entries still to take.  Every
-//      logit >= the k-th is kept, so all ties with the k-th are kept where
-//      argpartition keeps exactly k of them in an arbitrary order;
-//   3. p = exp(x / T - max / T) for the kept entries; the mass of each chunk
-//      of 1024 consecutive entries (fp64) goes to LDS; wave 0 scans the chunk
-//      masses for the chunk holding target = u * total, then scans that
-//      chunk's entries.  Each scan gives lane l the interval [lo_l, hi_l) with
-//      hi_l the same double as lo_{l+1}, so exactly one lane holds target.
-// A row whose mass is not a positive finite number (a NaN or +inf logit, all
-// logits -inf) gets token -1; np.random.choice raises ValueError there.
+// A row is read by many workgroups at once: one CU keeps too few misses in
+// flight to stream a 200-500 KB row quickly (~10 GB/s measured), so each row
+// is cut into segments of 2048 entries, one 256-thread workgroup per segment
+// (grid = segments x rows), each entry read from HBM exactly once:
+//   * every segment records its maximum and first index;
+//   * without top_k it also records its mass at its own maximum,
+//     sum exp(x / T - m_seg / T) (fp64);
+//   * with top_k it keeps its own top_k (every entry >= its k-th largest, by
+//     a radix select on an order-preserving 32-bit key, 8 bits per step,
+//     counted with LDS atomics) as candidates, written in index order.  The row's k-th
+//     largest is >= each segment's k-th largest, so the candidates hold every
+//     entry the row keeps.
+// A second kernel, one workgroup per row, finishes each row (the kernel
+// boundary publishes the segments' results; no fences or counters):
+//   * greedy: the argmax of the segment maxima;
+//   * without top_k: segment masses rescaled to the row maximum locate the
+//     segment holding target = u * total, which is rescanned with the exact
+//     p = exp(x / T - max / T);
+//   * with top_k: the k-th largest candidate (radix select; candidates staged
+//     in LDS when they fit), then the inverse CDF over the kept candidates.
+// Every scan gives thread t the interval [lo_t, hi_t) of cumulative mass with
+// hi_t the same double as lo_{t+1}, so exactly one thread holds target.
+// Every entry >= the k-th largest logit is kept: ties with the k-th are all
+// kept, where argpartition keeps exactly k of them in an arbitrary order.
+// A row whose maximum is not finite (a NaN or +inf logit, all logits -inf)
+// gets token -1 when sampling; np.random.choice raises ValueError there.
 #include "tl_common.h"
 
 #include <limits.h>
@@ -39,13 +47,45 @@
 
 namespace {
 
-constexpr int kSThreads = 1024;
-constexpr int kSWaves = kSThreads / 64;
-constexpr int kChunk = 1024;                  // entries per chunk of the inverse CDF
-constexpr int kPerLane = kChunk / 64;         // a lane's run inside a chunk
-constexpr int kMaxChunks = 256;               // wave 0 holds 4 chunk masses per lane
-constexpr int kMaxVocab = 255 * kSThreads;    // per-thread radix counts fit 8 bits
-constexpr int kSweep = 16;                    // loads in flight per thread in a sweep
+constexpr int kBT = 256;                    // threads per workgroup
+constexpr int kBW = kBT / 64;               // waves per workgroup
+constexpr int kPer = 8;                     // entries per thread in a segment
+constexpr int kSeg = kBT * kPer;            // entries per segment
+constexpr int kMaxSeg = 128;                // segments per row (2 per lane of one wave)
+constexpr int kMaxVocab = kMaxSeg * kSeg;   // 262144
+constexpr int kLdsCand = 6144;              // candidates the finishing workgroup stages in LDS
+constexpr int kMaxRows = 65535;             // grid.y
+
+struct Ws {
+  double* mass;    // [rows][G] segment mass at the segment maximum
+  float* smax;     // [rows][G] segment maximum
+  int* sarg;       // [rows][G] its first index
+  int* count;      // [rows][G] candidates kept by the segment
+  float* cx;       // [rows][vocab] candidate logits, segment g's list at g * kSeg
+  int* ci;         // [rows][vocab] their indices
+};
+
+size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
+int n_segments(int vocab) { return (vocab + kSeg - 1) / kSeg; }
+
+// Workspace layout; base == nullptr only sizes it.
+size_t ws_layout(int rows, int vocab, char* base, Ws* ws) {
+  const size_t R = (size_t)rows, G = (size_t)n_segments(vocab), V = (size_t)vocab;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char* p = base ? base + off : nullptr;
+    off += align256(bytes);
+    return p;
+  };
+  char* mass = take(R * G * 8);
+  char* smax = take(R * G * 4);
+  char* sarg = take(R * G * 4);
+  char* count = take(R * G * 4);
+  char* cx = take(R * V * 4);
+  char* ci = take(R * V * 4);
+  if (ws) *ws = Ws{(double*)mass, (float*)smax, (int*)sarg, (int*)count, (float*)cx, (int*)ci};
+  return off;
+}
 
 template <typename T>
 __device__ __forceinline__ float logit(const void* row, int i) {
@@ -67,41 +107,6 @@ __device__ __forceinline__ unsigned order_key(float x) {
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-// f(x, i) for every entry of the row, thread t taking i = t + 1024 j.  Each
-// thread issues kSweep loads before it uses any, so a sweep waits for memory
-// once per kSweep * 1024 entries instead of once per 1024.
-template <typename T, typename F>
-__device__ __forceinline__ void sweep(const void* row, int vocab, F&& f) {
-  for (int base = threadIdx.x; base < vocab; base += kSweep * kSThreads) {
-    float v[kSweep];
-#pragma unroll
-    for (int u = 0; u < kSweep; ++u) {
-      const int i = base + u * kSThreads;
-      v[u] = i < vocab ? logit<T>(row, i) : 0.f;
-    }
-#pragma unroll
-    for (int u = 0; u < kSweep; ++u)
-      if (base + u * kSThreads < vocab) f(v[u], base + u * kSThreads);
-  }
-}
-
-// Count the 4-bit digit of key at shift: digits 0-7 in lo8, 8-15 in hi8,
-// 8 bits per digit.
-__device__ __forceinline__ void add_digit(unsigned key, int shift, uint64_t& lo8, uint64_t& hi8) {
-  const unsigned d = (key >> shift) & 15u;
-  const uint64_t inc = 1ull << ((d & 7u) * 8u);
-  if (d < 8u)
-    lo8 += inc;
-  else
-    hi8 += inc;
-}
-
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-  return v;
-}
-
 __device__ __forceinline__ double wave_incl_scan_d(double v, int lane) {
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
@@ -111,227 +116,421 @@ __device__ __forceinline__ double wave_incl_scan_d(double v, int lane) {
   return v;
 }
 
-template <typename T>
-__global__ __launch_bounds__(kSThreads) void sample_kernel(const void* logits, int64_t row_stride, int vocab,
-                                                           float temperature, int top_k, const double* uniforms,
-                                                           int32_t* out) {
-  __shared__ float s_max[kSWaves];
-  __shared__ int s_arg[kSWaves];
-  __shared__ unsigned s_hist[kSWaves][16];
-  __shared__ unsigned s_sel[3];
-  __shared__ double s_chunk[kMaxChunks];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const void* row = (const char*)logits + (int64_t)blockIdx.x * row_stride * T::size;
+__device__ __forceinline__ int wave_incl_scan_i(int v, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(v, d);
+    if (lane >= d) v += y;
+  }
+  return v;
+}
 
-  // 1. maximum and its first index; with a top_k filter the same sweep
-  //    counts the first (top 4 bits) radix digits
-  const bool filter = temperature > 0.f && top_k > 0 && top_k < vocab;
-  float bm = -INFINITY;
-  int bi = INT_MAX;
-  uint64_t lo8 = 0, hi8 = 0;  // digit counts of this thread, 8 bits each
-  sweep<T>(row, vocab, [&](float x, int i) {
-    if (beats(x, i, bm, bi)) {
-      bm = x;
-      bi = i;
-    }
-    if (filter) add_digit(order_key(x), 28, lo8, hi8);
-  });
+struct LdsSeg {
+  float m[kBW];
+  int a[kBW];
+  double d[kBW];
+  int i[kBW];
+  unsigned hist[256];
+  unsigned sel[3];
+};
+
+struct LdsFin : LdsSeg {
+  int pick;
+  double pick_lo;
+  double target;
+  int off[kMaxSeg + 1];
+  float cx[kLdsCand];
+  int ci[kLdsCand];
+};
+
+// (max, first index) over the workgroup; every thread gets the result.
+__device__ __forceinline__ void block_argmax(float& m, int& a, LdsSeg& s) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
-    const float om = __shfl_xor(bm, off);
-    const int oi = __shfl_xor(bi, off);
-    if (beats(om, oi, bm, bi)) {
-      bm = om;
-      bi = oi;
+    const float om = __shfl_xor(m, off);
+    const int oa = __shfl_xor(a, off);
+    if (beats(om, oa, m, a)) {
+      m = om;
+      a = oa;
     }
   }
+  __syncthreads();  // earlier readers of s.m / s.a are done
   if (lane == 0) {
-    s_max[wave] = bm;
-    s_arg[wave] = bi;
+    s.m[wave] = m;
+    s.a[wave] = a;
   }
   __syncthreads();
-  bm = s_max[0];
-  bi = s_arg[0];
-  for (int w = 1; w < kSWaves; ++w)
-    if (beats(s_max[w], s_arg[w], bm, bi)) {
-      bm = s_max[w];
-      bi = s_arg[w];
+  m = s.m[0];
+  a = s.a[0];
+#pragma unroll
+  for (int w = 1; w < kBW; ++w)
+    if (beats(s.m[w], s.a[w], m, a)) {
+      m = s.m[w];
+      a = s.a[w];
     }
-  if (!(temperature > 0.f)) {
-    if (tid == 0) out[blockIdx.x] = bi;
-    return;
-  }
+}
 
-  // 2. key of the k-th largest logit (0 keeps everything)
-  unsigned thr = 0u;
-  if (filter) {
-    unsigned prefix = 0u, need = (unsigned)top_k;
-    for (int shift = 28; shift >= 0; shift -= 4) {
-      if (shift != 28) {  // the top digit was counted with the maximum
-        const unsigned hmask = ~0u << (shift + 4);
-        lo8 = hi8 = 0;
-        sweep<T>(row, vocab, [&](float x, int) {
-          const unsigned key = order_key(x);
-          if ((key & hmask) == prefix) add_digit(key, shift, lo8, hi8);
-        });
-      }
-      // 16-bit fields for the wave sum (at most 64 * 255 per digit)
-      uint64_t w16[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint64_t src = q < 2 ? lo8 : hi8;
-        uint64_t v = 0;
-#pragma unroll
-        for (int f = 0; f < 4; ++f) v |= ((src >> (8 * ((q & 1) * 4 + f))) & 0xFFull) << (16 * f);
-        w16[q] = v;
-      }
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) w16[q] += __shfl_xor(w16[q], off);
-      if (lane == 0)
-#pragma unroll
-        for (int d = 0; d < 16; ++d) s_hist[wave][d] = (unsigned)((w16[d >> 2] >> (16 * (d & 3))) & 0xFFFFull);
-      __syncthreads();
-      if (wave == 0) {
-        unsigned cnt = 0;
-        if (lane < 16)
-          for (int w = 0; w < kSWaves; ++w) cnt += s_hist[w][lane];
-        unsigned suf = cnt;  // lane d: entries whose digit is >= d
-#pragma unroll
-        for (int d = 1; d < 16; d <<= 1) {
-          const unsigned y = __shfl_down(suf, d);
-          if (lane + d < 16) suf += y;
-        }
-        // the largest digit whose suffix still holds `need` entries (digit 0
-        // always does: its suffix is every entry under the prefix)
-        const int D = __popcll(__ballot(lane < 16 && suf >= need)) - 1;
-        const unsigned above = __shfl(suf, D + 1);  // lane 16 holds 0
-        const unsigned inbin = __shfl(cnt, D);
-        if (lane == 0) {
-          s_sel[0] = (unsigned)D;
-          s_sel[1] = need - above;
-          s_sel[2] = inbin;
-        }
-      }
-      __syncthreads();
-      prefix |= s_sel[0] << shift;
-      thr = prefix;
-      if (s_sel[2] == s_sel[1]) break;  // the whole bin is kept: lower bits do not matter
-      need = s_sel[1];
-    }
-  }
-
-  // 3. chunk masses, then the inverse CDF in wave 0
-  const float ms = bm / temperature;
-  auto prob_of = [&](float x) -> float { return order_key(x) >= thr ? expf(x / temperature - ms) : 0.f; };
-  const int n_chunks = (vocab + kChunk - 1) / kChunk;
-  for (int c = wave; c < n_chunks; c += kSWaves) {
-    float v[kPerLane];
-#pragma unroll
-    for (int j = 0; j < kPerLane; ++j) {
-      const int i = c * kChunk + j * 64 + lane;
-      v[j] = i < vocab ? logit<T>(row, i) : 0.f;
-    }
-    double s = 0.0;
-#pragma unroll
-    for (int j = 0; j < kPerLane; ++j)
-      if (c * kChunk + j * 64 + lane < vocab) s += (double)prob_of(v[j]);
-    s = wave_sum_d(s);
-    if (lane == 0) s_chunk[c] = s;
-  }
-  __syncthreads();
-  if (wave != 0) return;
-
-  // lane l: chunks 4l .. 4l+3
-  double cm[4], mine = 0.0;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int c = 4 * lane + q;
-    cm[q] = c < n_chunks ? s_chunk[c] : 0.0;
-    mine += cm[q];
-  }
-  double incl = wave_incl_scan_d(mine, lane);
+// Workgroup scan of v: [lo, hi) is this thread's interval, total the sum.  The
+// wave offsets are summed in one order by every thread, so the hi of one
+// thread is the lo of the next bit for bit, and the last hi is total.
+__device__ __forceinline__ void block_scan_d(double v, double& lo, double& hi, double& total, LdsSeg& s) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const double incl = wave_incl_scan_d(v, lane);
   double excl = __shfl_up(incl, 1);
   if (lane == 0) excl = 0.0;
-  const double total = __shfl(incl, 63);
-  if (!(total > 0.0) || !(total < INFINITY)) {
-    if (lane == 0) out[blockIdx.x] = -1;
-    return;
-  }
-  const double u = fmin(fmax(uniforms[blockIdx.x], 0.0), 1.0);
-  const double target = u * total;
-  // The lane whose interval holds target; when rounding leaves target at
-  // total, the last lane with mass (its hi is total).
-  uint64_t claim = __ballot(excl < incl && excl <= target && (target < incl || incl >= total));
-  if (!claim) {  // not reachable: the intervals tile [0, total]
-    if (lane == 0) out[blockIdx.x] = -1;
-    return;
-  }
-  int owner = __ffsll((unsigned long long)claim) - 1;
-  int cq = -1, lastq = 0;
-  double acc = excl, clo = excl, clo_last = excl;
+  __syncthreads();  // earlier readers of s.d are done
+  if (lane == 63) s.d[wave] = incl;
+  __syncthreads();
+  double base = 0.0;
+  total = 0.0;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    if (cm[q] > 0.0) {
-      lastq = q;
-      clo_last = acc;
-      const double next = acc + cm[q];
-      if (cq < 0 && next > target) {
-        cq = q;
-        clo = acc;
-      }
-      acc = next;
-    }
+  for (int w = 0; w < kBW; ++w) {
+    if (w == wave) base = total;
+    total += s.d[w];
   }
-  if (cq < 0) {
-    cq = lastq;
-    clo = clo_last;
-  }
-  const int chunk = 4 * __shfl(lane, owner) + __shfl(cq, owner);
-  clo = __shfl(clo, owner);
+  lo = base + excl;
+  hi = base + incl;
+}
 
-  // lane l: entries chunk * 1024 + 16 l .. + 15
-  const int e0 = chunk * kChunk + lane * kPerLane;
-  float pr[kPerLane];
+// Key of the need-th largest entry (1 <= need <= number of entries): radix
+// select from the top byte down.  each(f) calls f(key) for every entry this
+// thread holds.  A step counts the byte under the current prefix into 256
+// LDS bins; wave 0 finds the largest byte D whose suffix still holds `need`
+// entries.  It stops early when D's bin holds exactly the entries still to
+// take: then every entry >= the prefix (lower bits zero) is in the top need.
+template <class Each>
+__device__ __forceinline__ unsigned kth_key(Each&& each, unsigned need, LdsSeg& s) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  unsigned prefix = 0u;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    const unsigned hmask = shift == 24 ? 0u : ~0u << (shift + 8);
+    for (int b = threadIdx.x; b < 256; b += kBT) s.hist[b] = 0u;
+    __syncthreads();
+    each([&](unsigned key) {
+      if ((key & hmask) == prefix) atomicAdd(&s.hist[(key >> shift) & 255u], 1u);
+    });
+    __syncthreads();
+    if (wave == 0) {
+      unsigned c[4], lsum = 0;  // lane l: bins 4l .. 4l+3
 #pragma unroll
-  for (int j = 0; j < kPerLane; ++j) pr[j] = e0 + j < vocab ? logit<T>(row, e0 + j) : 0.f;
-  mine = 0.0;
+      for (int q = 0; q < 4; ++q) {
+        c[q] = s.hist[4 * lane + q];
+        lsum += c[q];
+      }
+      unsigned v = lsum;  // entries in lanes >= l
 #pragma unroll
-  for (int j = 0; j < kPerLane; ++j) {
-    pr[j] = e0 + j < vocab ? prob_of(pr[j]) : 0.f;
-    mine += (double)pr[j];
-  }
-  incl = wave_incl_scan_d(mine, lane);
-  excl = __shfl_up(incl, 1);
-  if (lane == 0) excl = 0.0;
-  const double lo = clo + excl, hi = clo + incl, end = clo + __shfl(incl, 63);
-  claim = __ballot(lo < hi && lo <= target && (target < hi || hi >= end));
-  if (!claim) {  // not reachable: the chunk was chosen for holding mass at target
-    if (lane == 0) out[blockIdx.x] = -1;
-    return;
-  }
-  owner = __ffsll((unsigned long long)claim) - 1;
-  if (lane == owner) {
-    int tok = -1, last = -1;
-    acc = lo;
-#pragma unroll
-    for (int j = 0; j < kPerLane; ++j) {
-      if (pr[j] > 0.f) {
-        last = e0 + j;
-        acc += (double)pr[j];
-        if (tok < 0 && acc > target) tok = e0 + j;
+      for (int d = 1; d < 64; d <<= 1) {
+        const unsigned y = __shfl_down(v, d);
+        if (lane + d < 64) v += y;
+      }
+      // lane 0's suffix is every entry under the prefix, which holds `need`
+      const int L = __popcll(__ballot(v >= need)) - 1;
+      if (lane == L) {
+        unsigned suf = v - lsum;  // entries in lanes > L
+        int q = 3;
+        for (;; --q) {
+          suf += c[q];
+          if (suf >= need || q == 0) break;
+        }
+        s.sel[0] = (unsigned)(4 * L + q);
+        s.sel[1] = need - (suf - c[q]);
+        s.sel[2] = c[q];
       }
     }
-    out[blockIdx.x] = tok >= 0 ? tok : last;
+    __syncthreads();
+    prefix |= s.sel[0] << shift;
+    const bool settled = shift == 0 || s.sel[2] == s.sel[1];
+    need = s.sel[1];
+    if (settled) break;
+    // The next step clears s.hist only after wave 0 has read it (the barrier
+    // above), and writes s.sel only after its second barrier, which every
+    // thread reaches after reading s.sel here.
+  }
+  return prefix;
+}
+
+// One segment of one row: grid (segments, rows).
+template <typename T>
+__global__ __launch_bounds__(kBT) void segment_kernel(const void* logits, int64_t row_stride, int vocab,
+                                                      float temperature, int top_k, Ws ws) {
+  __shared__ LdsSeg s;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = blockIdx.x, r = blockIdx.y, G = gridDim.x;
+  const void* row = (const char*)logits + (int64_t)r * row_stride * T::size;
+  const bool greedy = !(temperature > 0.f);
+  const bool filter = !greedy && top_k > 0 && top_k < vocab;
+  const int s0 = g * kSeg;
+  const int nseg = min(kSeg, vocab - s0);
+  const int i0 = s0 + tid * kPer;  // this thread's kPer consecutive entries
+  const size_t pi = (size_t)r * G + g;
+
+  // ---- this segment ----
+  float x[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) x[j] = i0 + j < vocab ? logit<T>(row, i0 + j) : -INFINITY;
+  float m = -INFINITY;
+  int a = INT_MAX;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j)
+    if (i0 + j < vocab && beats(x[j], i0 + j, m, a)) {
+      m = x[j];
+      a = i0 + j;
+    }
+  block_argmax(m, a, s);
+  if (tid == 0) {
+    ws.smax[pi] = m;
+    ws.sarg[pi] = a;
+  }
+  if (!greedy && !filter) {
+    double v = 0.0;
+    if (m > -INFINITY && m < INFINITY) {
+      const float ms = m / temperature;
+#pragma unroll
+      for (int j = 0; j < kPer; ++j)
+        if (i0 + j < vocab) v += (double)expf(x[j] / temperature - ms);
+    }
+    double lo, hi, tot;
+    block_scan_d(v, lo, hi, tot, s);
+    if (tid == 0) ws.mass[pi] = tot;
+  }
+  if (filter) {
+    unsigned thr = 0u;  // keep the whole segment when it has at most top_k entries
+    if (top_k < nseg)
+      thr = kth_key(
+          [&](auto&& f) {
+#pragma unroll
+            for (int j = 0; j < kPer; ++j)
+              if (i0 + j < vocab) f(order_key(x[j]));
+          },
+          (unsigned)top_k, s);
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) c += (i0 + j < vocab && order_key(x[j]) >= thr) ? 1 : 0;
+    const int incl = wave_incl_scan_i(c, lane);
+    __syncthreads();
+    if (lane == 63) s.i[wave] = incl;
+    __syncthreads();
+    int pos = incl - c, n_kept = 0;
+#pragma unroll
+    for (int w = 0; w < kBW; ++w) {
+      if (w < wave) pos += s.i[w];
+      n_kept += s.i[w];
+    }
+    const size_t base = (size_t)r * vocab + s0;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j)
+      if (i0 + j < vocab && order_key(x[j]) >= thr) {
+        ws.cx[base + pos] = x[j];
+        ws.ci[base + pos] = i0 + j;
+        ++pos;
+      }
+    if (tid == 0) ws.count[pi] = n_kept;
+  }
+
+}
+
+// The rest of each row, one workgroup per row, after segment_kernel.
+template <typename T>
+__global__ __launch_bounds__(kBT) void finish_kernel(const void* logits, int64_t row_stride, int vocab,
+                                                     float temperature, int top_k, const double* uniforms,
+                                                     int32_t* out, Ws ws, int G) {
+  __shared__ LdsFin s;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = blockIdx.x;
+  const void* row = (const char*)logits + (int64_t)r * row_stride * T::size;
+  const bool greedy = !(temperature > 0.f);
+  const bool filter = !greedy && top_k > 0 && top_k < vocab;
+
+  float M = -INFINITY;
+  int A = INT_MAX;
+  if (tid < G) {
+    M = ws.smax[(size_t)r * G + tid];
+    A = ws.sarg[(size_t)r * G + tid];
+  }
+  block_argmax(M, A, s);
+  if (tid == 0) out[r] = greedy ? A : -1;  // sampling: replaced below by the thread holding the draw
+  if (greedy || !(M > -INFINITY && M < INFINITY)) return;
+  const float Ms = M / temperature;
+  const double u = fmin(fmax(uniforms[r], 0.0), 1.0);
+
+  if (!filter) {
+    // segment weights: mass at the segment maximum rescaled to the row's
+    if (wave == 0) {
+      double wv[2], mine = 0.0;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int gg = 2 * lane + q;
+        wv[q] = 0.0;
+        if (gg < G) {
+          const float mg = ws.smax[(size_t)r * G + gg];
+          if (mg > -INFINITY) wv[q] = ws.mass[(size_t)r * G + gg] * exp((double)(mg / temperature) - (double)Ms);
+        }
+        mine += wv[q];
+      }
+      const double incl = wave_incl_scan_d(mine, lane);
+      double excl = __shfl_up(incl, 1);
+      if (lane == 0) excl = 0.0;
+      const double total = __shfl(incl, 63);
+      const double target = u * total;
+      const uint64_t claim = __ballot(excl < incl && excl <= target && (target < incl || incl >= total));
+      int gsel = -1;
+      double clo = excl;
+      if (claim) {
+        const int owner = __ffsll((unsigned long long)claim) - 1;
+        double acc = excl, lo_hit = excl, lo_last = excl;
+        int q_hit = -1, q_last = 0;
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+          if (wv[q] > 0.0) {
+            q_last = q;
+            lo_last = acc;
+            const double next = acc + wv[q];
+            if (q_hit < 0 && next > target) {
+              q_hit = q;
+              lo_hit = acc;
+            }
+            acc = next;
+          }
+        const int q = q_hit >= 0 ? q_hit : q_last;
+        gsel = 2 * owner + __shfl(q, owner);
+        clo = __shfl(q_hit >= 0 ? lo_hit : lo_last, owner);
+      }
+      if (lane == 0) {
+        s.pick = gsel;
+        s.pick_lo = clo;
+        s.target = target;
+      }
+    }
+    __syncthreads();
+    const int gs = s.pick;
+    const double clo = s.pick_lo, target = s.target;
+    if (gs < 0) return;  // not reachable: the weights tile [0, total]
+    const int e0 = gs * kSeg + tid * kPer;
+    float p[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) p[j] = e0 + j < vocab ? logit<T>(row, e0 + j) : -INFINITY;
+    double mine = 0.0;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      p[j] = e0 + j < vocab ? expf(p[j] / temperature - Ms) : 0.f;
+      mine += (double)p[j];
+    }
+    double lo, hi, tot;
+    block_scan_d(mine, lo, hi, tot, s);
+    lo += clo;
+    hi += clo;
+    const double end = clo + tot;
+    if (lo < hi && lo <= target && (target < hi || hi >= end)) {
+      double acc = lo;
+      int tok = -1, last = -1;
+#pragma unroll
+      for (int j = 0; j < kPer; ++j)
+        if (p[j] > 0.f) {
+          last = e0 + j;
+          acc += (double)p[j];
+          if (tok < 0 && acc > target) tok = e0 + j;
+        }
+      out[r] = tok >= 0 ? tok : last;
+    }
+    return;
+  }
+
+  // ---- top_k: the candidates of all segments, in index order ----
+  if (wave == 0) {
+    const int g0 = 2 * lane, g1 = 2 * lane + 1;
+    const int c0 = g0 < G ? ws.count[(size_t)r * G + g0] : 0;
+    const int c1 = g1 < G ? ws.count[(size_t)r * G + g1] : 0;
+    const int incl = wave_incl_scan_i(c0 + c1, lane);
+    if (g0 < G) s.off[g0] = incl - c0 - c1;
+    if (g1 < G) s.off[g1] = incl - c1;
+    if (lane == 63) s.off[G] = incl;
+  }
+  __syncthreads();
+  const int C = s.off[G];
+  const bool staged = C <= kLdsCand;
+  // position in the workspace of flat candidate f: the last segment whose
+  // list starts at or before f (empty lists share their start with the next)
+  auto locate = [&](int f) -> size_t {
+    int lo = 0, hi = G - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s.off[mid] <= f)
+        lo = mid;
+      else
+        hi = mid - 1;
+    }
+    return (size_t)r * vocab + (size_t)lo * kSeg + (size_t)(f - s.off[lo]);
+  };
+  if (staged) {
+    for (int f0 = tid; f0 < C; f0 += 4 * kBT) {
+      size_t at[4];
+      float vx[4];
+      int vi[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) at[q] = f0 + q * kBT < C ? locate(f0 + q * kBT) : 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (f0 + q * kBT < C) {
+          vx[q] = ws.cx[at[q]];
+          vi[q] = ws.ci[at[q]];
+        }
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (f0 + q * kBT < C) {
+          s.cx[f0 + q * kBT] = vx[q];
+          s.ci[f0 + q * kBT] = vi[q];
+        }
+    }
+    __syncthreads();
+  }
+  auto cand_x = [&](int f) -> float { return staged ? s.cx[f] : ws.cx[locate(f)]; };
+  auto cand_i = [&](int f) -> int { return staged ? s.ci[f] : ws.ci[locate(f)]; };
+
+  // the row's k-th largest key among the candidates (C >= top_k: every
+  // segment kept min(top_k, its size) or more)
+  const unsigned thr = kth_key(
+      [&](auto&& fn) {
+        for (int f = tid; f < C; f += kBT) fn(order_key(cand_x(f)));
+      },
+      (unsigned)top_k, s);
+
+  // inverse CDF over the kept candidates, contiguous runs per thread
+  const int run = (C + kBT - 1) / kBT;
+  const int f0 = min(C, tid * run), f1 = min(C, f0 + run);
+  double mine = 0.0;
+  for (int f = f0; f < f1; ++f) {
+    const float xv = cand_x(f);
+    if (order_key(xv) >= thr) mine += (double)expf(xv / temperature - Ms);
+  }
+  double lo, hi, total;
+  block_scan_d(mine, lo, hi, total, s);
+  const double target = u * total;
+  if (lo < hi && lo <= target && (target < hi || hi >= total)) {
+    double acc = lo;
+    int tok = -1, last = -1;
+    for (int f = f0; f < f1; ++f) {
+      const float xv = cand_x(f);
+      if (order_key(xv) < thr) continue;
+      const float pv = expf(xv / temperature - Ms);
+      if (pv > 0.f) {
+        last = f;
+        acc += (double)pv;
+        if (tok < 0 && acc > target) tok = f;
+      }
+    }
+    out[r] = cand_i(tok >= 0 ? tok : last);
   }
 }
 
 template <typename T>
 void launch(const void* logits, int rows, int vocab, int64_t row_stride, float temperature, int top_k,
-            const double* uniforms, int32_t* tokens, hipStream_t st) {
-  hipLaunchKernelGGL((sample_kernel<T>), dim3((unsigned)rows), dim3(kSThreads), 0, st, logits, row_stride, vocab,
-                     temperature, top_k, uniforms, tokens);
+            const double* uniforms, int32_t* tokens, const Ws& ws, hipStream_t st) {
+  const int G = n_segments(vocab);
+  hipLaunchKernelGGL((segment_kernel<T>), dim3((unsigned)G, (unsigned)rows), dim3(kBT), 0, st, logits, row_stride,
+                     vocab, temperature, top_k, ws);
+  hipLaunchKernelGGL((finish_kernel<T>), dim3((unsigned)rows), dim3(kBT), 0, st, logits, row_stride, vocab,
+                     temperature, top_k, uniforms, tokens, ws, G);
 }
 
 }  // namespace
@@ -340,17 +539,26 @@ extern "C" {
 
 int tl_sample_max_vocab(void) { return kMaxVocab; }
 
+size_t tl_sample_workspace_bytes(int rows, int vocab) {
+  if (rows <= 0 || rows > kMaxRows || vocab <= 0 || vocab > kMaxVocab) return 0;
+  return ws_layout(rows, vocab, nullptr, nullptr);
+}
+
 int tl_sample(const void* logits, int rows, int vocab, int64_t row_stride, float temperature, int top_k,
-              const double* uniforms, int32_t* tokens, int dtype, void* stream) {
-  if (rows < 0 || vocab <= 0 || vocab > kMaxVocab || row_stride < vocab || top_k < 0) return TL_ERR_INVALID;
+              const double* uniforms, int32_t* tokens, void* workspace, size_t workspace_bytes, int dtype,
+              void* stream) {
+  if (rows < 0 || rows > kMaxRows || vocab <= 0 || vocab > kMaxVocab || row_stride < vocab || top_k < 0)
+    return TL_ERR_INVALID;
   if (dtype != TL_DTYPE_F32 && dtype != TL_DTYPE_F16 && dtype != TL_DTYPE_BF16) return TL_ERR_INVALID;
   if (rows == 0) return 0;
-  if (!logits || !tokens || (temperature > 0.f && !uniforms)) return TL_ERR_INVALID;
+  if (!logits || !tokens || !workspace || (temperature > 0.f && !uniforms)) return TL_ERR_INVALID;
+  Ws ws;
+  if (workspace_bytes < ws_layout(rows, vocab, (char*)workspace, &ws)) return TL_ERR_INVALID;
   hipStream_t st = tl_resolve_stream(stream);
   switch (dtype) {
-    case TL_DTYPE_F32: launch<F32>(logits, rows, vocab, row_stride, temperature, top_k, uniforms, tokens, st); break;
-    case TL_DTYPE_F16: launch<F16>(logits, rows, vocab, row_stride, temperature, top_k, uniforms, tokens, st); break;
-    default: launch<BF16>(logits, rows, vocab, row_stride, temperature, top_k, uniforms, tokens, st);
+    case TL_DTYPE_F32: launch<F32>(logits, rows, vocab, row_stride, temperature, top_k, uniforms, tokens, ws, st); break;
+    case TL_DTYPE_F16: launch<F16>(logits, rows, vocab, row_stride, temperature, top_k, uniforms, tokens, ws, st); break;
+    default: launch<BF16>(logits, rows, vocab, row_stride, temperature, top_k, uniforms, tokens, ws, st);
   }
   return tl_launch_status();
 }

@@ -37,13 +37,15 @@ _GREEDY_T = 1e-6  # model.py:569
 
 
 class _Buffers:
-    """Small device buffers reused across calls (copies and kernels are
-    ordered on the library stream, so reuse cannot overtake a pending kernel)."""
+    """Device buffers reused across calls (copies and kernels are ordered on
+    the library stream, so reuse cannot overtake a pending kernel): the draw
+    and token of :func:`sample`, and the sampler's workspace."""
 
     def __init__(self):
         self.cap = 0
         self.u = None
         self.tok = None
+        self.ws = None
 
     def get(self, rows: int):
         if rows > self.cap:
@@ -51,6 +53,15 @@ class _Buffers:
             self.u = gpu.allocate((self.cap,), np.float64)
             self.tok = gpu.allocate((self.cap,), np.int32)
         return self.u, self.tok
+
+    def workspace(self, rows: int, vocab: int):
+        need = int(gpu.runtime().tl_sample_workspace_bytes(rows, vocab))
+        if need == 0:
+            raise ValueError(f"sampling {rows} rows of vocab {vocab} is not supported "
+                             f"(rows <= 65535, vocab <= {max_vocab()})")
+        if self.ws is None or self.ws.nbytes < need:
+            self.ws = gpu.allocate((need,), np.uint8)
+        return self.ws
 
 
 _bufs = _Buffers()
@@ -73,9 +84,10 @@ def _launch(ptr: int, rows: int, vocab: int, row_stride: int, itemsize_dtype, te
     t = float(np.float32(temperature)) if temperature > _GREEDY_T else 0.0
     k = int(top_k) if top_k > 0 else 0
     k = min(k, vocab)
+    ws = _bufs.workspace(rows, vocab)
     status = gpu.runtime().tl_sample(ctypes.c_void_p(ptr), rows, vocab, row_stride, t, k,
                                      vp(u_dev) if t > 0.0 else ctypes.c_void_p(None), vp(tok_dev),
-                                     gpu.dtype_code(itemsize_dtype), None)
+                                     vp(ws), ws.nbytes, gpu.dtype_code(itemsize_dtype), None)
     check_status(status, "sample")
 
 
