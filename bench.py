@@ -586,7 +586,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build measures one GPU only; the attention path does not "
-                                   "shard across GPUs (see DESIGN.md for how it would)",
+                                   "shard across GPUs in this build",
                           "n_gpus": args.gpus}))
         sys.exit(2)
 
@@ -642,7 +642,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": DT_SHORT[cfg.dtype],
-        "data": "synthetic (seeded N(0,1) inputs, BASELINE.md recipe)",
+        "data": "synthetic (seeded N(0,1) q/k/v, decode lengths drawn U[4096, 16383])",
         "config": {
             "workload": f"{cfg.name} (config {head})" + (" + llama3.2-3b-prefill-bf16 (config 5a)" if "5a" in results and head == "5b" else ""),
             "batch": cfg.batch, "n_head": cfg.n_head, "n_kv_head": cfg.n_kv_head, "d_k": cfg.d_k,

@@ -157,8 +157,7 @@ int tl_rope_kv_append(void* q, const void* k_new, const void* v_new,
                       const int64_t* v_cache_strides, int dtype, void* stream);
 
 /* ---------------------------------------------------------------------------
- * Dense projection GEMM of the model step (the row SURVEY lists after the
- * attention path): C = A . B, row-major, A (m, k) with row stride lda, B
+ * Dense projection GEMM of the model step: C = A . B, row-major, A (m, k) with row stride lda, B
  * (k, n) with ldb, C (m, n) with ldc, all of one dtype, fp32 accumulation.
  * Replaces the Triton GEMM gemm(h_dev, w_dev, out_dev)
  * (triton_llm/kernels/gemm.py:53-108) used for every projection in
