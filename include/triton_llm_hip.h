@@ -220,6 +220,13 @@ size_t tl_sample_workspace_bytes(int rows, int vocab);
 int tl_sample(const void* logits, int rows, int vocab, int64_t row_stride, float temperature,
               int top_k, const double* uniforms, int32_t* tokens, void* workspace,
               size_t workspace_bytes, int dtype, void* stream);
+/* One row, the draw passed by value: the per-token call of the models'
+ * generate loops (smollm2_triton/model.py:458-460), with no draw upload.
+ * Same results as tl_sample with rows = 1 and uniforms = {uniform};
+ * workspace: tl_sample_workspace_bytes(1, vocab). */
+int tl_sample_row(const void* logits, int vocab, float temperature, int top_k, double uniform,
+                  int32_t* token, void* workspace, size_t workspace_bytes, int dtype,
+                  void* stream);
 
 #ifdef __cplusplus
 }

@@ -254,3 +254,22 @@ def test_workspace_reuse_across_layouts():
         bad, near = compare(x, 1.1, k, u, run_rows(x, "float32", 1.1, k, u))
         assert not bad and near <= 1
         np.testing.assert_array_equal(run_rows(x, "float32", 0.0, 0, None), np.argmax(x, axis=1))
+
+
+def test_sample_row_equals_batched_entry():
+    """tl_sample_row (draw by value) gives tl_sample's tokens for the same draws."""
+    lib = gpu.runtime()
+    rng = np.random.default_rng(33)
+    for V, T, k in ((100, 1.0, 0), (49152, 0.8, 50), (128256, 0.7, 0), (5000, 0.0, 0)):
+        x = rng.standard_normal((6, V)).astype(np.float32)
+        u = rng.random(6)
+        want = run_rows(x, "float32", T, k, u)
+        nws = lib.tl_sample_workspace_bytes(1, V)
+        ws = gpu.allocate((nws,), np.uint8)
+        tok = gpu.allocate((1,), np.int32)
+        for r in range(6):
+            row = gpu.to_device(x[r])
+            assert lib.tl_sample_row(row.ptr, V, T, k, float(u[r]), tok.ptr, ws.ptr, nws, 0, None) == 0
+            gpu.synchronize()
+            assert int(tok.to_numpy()[0]) == int(want[r])
+        assert lib.tl_sample_row(row.ptr, V, T, k, 0.5, tok.ptr, ws.ptr, nws - 1, 0, None) != 0

@@ -334,7 +334,7 @@ __global__ __launch_bounds__(kBT) void segment_kernel(const void* logits, int64_
 template <typename T>
 __global__ __launch_bounds__(kBT) void finish_kernel(const void* logits, int64_t row_stride, int vocab,
                                                      float temperature, int top_k, const double* uniforms,
-                                                     int32_t* out, Ws ws, int G) {
+                                                     double uniform, int32_t* out, Ws ws, int G) {
   __shared__ LdsFin s;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = blockIdx.x;
@@ -352,7 +352,7 @@ __global__ __launch_bounds__(kBT) void finish_kernel(const void* logits, int64_t
   if (tid == 0) out[r] = greedy ? A : -1;  // sampling: replaced below by the thread holding the draw
   if (greedy || !(M > -INFINITY && M < INFINITY)) return;
   const float Ms = M / temperature;
-  const double u = fmin(fmax(uniforms[r], 0.0), 1.0);
+  const double u = fmin(fmax(uniforms ? uniforms[r] : uniform, 0.0), 1.0);
 
   if (!filter) {
     // segment weights: mass at the segment maximum rescaled to the row's
@@ -525,12 +525,12 @@ __global__ __launch_bounds__(kBT) void finish_kernel(const void* logits, int64_t
 
 template <typename T>
 void launch(const void* logits, int rows, int vocab, int64_t row_stride, float temperature, int top_k,
-            const double* uniforms, int32_t* tokens, const Ws& ws, hipStream_t st) {
+            const double* uniforms, double uniform, int32_t* tokens, const Ws& ws, hipStream_t st) {
   const int G = n_segments(vocab);
   hipLaunchKernelGGL((segment_kernel<T>), dim3((unsigned)G, (unsigned)rows), dim3(kBT), 0, st, logits, row_stride,
                      vocab, temperature, top_k, ws);
   hipLaunchKernelGGL((finish_kernel<T>), dim3((unsigned)rows), dim3(kBT), 0, st, logits, row_stride, vocab,
-                     temperature, top_k, uniforms, tokens, ws, G);
+                     temperature, top_k, uniforms, uniform, tokens, ws, G);
 }
 
 }  // namespace
@@ -544,23 +544,49 @@ size_t tl_sample_workspace_bytes(int rows, int vocab) {
   return ws_layout(rows, vocab, nullptr, nullptr);
 }
 
-int tl_sample(const void* logits, int rows, int vocab, int64_t row_stride, float temperature, int top_k,
-              const double* uniforms, int32_t* tokens, void* workspace, size_t workspace_bytes, int dtype,
-              void* stream) {
+}  // extern "C"
+
+namespace {
+
+int sample_impl(const void* logits, int rows, int vocab, int64_t row_stride, float temperature, int top_k,
+                const double* uniforms, double uniform, int32_t* tokens, void* workspace, size_t workspace_bytes,
+                int dtype, void* stream) {
   if (rows < 0 || rows > kMaxRows || vocab <= 0 || vocab > kMaxVocab || row_stride < vocab || top_k < 0)
     return TL_ERR_INVALID;
   if (dtype != TL_DTYPE_F32 && dtype != TL_DTYPE_F16 && dtype != TL_DTYPE_BF16) return TL_ERR_INVALID;
   if (rows == 0) return 0;
-  if (!logits || !tokens || !workspace || (temperature > 0.f && !uniforms)) return TL_ERR_INVALID;
+  if (!logits || !tokens || !workspace) return TL_ERR_INVALID;
   Ws ws;
   if (workspace_bytes < ws_layout(rows, vocab, (char*)workspace, &ws)) return TL_ERR_INVALID;
   hipStream_t st = tl_resolve_stream(stream);
   switch (dtype) {
-    case TL_DTYPE_F32: launch<F32>(logits, rows, vocab, row_stride, temperature, top_k, uniforms, tokens, ws, st); break;
-    case TL_DTYPE_F16: launch<F16>(logits, rows, vocab, row_stride, temperature, top_k, uniforms, tokens, ws, st); break;
-    default: launch<BF16>(logits, rows, vocab, row_stride, temperature, top_k, uniforms, tokens, ws, st);
+    case TL_DTYPE_F32:
+      launch<F32>(logits, rows, vocab, row_stride, temperature, top_k, uniforms, uniform, tokens, ws, st);
+      break;
+    case TL_DTYPE_F16:
+      launch<F16>(logits, rows, vocab, row_stride, temperature, top_k, uniforms, uniform, tokens, ws, st);
+      break;
+    default: launch<BF16>(logits, rows, vocab, row_stride, temperature, top_k, uniforms, uniform, tokens, ws, st);
   }
   return tl_launch_status();
+}
+
+}  // namespace
+
+extern "C" {
+
+int tl_sample(const void* logits, int rows, int vocab, int64_t row_stride, float temperature, int top_k,
+              const double* uniforms, int32_t* tokens, void* workspace, size_t workspace_bytes, int dtype,
+              void* stream) {
+  if (temperature > 0.f && !uniforms) return TL_ERR_INVALID;
+  return sample_impl(logits, rows, vocab, row_stride, temperature, top_k, uniforms, 0.0, tokens, workspace,
+                     workspace_bytes, dtype, stream);
+}
+
+int tl_sample_row(const void* logits, int vocab, float temperature, int top_k, double uniform, int32_t* token,
+                  void* workspace, size_t workspace_bytes, int dtype, void* stream) {
+  return sample_impl(logits, 1, vocab, vocab, temperature, top_k, nullptr, uniform, token, workspace,
+                     workspace_bytes, dtype, stream);
 }
 
 }  // extern "C"

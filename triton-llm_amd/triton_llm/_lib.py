@@ -83,6 +83,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tl_sample_max_vocab": (_c_int, []),
     "tl_sample_workspace_bytes": (_c_size, [_c_int, _c_int]),
     "tl_sample": (_c_int, [_vp, _c_int, _c_int, _c_i64, _c_float, _c_int, _vp, _vp, _vp, _c_size, _c_int, _vp]),
+    "tl_sample_row": (_c_int, [_vp, _c_int, _c_float, _c_int, ctypes.c_double, _vp, _vp, _c_size, _c_int, _vp]),
 }
 
 _lib: ctypes.CDLL | None = None

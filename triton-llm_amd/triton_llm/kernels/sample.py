@@ -10,6 +10,7 @@ gpt2_triton/model.py:424-438), which needs the logits row downloaded first:
   otherwise one uniform draw from NumPy's global stream -- the draw
   ``np.random.choice`` itself would take -- so ``np.random.seed(s)`` makes
   runs repeatable as the reference's server does (scripts/serve_model.py:391).
+  The draw goes to the device as a kernel argument (``tl_sample_row``).
   ``top_k <= 0`` keeps every entry, ``top_k`` beyond the vocabulary is capped.
 * :func:`sample_rows` -- one token per row of ``(rows, vocab)`` logits into a
   device int32 tensor, with caller-supplied draws or draws from NumPy's
@@ -38,21 +39,17 @@ _GREEDY_T = 1e-6  # model.py:569
 
 class _Buffers:
     """Device buffers reused across calls (copies and kernels are ordered on
-    the library stream, so reuse cannot overtake a pending kernel): the draw
-    and token of :func:`sample`, and the sampler's workspace."""
+    the library stream, so reuse cannot overtake a pending kernel): the token
+    of :func:`sample` and the sampler's workspace."""
 
     def __init__(self):
-        self.cap = 0
-        self.u = None
         self.tok = None
         self.ws = None
 
-    def get(self, rows: int):
-        if rows > self.cap:
-            self.cap = max(rows, 64)
-            self.u = gpu.allocate((self.cap,), np.float64)
-            self.tok = gpu.allocate((self.cap,), np.int32)
-        return self.u, self.tok
+    def token(self):
+        if self.tok is None:
+            self.tok = gpu.allocate((1,), np.int32)
+        return self.tok
 
     def workspace(self, rows: int, vocab: int):
         need = int(gpu.runtime().tl_sample_workspace_bytes(rows, vocab))
@@ -99,12 +96,15 @@ def sample(logits_dev: "gpu.DeviceTensor", temperature: float, top_k: int, row: 
     if not -rows <= row < rows:
         raise IndexError(f"row {row} out of range for {rows} rows")
     row %= rows
-    u_dev, tok_dev = _bufs.get(1)
+    tok_dev = _bufs.token()
     greedy = not temperature > _GREEDY_T
-    if not greedy:
-        u_dev.from_numpy(np.full(u_dev.shape, np.random.random_sample(), np.float64))
+    u = 0.0 if greedy else float(np.random.random_sample())  # greedy consumes no draw
+    t = 0.0 if greedy else float(np.float32(temperature))
+    k = min(int(top_k), vocab) if top_k > 0 else 0
+    ws = _bufs.workspace(1, vocab)
     ptr = logits_dev.data_ptr() + row * vocab * logits_dev.dtype.itemsize
-    _launch(ptr, 1, vocab, vocab, logits_dev.dtype, temperature, top_k, u_dev, tok_dev)
+    check_status(gpu.runtime().tl_sample_row(ctypes.c_void_p(ptr), vocab, t, k, u, vp(tok_dev), vp(ws), ws.nbytes,
+                                             gpu.dtype_code(logits_dev.dtype), None), "sample")
     tok = int(tok_dev.to_numpy()[0])
     if tok < 0:
         raise ValueError("probabilities contain NaN")
