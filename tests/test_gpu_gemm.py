@@ -55,6 +55,35 @@ def test_gemm_projection_shapes(dtype, M, K, N):
         np.testing.assert_allclose(got, exp, rtol=8e-3, atol=1e-2)
 
 
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+@pytest.mark.parametrize("M", [1, 4])
+@pytest.mark.parametrize("K,N", [(960, 49152), (576, 49152), (1024, 65536), (1040, 65536)])
+def test_gemm_lm_head_shapes(dtype, M, K, N):
+    """The lm_head of a decoded token: so many column tiles that K is one
+    slice (960, 576, 1024), stored straight to C with no reduce pass; 1040 just
+    past one slice takes the reduce.  Also into a strided C (ldc > N)."""
+    rng = np.random.default_rng(K + M)
+    a = on.to_storage(rng.standard_normal((M, K), dtype=np.float32), dtype)
+    b = on.to_storage(rng.standard_normal((K, N), dtype=np.float32) / np.sqrt(K), dtype)
+    exp = gemm_ref(on.from_storage(a, dtype), on.from_storage(b, dtype))
+    got = on.from_storage(gemm_cpu(a, b, dtype), dtype)
+    tol = (2e-3, 0.0) if dtype == "float32" else (1e-2, 8e-3)
+    np.testing.assert_allclose(got, exp, atol=tol[0], rtol=tol[1])
+    # strided C through the C ABI: row stride N + 64, padding left untouched
+    lib = gpu.runtime()
+    code = gpu.dtype_code(H.GPU_DTYPES[dtype])
+    ldc = N + 64
+    pad = np.full((M, ldc), 7.0, np.float32)
+    c_dev = H.upload(on.to_storage(pad, dtype), dtype)
+    a_dev, b_dev = H.upload(a, dtype), H.upload(b, dtype)
+    nws = lib.tl_gemm_workspace_bytes(M, N, K, code)
+    ws = gpu.allocate((max(nws, 1),), np.uint8)
+    assert lib.tl_gemm(a_dev.ptr, b_dev.ptr, c_dev.ptr, M, N, K, K, N, ldc, ws.ptr, nws, code, None) == 0
+    c = on.from_storage(H.download(c_dev), dtype)
+    np.testing.assert_allclose(c[:, :N], exp, atol=tol[0], rtol=tol[1])
+    assert (c[:, N:] == 7.0).all()
+
+
 @pytest.mark.parametrize("M,K,N", [(1, 130, 33), (2, 7, 40), (5, 1000, 100), (8, 4100, 260)])
 def test_gemm_few_rows_odd_shapes(M, K, N):
     """Few-row products on shapes the streaming kernel handles partly (a

@@ -92,10 +92,13 @@ __device__ __forceinline__ void unpack_words(const u32x4& w, float (&f)[16 / T::
 // reads 16 bytes of row k0 + 16 i + 4 w + r, columns chunk c; its MT x CPC
 // sums cover the rows it read.  The four row groups of a wave, then the four
 // waves, are added up and the slice's partial product is stored.
+// With a single K-slice (gridDim.y == 1) the sums are the result: they are
+// rounded and stored to C directly, and no reduce pass follows.
 template <typename T, int MT>
 __global__ __launch_bounds__(kSkThreads) void skinny_partial_kernel(const void* __restrict__ a, const void* __restrict__ b,
-                                                                     float* __restrict__ ws, int m, int n, int k,
-                                                                     int64_t lda, int64_t ldb, int tk) {
+                                                                     float* __restrict__ ws, void* __restrict__ out,
+                                                                     int m, int n, int k, int64_t lda, int64_t ldb,
+                                                                     int64_t ldc, int tk) {
   constexpr int CPC = 16 / T::size;  // columns per 16-byte chunk
   constexpr int COLS = 16 * CPC;     // columns per tile
   using Bits = typename T::bits;
@@ -176,8 +179,13 @@ __global__ __launch_bounds__(kSkThreads) void skinny_partial_kernel(const void* 
   for (int idx = tid; idx < MT * COLS; idx += kSkThreads) {
     const int mi = idx / COLS, cc = idx % COLS;
     const int col = blockIdx.x * COLS + cc;
-    if (mi < m && col < n)
-      ws[((int64_t)blockIdx.y * m + mi) * n + col] = s_sum[0][mi][cc] + s_sum[1][mi][cc] + s_sum[2][mi][cc] + s_sum[3][mi][cc];
+    if (mi < m && col < n) {
+      const float v = s_sum[0][mi][cc] + s_sum[1][mi][cc] + s_sum[2][mi][cc] + s_sum[3][mi][cc];
+      if (gridDim.y == 1)
+        ((Bits*)out)[(int64_t)mi * ldc + col] = from_f32<T>(v);
+      else
+        ws[((int64_t)blockIdx.y * m + mi) * n + col] = v;
+    }
   }
 }
 
@@ -207,15 +215,19 @@ int launch_skinny(const void* a, const void* b, void* c, int m, int n, int k, in
   const SkinnyPlan s = skinny_plan(n, k, T::size);
   dim3 grid((unsigned)s.n_tiles, (unsigned)s.ks);
   if (m <= 1)
-    hipLaunchKernelGGL((skinny_partial_kernel<T, 1>), grid, dim3(kSkThreads), 0, st, a, b, (float*)ws, m, n, k, lda, ldb, s.tk);
+    hipLaunchKernelGGL((skinny_partial_kernel<T, 1>), grid, dim3(kSkThreads), 0, st, a, b, (float*)ws, c, m, n, k, lda, ldb,
+                       ldc, s.tk);
   else if (m <= 2)
-    hipLaunchKernelGGL((skinny_partial_kernel<T, 2>), grid, dim3(kSkThreads), 0, st, a, b, (float*)ws, m, n, k, lda, ldb, s.tk);
+    hipLaunchKernelGGL((skinny_partial_kernel<T, 2>), grid, dim3(kSkThreads), 0, st, a, b, (float*)ws, c, m, n, k, lda, ldb,
+                       ldc, s.tk);
   else if (m <= 4)
-    hipLaunchKernelGGL((skinny_partial_kernel<T, 4>), grid, dim3(kSkThreads), 0, st, a, b, (float*)ws, m, n, k, lda, ldb, s.tk);
+    hipLaunchKernelGGL((skinny_partial_kernel<T, 4>), grid, dim3(kSkThreads), 0, st, a, b, (float*)ws, c, m, n, k, lda, ldb,
+                       ldc, s.tk);
   else
-    hipLaunchKernelGGL((skinny_partial_kernel<T, 8>), grid, dim3(kSkThreads), 0, st, a, b, (float*)ws, m, n, k, lda, ldb, s.tk);
+    hipLaunchKernelGGL((skinny_partial_kernel<T, 8>), grid, dim3(kSkThreads), 0, st, a, b, (float*)ws, c, m, n, k, lda, ldb,
+                       ldc, s.tk);
   int e = tl_launch_status();
-  if (e) return e;
+  if (e || s.ks == 1) return e;
   const int64_t outs = (int64_t)m * n;
   hipLaunchKernelGGL((skinny_reduce_kernel<T>), dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, st,
                      (const float*)ws, c, m, n, ldc, s.ks);
