@@ -463,20 +463,22 @@ __global__ __launch_bounds__(kBT) void finish_kernel(const void* logits, int64_t
     return (size_t)r * vocab + (size_t)lo * kSeg + (size_t)(f - s.off[lo]);
   };
   if (staged) {
-    for (int f0 = tid; f0 < C; f0 += 4 * kBT) {
-      size_t at[4];
-      float vx[4];
-      int vi[4];
+    // kStage loads per thread in flight: up to 4096 candidates in one round trip
+    constexpr int kStage = 16;
+    for (int f0 = tid; f0 < C; f0 += kStage * kBT) {
+      size_t at[kStage];
+      float vx[kStage];
+      int vi[kStage];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) at[q] = f0 + q * kBT < C ? locate(f0 + q * kBT) : 0;
+      for (int q = 0; q < kStage; ++q) at[q] = f0 + q * kBT < C ? locate(f0 + q * kBT) : 0;
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
+      for (int q = 0; q < kStage; ++q)
         if (f0 + q * kBT < C) {
           vx[q] = ws.cx[at[q]];
           vi[q] = ws.ci[at[q]];
         }
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
+      for (int q = 0; q < kStage; ++q)
         if (f0 + q * kBT < C) {
           s.cx[f0 + q * kBT] = vx[q];
           s.ci[f0 + q * kBT] = vi[q];
