@@ -113,6 +113,9 @@ int tl_attention_fwd(const void* q, const void* k, const void* v, void* o,
  * Q/O: (batch, n_head, d_k) with {batch, head} strides.  Caches:
  * (batch, n_kv_head, max_ctx, d_k) with {batch, head, seq} strides.
  * Sequence b attends to positions [0, min(cache_lens[b] + len_add, max_ctx)).
+ * cache_lens may be NULL: every sequence then attends to len_add positions
+ * (a caller that knows the length on the host passes it by value, with no
+ * upload).
  * The cached positions of all sequences and KV heads are cut into equal
  * shares, one per resident workgroup of the device; split_size (multiple of
  * 16; 0 picks tl_decode_split_size) is the smallest share, which bounds the

@@ -48,9 +48,26 @@ def attention_gqa_cpu(q, k, v, n_head, n_kv_head, causal=True, dtype="float32", 
 
 
 def max_abs(a, b) -> float:
-    a = np.asarray(a, dtype=np.float64)
-    b = np.asarray(b, dtype=np.float64)
-    return float(np.nanmax(np.abs(a - b))) if a.size else 0.0
+    """Largest |a - b| over the broadcast arrays, NaN-strict.
+
+    A NaN on one side only makes the error +inf, so a partly-NaN result can
+    never pass a tolerance.  NaN on both sides at the same position counts as
+    agreement (fully masked rows are NaN by definition), and equal
+    infinities count as zero error.
+    """
+    a, b = np.broadcast_arrays(np.asarray(a, dtype=np.float64), np.asarray(b, dtype=np.float64))
+    if a.size == 0:
+        return 0.0
+    nan_a, nan_b = np.isnan(a), np.isnan(b)
+    if np.any(nan_a != nan_b):
+        return float("inf")
+    keep = ~nan_a
+    a, b = a[keep], b[keep]
+    if a.size == 0:
+        return 0.0
+    diff = np.abs(a - b)
+    diff[a == b] = 0.0  # inf == inf
+    return float(diff.max())
 
 
 def report(name: str, err: float, tol: float) -> None:

@@ -55,7 +55,11 @@ def test_prefill_config_5a_full_size_sampled_rows():
     got = gpu_prefill(cfg, oi.make_prefill_raw(cfg))
     assert np.all(np.isfinite(got))
     ref = oi.make_prefill(cfg)
-    rows = np.unique(np.concatenate([np.arange(0, 8), np.arange(127, 136),
+    # Both rows either side of every 256-row query-tile boundary (255/256,
+    # 511/512, ... 8191), the 128-key boundary, the first and last rows, and
+    # an even spread in between.
+    tile = np.arange(256, cfg.seq, 256)
+    rows = np.unique(np.concatenate([np.arange(0, 8), np.arange(127, 136), tile - 1, tile,
                                      np.linspace(0, cfg.seq - 1, 48).astype(int),
                                      np.arange(cfg.seq - 8, cfg.seq)]))
     exp = oa.attention_bhsd(ref["q"], ref["k"], ref["v"], causal=True, sm_scale=cfg.scale,

@@ -138,7 +138,7 @@ struct DecodeParams {
 };
 
 __device__ __forceinline__ int ctx_len(const DecodeParams& p, int b) {
-  int c = p.lens[b] + p.len_add;
+  int c = (p.lens ? p.lens[b] : 0) + p.len_add;
   c = c < 0 ? 0 : c;
   return c > p.max_ctx ? p.max_ctx : c;
 }
@@ -654,7 +654,7 @@ int tl_attention_decode(const void* q, const void* k_cache, const void* v_cache,
                         float sm_scale, int split_size, int dtype,
                         void* stream) {
   if (batch == 0 || n_head == 0) return 0;
-  if (!q || !k_cache || !v_cache || !cache_lens || !o || !workspace || batch < 0 ||
+  if (!q || !k_cache || !v_cache || !o || !workspace || batch < 0 ||
       n_head < 0 || n_kv_head < 1 || n_head % n_kv_head != 0 || max_ctx < 1 ||
       !q_strides || !k_strides || !v_strides || !o_strides)
     return TL_ERR_INVALID;

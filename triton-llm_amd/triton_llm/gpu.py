@@ -15,12 +15,23 @@ ziliangpeng/triton-llm: ``DeviceTensor`` :184-227, ``allocate`` :230,
   synchronisation.  ``to_host`` waits for that stream before returning.
 * bfloat16 is a first-class storage dtype: ``gpu.bfloat16`` is a uint16 NumPy
   dtype tagged with metadata, and host arrays of it hold raw bf16 bit patterns.
+* Freed blocks are cached for reuse.  ``hipFree`` waits for the whole
+  device, so the reference's free-on-``__del__`` puts a device
+  synchronisation into every call that drops a temporary.  Here a dropped
+  tensor's block (up to ``POOL_MAX_BLOCK`` bytes, ``POOL_MAX_BYTES`` in all)
+  goes to a free list keyed by its rounded size, and the next ``allocate`` of
+  that size takes it without ``hipMalloc``.  Reuse is safe because every
+  kernel and copy of this package runs on the one library stream: work that
+  used the block is ordered before any work that uses it again.  Blocks are
+  uninitialised either way.  ``empty_cache()`` returns the cached blocks to
+  HIP, and an allocation that fails empties the cache and tries once more.
 """
 
 from __future__ import annotations
 
 import ctypes
 import os
+import threading
 
 import numpy as np
 
@@ -103,8 +114,65 @@ def check_error(err):
         raise RuntimeError(f"GPU runtime error ({_backend or 'hip'}): {err} ({_lib.error_string(err)})")
 
 
+# ---- block cache -------------------------------------------------------------
+
+POOL_MAX_BLOCK = 256 << 20  # larger blocks go straight back to hipFree
+POOL_MAX_BYTES = 2 << 30    # most bytes held in freed blocks
+_POOL_ALIGN = 256
+_pool: dict[int, list[int]] = {}
+_pool_bytes = 0
+_pool_lock = threading.Lock()
+
+
+def _block_size(nbytes: int) -> int:
+    return (nbytes + _POOL_ALIGN - 1) // _POOL_ALIGN * _POOL_ALIGN
+
+
+def _take_block(size: int):
+    """A cached block of exactly ``size`` bytes (address), or None."""
+    global _pool_bytes
+    with _pool_lock:
+        blocks = _pool.get(size)
+        if blocks:
+            _pool_bytes -= size
+            return blocks.pop()
+    return None
+
+
+def _release_block(addr: int, size: int) -> None:
+    """Keep a dropped tensor's block for reuse, or hand it back to HIP."""
+    global _pool_bytes
+    with _pool_lock:
+        if size <= POOL_MAX_BLOCK and _pool_bytes + size <= POOL_MAX_BYTES:
+            _pool.setdefault(size, []).append(addr)
+            _pool_bytes += size
+            return
+    _rt.tl_free(ctypes.c_void_p(addr))
+
+
+def empty_cache() -> None:
+    """Return every cached free block to HIP (hipFree)."""
+    global _pool_bytes
+    with _pool_lock:
+        blocks = [a for lst in _pool.values() for a in lst]
+        _pool.clear()
+        _pool_bytes = 0
+    for addr in blocks:
+        _rt.tl_free(ctypes.c_void_p(addr))
+
+
+def cached_bytes() -> int:
+    """Bytes held in cached free blocks."""
+    return _pool_bytes
+
+
 class DeviceTensor:
-    """Wrapper for a GPU device pointer with automatic cleanup (reference gpu.py:184)."""
+    """Wrapper for a GPU device pointer with automatic cleanup (reference gpu.py:184).
+
+    An owning tensor's block goes back to the block cache when the tensor is
+    dropped (see the module docstring); a view (``defer_free=False``) owns
+    nothing.
+    """
 
     def __init__(self, ptr, shape, dtype, nbytes, defer_free=True):
         self.ptr = ptr
@@ -117,7 +185,7 @@ class DeviceTensor:
         if getattr(self, "_defer_free", False) and self.ptr and self.ptr.value is not None:
             try:
                 if _rt is not None:
-                    _rt.tl_free(self.ptr)
+                    _release_block(self.ptr.value, _block_size(self.nbytes))
             except Exception:
                 pass
 
@@ -150,12 +218,23 @@ class DeviceTensor:
 
 
 def allocate(shape, dtype=np.float32):
-    """Allocate (uninitialised) memory on the GPU."""
+    """Allocate (uninitialised) memory on the GPU: a cached block of the same
+    rounded size if one is free, else ``hipMalloc``."""
     _initialize()
     shape = tuple(int(s) for s in shape)
     nbytes = int(np.prod(shape) * np.dtype(dtype).itemsize)
+    if nbytes == 0:
+        return DeviceTensor(ctypes.c_void_p(), shape, dtype, 0)
+    size = _block_size(nbytes)
+    addr = _take_block(size)
+    if addr is not None:
+        return DeviceTensor(ctypes.c_void_p(addr), shape, dtype, nbytes)
     ptr = ctypes.c_void_p()
-    check_error(_rt.tl_malloc(ctypes.byref(ptr), nbytes))
+    err = _rt.tl_malloc(ctypes.byref(ptr), size)
+    if err != CUDA_SUCCESS and _pool_bytes:
+        empty_cache()  # out of memory with blocks cached: give them back, try once more
+        err = _rt.tl_malloc(ctypes.byref(ptr), size)
+    check_error(err)
     return DeviceTensor(ptr, shape, dtype, nbytes)
 
 

@@ -51,12 +51,34 @@ def vp(t) -> ctypes.c_void_p:
     return t.ptr if isinstance(t.ptr, ctypes.c_void_p) else ctypes.c_void_p(t.ptr)
 
 
-def scratch(nbytes: int, workspace=None):
-    """Return a workspace of at least ``nbytes`` (the caller's if big enough)."""
+def scratch(nbytes: int, workspace=None, key: str = "scratch"):
+    """Return a workspace of at least ``nbytes``: the caller's (ValueError if
+    too small), else the shared one kept for ``key``."""
     if nbytes == 0:
         return None
     if workspace is not None:
         if workspace.nbytes < nbytes:
             raise ValueError(f"workspace holds {workspace.nbytes} bytes, {nbytes} required")
         return workspace
-    return gpu.allocate((nbytes,), np.uint8)
+    return shared_workspace(key, nbytes)
+
+
+# Workspaces kept across calls, one per purpose, grown on demand.  Every call
+# runs on the library stream, so consecutive calls are ordered and may share
+# one buffer; allocating per call would cost a hipMalloc (and the free a
+# device synchronisation) each time.
+_shared: dict[str, "gpu.DeviceTensor"] = {}
+
+
+def shared_workspace(key: str, nbytes: int):
+    """A device buffer of at least ``nbytes`` kept for ``key`` (None for 0).
+    Grows to the next power of two (at least 1 MiB) when too small."""
+    if nbytes == 0:
+        return None
+    ws = _shared.get(key)
+    if ws is None or ws.nbytes < nbytes:
+        size = max(1 << 20, 1 << (int(nbytes) - 1).bit_length())
+        _shared.pop(key, None)
+        ws = gpu.allocate((size,), np.uint8)
+        _shared[key] = ws
+    return ws

@@ -23,7 +23,7 @@ from __future__ import annotations
 import numpy as np
 
 from triton_llm import gpu
-from ._common import check_status, default_scale, same_dtype, scratch, vp
+from ._common import check_status, default_scale, same_dtype, shared_workspace, vp
 from triton_llm import _lib
 
 DECODE_D = (64, 128)
@@ -100,7 +100,7 @@ def attention_gqa(
         kv_str = _lib.strides(n_kv_head * seq_k * d_k, seq_k * d_k, d_k)
         lib = gpu.runtime()
         ws_bytes = lib.tl_attention_fwd_workspace_bytes(1, n_kv_head, seq_k, d_k, code)
-        ws = scratch(ws_bytes)
+        ws = shared_workspace("attention_gqa.prefill", ws_bytes)
         status = lib.tl_attention_fwd(
             vp(q_dev), vp(k_dev), vp(v_dev), vp(o_dev), vp(ws), ws_bytes,
             1, n_head, n_kv_head, seq_q, seq_k, d_k,
@@ -108,30 +108,25 @@ def attention_gqa(
             float(sm_scale), 1 if causal else 0, code, None,
         )
         check_status(status, "attention_gqa")
-        _keepalive(o_dev, ws)
     return o_dev
 
 
 def _decode_one(q_dev, k_dev, v_dev, o_dev, n_head, n_kv_head, seq_k, d_k, sm_scale, code):
-    """seq_q == 1: every query row sees all seq_k keys (causal or not)."""
+    """seq_q == 1: every query row sees all seq_k keys (causal or not).
+
+    The length goes to the kernel by value (``cache_lens`` NULL, ``len_add``
+    = seq_k) and the split-K partials use a workspace kept across calls, so
+    a decode step uploads nothing, waits for nothing and, once the output
+    block is cached, allocates nothing."""
     lib = gpu.runtime()
-    lens = gpu.to_device(np.array([seq_k], dtype=np.int32))
     split = lib.tl_decode_split_size(1, n_kv_head, seq_k)
     ws_bytes = lib.tl_attention_decode_workspace_bytes(1, n_head, seq_k, d_k, split)
-    ws = scratch(ws_bytes)
+    ws = shared_workspace("attention_gqa.decode", ws_bytes)
     qo = _lib.strides(n_head * d_k, d_k)
     kv = _lib.strides(n_kv_head * seq_k * d_k, seq_k * d_k, d_k)
     status = lib.tl_attention_decode(
-        vp(q_dev), vp(k_dev), vp(v_dev), vp(lens), 0, vp(o_dev), vp(ws), ws_bytes,
+        vp(q_dev), vp(k_dev), vp(v_dev), None, seq_k, vp(o_dev), vp(ws), ws.nbytes,
         1, n_head, n_kv_head, seq_k, d_k, qo, kv, kv, qo,
         float(sm_scale), split, code, None,
     )
     check_status(status, "attention_gqa(decode)")
-    _keepalive(o_dev, ws, lens)
-
-
-def _keepalive(owner, *bufs):
-    """Tie scratch buffers to the output so they are not freed before the
-    stream has consumed them (hipFree would also wait, but keeping them
-    referenced avoids the implicit device synchronisation)."""
-    owner._scratch = tuple(b for b in bufs if b is not None)

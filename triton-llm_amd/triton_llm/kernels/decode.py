@@ -154,7 +154,7 @@ def attention_decode(q_dev, k_cache, v_cache, cache_lens, n_head: int, n_kv_head
     elif int(np.prod(out.shape)) != batch * n_head * d_k or gpu.dtype_name(out.dtype) != gpu.dtype_name(q_dev.dtype):
         raise ValueError(f"out must hold (batch, n_head, d_k) of the input dtype, got {out.shape}")
     ws_bytes, split = decode_workspace_bytes(batch, n_head, n_kv_head, max_ctx, d_k, split)
-    ws = scratch(ws_bytes, workspace)
+    ws = scratch(ws_bytes, workspace, key="decode")
     qo = _lib.strides(n_head * d_k, d_k)
     c_str = _lib.strides(n_kv * max_ctx * d_k, max_ctx * d_k, d_k)
     status = gpu.runtime().tl_attention_decode(
@@ -164,8 +164,6 @@ def attention_decode(q_dev, k_cache, v_cache, cache_lens, n_head: int, n_kv_head
         float(sm_scale), split, code, None,
     )
     check_status(status, "attention_decode")
-    if workspace is None:
-        out._scratch = (ws,)
     return out
 
 

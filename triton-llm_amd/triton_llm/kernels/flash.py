@@ -45,7 +45,7 @@ def flash_attention_strided(q, k, v, out, *, batch, n_head, n_kv_head, seq_q, se
         sm_scale = default_scale(d_k)
     lib = gpu.runtime()
     ws_bytes = lib.tl_attention_fwd_workspace_bytes(batch, n_kv_head, seq_k, d_k, code)
-    ws = scratch(ws_bytes, workspace)
+    ws = scratch(ws_bytes, workspace, key="flash")
     status = lib.tl_attention_fwd(
         vp(q), vp(k), vp(v), vp(out), vp(ws), ws.nbytes if ws is not None else 0,
         batch, n_head, n_kv_head, seq_q, seq_k, d_k,
@@ -53,8 +53,6 @@ def flash_attention_strided(q, k, v, out, *, batch, n_head, n_kv_head, seq_q, se
         _lib.strides(*o_strides), float(sm_scale), 1 if causal else 0, code, None,
     )
     check_status(status, "flash_attention")
-    if workspace is None and ws is not None:
-        out._scratch = (ws,)
     return out
 
 

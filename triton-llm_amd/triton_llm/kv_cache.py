@@ -125,6 +125,13 @@ class GpuKVCache:
                 raise ValueError(f"{name} must be ({seq}, {Hkv * D}), got {t.shape}")
         prev = self._cache_len
         total_after = check_step(prev, seq, self.max_seq)
+        if cos_dev is not None and seq and prev + seq > cos_dev.shape[0]:
+            # apply_rope's check (rope.py:194-198): the kernel would skip rows
+            # past the table, leaving q unrotated and the cache row unwritten.
+            raise ValueError(
+                f"position_offset ({prev}) + seq_len ({seq}) "
+                f"exceeds cos/sin table size ({cos_dev.shape[0]})"
+            )
         cache = self.kv_cache_dev[layer]
         out = gpu.allocate((seq, H * D), q_dev.dtype)
         if seq == 0:
