@@ -1,17 +1,21 @@
 """Benchmark of the MI355X attention path on one GPU.
 
-Default workload: the Llama-3.2-3B-shaped configuration BASELINE.json quotes
-its targets on --
-  5b  decode: batch 64, 24 query / 8 KV heads, d 128, cache 16384, lengths
-      U[4096, 16383]; one step = RoPE + KV append + split-K attention;
-  5a  prefill: batch 1, 24 / 8 heads, d 128, seq 8192, causal.
-``value`` is the decode step's algorithmic HBM throughput (GB/s); the prefill
-figure (TFLOP/s) is reported in the ``prefill`` object.  Each carries a
-``roofline`` (events on the library stream around the attention kernels) and a
-``cpu_baseline`` (the NumPy oracle of the same attention on a bounded sample,
-timed on this host's cores).
+Default run: every configuration of BASELINE.json, each timed on its own with
+inputs resident in HBM --
+  1   GPT-2 causal prefill fp32 (B1 H12 D64 S128);
+  2   GPT-2 decode fp16 (B8 H12 D64, cache 1024);
+  3   SmolLM2-135M GQA causal prefill bf16 (B4 Hq9 Hkv3 D64 S2048);
+  4   SmolLM2-360M GQA decode bf16 (B32 Hq15 Hkv5 D64, cache 8192);
+  5a  Llama-3.2-3B GQA causal prefill bf16 (B1 Hq24 Hkv8 D128 S8192);
+  5b  Llama-3.2-3B GQA decode bf16 (B64 Hq24 Hkv8 D128, cache 16384);
+a decode step is RoPE + KV append + split-K attention.  ``value`` is 5b's
+decode-step HBM throughput (GB/s), the headline; 5a is repeated in the
+``prefill`` object and every config sits in ``configs``, each with its
+``roofline`` (HIP events on the library stream around the attention call) and
+``cpu_baseline`` (the NumPy oracle of the same attention, a bounded number of
+passes on this host's cores).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 5|all|1|2|3|4|5a|5b]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config all|5|1|2|3|4|5a|5b]
 """
 
 from __future__ import annotations
@@ -81,6 +85,30 @@ def profile_traffic(name):
     return None
 
 
+def clock_ramp(step, ramp_ms):
+    """Run ``step(i)`` untimed until ``ramp_ms`` of wall time has passed (at
+    most 2000 calls).  The GPU's shader clock climbs over the first tens of
+    milliseconds of sustained load; this puts the warm-up and timed steps at
+    the clock the GPU holds under a serving load, whatever --warmup is.  The
+    ramp's steps are the same work as the timed ones and are never timed.
+    Returns (calls, ms)."""
+    from triton_llm import gpu
+
+    if ramp_ms <= 0:
+        return 0, 0.0
+    t0 = time.perf_counter()
+    n = 0
+    while n < 2000:
+        step(n)
+        n += 1
+        if n % 4 == 0:
+            gpu.synchronize()
+            if (time.perf_counter() - t0) * 1e3 >= ramp_ms:
+                break
+    gpu.synchronize()
+    return n, (time.perf_counter() - t0) * 1e3
+
+
 def cpu_threads():
     n = os.environ.get("OMP_NUM_THREADS") or os.environ.get("OPENBLAS_NUM_THREADS")
     try:
@@ -111,7 +139,7 @@ def cpu_host():
 # decode
 # ---------------------------------------------------------------------------
 
-def bench_decode(cfg, steps, warmup, replicas=1, cpu=True, split=0):
+def bench_decode(cfg, steps, warmup, replicas=1, cpu=True, split=0, cpu_budget_s=10.0, ramp_ms=0.0):
     from oracle import attention as oa
     from oracle import inputs as oi
     from oracle import numerics as on
@@ -141,23 +169,25 @@ def bench_decode(cfg, steps, warmup, replicas=1, cpu=True, split=0):
     ws = decode_workspace(B, Hq, Hkv, cfg.max_ctx, D, split)
     lib = gpu.runtime()
 
-    def step(i):
+    def step(i, mark=None):
         kc, vc = caches[i % replicas]
         rope_kv_append(q, kn, vn, kc, vc, lens_d, cos_d, sin_d)
-        ev.record(3 * i + 1)
+        if mark is not None:
+            ev.record(mark)
         attention_decode(q, kc, vc, lens_d, Hq, Hkv, sm_scale=cfg.scale, len_add=1, out=out,
                          workspace=ws, split=split)
 
     ev = Events(lib, 3 * max(steps, warmup) + 3)
+    ramp = clock_ramp(step, ramp_ms)
     for i in range(warmup):
         ev.record(3 * i)
-        step(i)
+        step(i, 3 * i + 1)
         ev.record(3 * i + 2)
     gpu.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
         ev.record(3 * i)
-        step(i)
+        step(i, 3 * i + 1)
         ev.record(3 * i + 2)
     gpu.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
@@ -175,6 +205,7 @@ def bench_decode(cfg, steps, warmup, replicas=1, cpu=True, split=0):
         "unit": "GB/s",
         "ms_per_step": step_med,
         "wall_ms_per_step": wall_ms,
+        "clock_ramp": {"calls": ramp[0], "ms": round(ramp[1], 1)},
         "split": split,
         "roofline": {
             "bound": "hbm",
@@ -183,13 +214,13 @@ def bench_decode(cfg, steps, warmup, replicas=1, cpu=True, split=0):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": attn_bytes / (attn_med * 1e-3) / 1e9 / HBM_PEAK_GBS,
-            "traffic": profile_traffic("decode_split_kernel_llama3.2-3b-decode.md") if cfg.name == oi.CONFIGS["5b"].name else None,
+            "traffic": profile_traffic(f"decode_split_kernel_{cfg.name}.md"),
             "algorithmic_bytes": attn_bytes,
             "kernel_ms": attn_med,
         },
     }
     if cpu:
-        res["cpu_baseline"] = cpu_decode_baseline(cfg, data, oa, on)
+        res["cpu_baseline"] = cpu_decode_baseline(cfg, data, oa, on, budget_s=cpu_budget_s)
     return res
 
 
@@ -360,7 +391,7 @@ def cpu_decode_baseline(cfg, data, oa, on, budget_s=10.0):
 # prefill
 # ---------------------------------------------------------------------------
 
-def bench_prefill(cfg, steps, warmup, replicas=1, cpu=True):
+def bench_prefill(cfg, steps, warmup, replicas=1, cpu=True, cpu_budget_s=10.0, ramp_ms=0.0):
     from oracle import attention as oa
     from oracle import inputs as oi
     from oracle import numerics as on
@@ -393,6 +424,7 @@ def bench_prefill(cfg, steps, warmup, replicas=1, cpu=True):
         q, k, v, out = sets[i % replicas]
         flash_attention(q, k, v, causal=True, sm_scale=cfg.scale, out=out, workspace=ws)
 
+    ramp = clock_ramp(step, ramp_ms)
     for i in range(warmup):
         step(i)
     gpu.synchronize()
@@ -413,20 +445,22 @@ def bench_prefill(cfg, steps, warmup, replicas=1, cpu=True):
         "unit": "TFLOP/s",
         "ms_per_step": ms,
         "wall_ms_per_step": wall_ms,
+        "clock_ramp": {"calls": ramp[0], "ms": round(ramp[1], 1)},
         "roofline": {
             "bound": "mfma",
-            "kernel": "flash_fwd_16 + vt_pack_kernel (tl_attention_fwd)",
+            "kernel": ("flash_fwd_f32 (tl_attention_fwd)" if dt == "float32"
+                       else "flash_fwd_16 + vt_pack_kernel (tl_attention_fwd)"),
             "achieved": tf,
             "peak": peak,
             "unit": "TFLOP/s",
             "frac": tf / peak,
-            "traffic": profile_traffic("flash_fwd_16_llama3.2-3b-prefill.md") if cfg.name == oi.CONFIGS["5a"].name else None,
+            "traffic": profile_traffic(f"{'flash_fwd_f32' if dt == 'float32' else 'flash_fwd_16'}_{cfg.name}.md"),
             "algorithmic_flops": flops,
             "kernel_ms": ms,
         },
     }
     if cpu:
-        res["cpu_baseline"] = cpu_prefill_baseline(cfg, raw, oa, on, oi)
+        res["cpu_baseline"] = cpu_prefill_baseline(cfg, raw, oa, on, oi, budget_s=cpu_budget_s)
     return res
 
 
@@ -443,7 +477,7 @@ def cpu_prefill_baseline(cfg, raw, oa, on, oi, budget_s=10.0):
               for b in range(B) for h in range(Hkv)]
     flops = oi.prefill_flops(cfg)
     passes, t_total = [], 0.0
-    while t_total < budget_s or not passes:
+    while t_total < budget_s or len(passes) < 3:
         t0 = time.perf_counter()
         for q, k, v in groups:
             oa.attention_bhsd(q, k, v, causal=True, sm_scale=cfg.scale, block_q=512)
@@ -565,11 +599,16 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    # The GPU's clock ramps up over the first tens of milliseconds of sustained
-    # load; 100 untimed steps (~50 ms per workload) put the timed steps at the
-    # steady-state clock (3 warmup steps under-report prefill by ~10%).
-    ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--config", default="5")
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="all",
+                    help="all (default: every BASELINE config, headline 5b), 5 (5a + 5b), or one of "
+                         "1 2 3 4 5a 5b")
+    # The GPU's shader clock climbs over the first tens of milliseconds of
+    # sustained load: each config first runs its own step untimed for this long
+    # (measured: 5 warm-up steps alone left 5a ~10% slow).
+    ap.add_argument("--clock-ramp-ms", type=float, default=200.0)
+    ap.add_argument("--cpu-budget-s", type=float, default=4.0,
+                    help="CPU time per config for the NumPy baseline (at least 3 passes)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gemm", action="store_true",
                     help="time the model's projection GEMMs (tl_gemm) instead of attention")
@@ -613,17 +652,20 @@ def main():
     for name in sel:
         cfg = oi.CONFIGS[name]
         log(f"config {name}: {cfg.name}")
+        kw = dict(cpu=cpu, cpu_budget_s=args.cpu_budget_s, ramp_ms=args.clock_ramp_ms)
         if cfg.kind == "decode":
             cache_mb = 2 * cfg.batch * cfg.n_kv_head * cfg.max_ctx * cfg.d_k * (4 if cfg.dtype == "float32" else 2) / 1e6
             replicas = max(1, int(np.ceil(1024 / cache_mb))) if cache_mb < 1024 else 1
-            results[name] = bench_decode(cfg, args.steps, args.warmup, replicas=replicas, cpu=cpu,
-                                         split=args.decode_split)
+            results[name] = bench_decode(cfg, args.steps, args.warmup, replicas=replicas,
+                                         split=args.decode_split, **kw)
         else:
             # Q, K, V and O of one step; replicas so that >= 1 GB of other
             # inputs passes between two uses of one set (MALL is 256 MB).
             set_mb = (2 * cfg.n_head + 2 * cfg.n_kv_head) * cfg.batch * cfg.seq * cfg.d_k * (4 if cfg.dtype == "float32" else 2) / 1e6
             replicas = max(1, int(np.ceil(1024 / set_mb))) if set_mb < 1024 else 1
-            results[name] = bench_prefill(cfg, args.steps, args.warmup, replicas=replicas, cpu=cpu)
+            results[name] = bench_prefill(cfg, args.steps, args.warmup, replicas=replicas, **kw)
+        results[name]["workload"] = cfg.name
+        gpu.empty_cache()
         log(f"config {name}: {results[name]['value']:.1f} {results[name]['unit']} "
             f"({results[name]['roofline']['frac'] * 100:.1f}% of roofline)")
 
@@ -642,7 +684,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": DT_SHORT[cfg.dtype],
-        "data": "synthetic (seeded N(0,1) q/k/v, decode lengths drawn U[4096, 16383])",
+        "data": "synthetic (seeded N(0,1) q/k/v per BASELINE config; decode lengths drawn U[lo, hi])",
         "config": {
             "workload": f"{cfg.name} (config {head})" + (" + llama3.2-3b-prefill-bf16 (config 5a)" if "5a" in results and head == "5b" else ""),
             "batch": cfg.batch, "n_head": cfg.n_head, "n_kv_head": cfg.n_kv_head, "d_k": cfg.d_k,
@@ -652,10 +694,12 @@ def main():
     }
     if "cpu_baseline" in r:
         line["cpu_baseline"] = r["cpu_baseline"]
+    line["clock_ramp"] = {"ms": args.clock_ramp_ms,
+                          "note": "untimed steps of the same workload before the warm-up steps"}
     if "5a" in results and head != "5a":
         line["prefill"] = results["5a"]
-    if len(results) > 2 or (len(results) == 2 and "5a" not in results):
-        line["configs"] = results
+    if len(results) > 1:
+        line["configs"] = {k: v for k, v in results.items()}
     print(json.dumps(line))
 
 
