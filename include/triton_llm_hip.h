@@ -137,6 +137,24 @@ int tl_attention_decode(const void* q, const void* k_cache, const void* v_cache,
                         float sm_scale, int split_size, int dtype,
                         void* stream);
 
+/* The same decode with no workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * split partials live in a static device array of
+ * TL_DECODE_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends;
+ * problems whose tl_attention_decode_workspace_bytes exceeds it return
+ * TL_ERR_INVALID before any device work.  No hipMalloc / hipFree or other
+ * allocating call is made.  Calls that overlap in time on one GPU share that
+ * array and race: issue them on one stream.  Results are identical to
+ * tl_attention_decode's for the same arguments. */
+#define TL_DECODE_NOALLOC_SCRATCH_BYTES (32u << 20)
+int tl_attention_decode_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                const int32_t* cache_lens, int len_add, void* o, int batch,
+                                int n_head, int n_kv_head, int max_ctx, int d_k,
+                                const int64_t* q_strides, const int64_t* k_strides,
+                                const int64_t* v_strides, const int64_t* o_strides,
+                                float sm_scale, int split_size, int dtype, void* stream);
+
 /* ---------------------------------------------------------------------------
  * RoPE + KV-cache append, fused into the Q/K write.  Replaces the model's
  * host-side sequence  apply_rope(q) ; apply_rope(k) ; k/v -> host ;

@@ -46,6 +46,8 @@
 
 #include <math.h>
 
+#include <mutex>
+
 #include <type_traits>
 
 namespace {
@@ -618,6 +620,52 @@ int launch_decode_t(DecodeParams& p, int d_k, hipStream_t st) {
 
 size_t round256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+int decode_entry(const void* q, const void* k_cache, const void* v_cache,
+                 const int32_t* cache_lens, int len_add, void* o, void* workspace,
+                 size_t workspace_bytes, int batch, int n_head, int n_kv_head, int max_ctx,
+                 int d_k, const int64_t* q_strides, const int64_t* k_strides,
+                 const int64_t* v_strides, const int64_t* o_strides, float sm_scale,
+                 int split_size, int dtype, void* stream);
+
+}  // namespace
+
+// ---- Scratch of the entry point that allocates nothing --------------------
+// tl_attention_decode_noalloc keeps the split partials in this file-scope
+// device array instead of a caller's workspace.  Every GPU the library runs
+// on holds its own copy, at its own address, until the process ends.  In
+// host code the name `scratch` is only a stand-in for the symbol, never a
+// device address: the per-device address comes from hipGetSymbolAddress
+// (noalloc_scratch below) and only that pointer reaches kernels.  The
+// partials need no initial contents (each call's combine reads only the
+// slots its own split pass wrote), so nothing is cleared; calls that
+// overlap in time on one GPU share the array and race.
+static __device__ __align__(256) unsigned char scratch[TL_DECODE_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up once per device with
+// that device current.
+int noalloc_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return TL_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!p) return TL_ERR_UNSUPPORTED;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -653,6 +701,45 @@ int tl_attention_decode(const void* q, const void* k_cache, const void* v_cache,
                         const int64_t* v_strides, const int64_t* o_strides,
                         float sm_scale, int split_size, int dtype,
                         void* stream) {
+  return decode_entry(q, k_cache, v_cache, cache_lens, len_add, o, workspace, workspace_bytes,
+                      batch, n_head, n_kv_head, max_ctx, d_k, q_strides, k_strides, v_strides,
+                      o_strides, sm_scale, split_size, dtype, stream);
+}
+
+int tl_attention_decode_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                const int32_t* cache_lens, int len_add, void* o, int batch,
+                                int n_head, int n_kv_head, int max_ctx, int d_k,
+                                const int64_t* q_strides, const int64_t* k_strides,
+                                const int64_t* v_strides, const int64_t* o_strides,
+                                float sm_scale, int split_size, int dtype, void* stream) {
+  if (batch == 0 || n_head == 0) return 0;
+  if (batch < 0 || n_head < 0 || n_kv_head < 1 || max_ctx < 1) return TL_ERR_INVALID;
+  if (split_size == 0) split_size = tl_decode_split_size(batch, n_kv_head, max_ctx);
+  if (split_size < 16 || split_size % 16 != 0) return TL_ERR_INVALID;
+  // Larger problems than the static scratch holds are refused before any
+  // device work (the caller should use tl_attention_decode with a workspace).
+  if (tl_attention_decode_workspace_bytes(batch, n_head, max_ctx, d_k, split_size) >
+      (size_t)TL_DECODE_NOALLOC_SCRATCH_BYTES)
+    return TL_ERR_INVALID;
+  void* ws = nullptr;
+  const int st = noalloc_scratch(&ws);
+  if (st != 0) return st;
+  return decode_entry(q, k_cache, v_cache, cache_lens, len_add, o, ws,
+                      (size_t)TL_DECODE_NOALLOC_SCRATCH_BYTES, batch, n_head, n_kv_head, max_ctx,
+                      d_k, q_strides, k_strides, v_strides, o_strides, sm_scale, split_size, dtype,
+                      stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+int decode_entry(const void* q, const void* k_cache, const void* v_cache,
+                 const int32_t* cache_lens, int len_add, void* o, void* workspace,
+                 size_t workspace_bytes, int batch, int n_head, int n_kv_head, int max_ctx,
+                 int d_k, const int64_t* q_strides, const int64_t* k_strides,
+                 const int64_t* v_strides, const int64_t* o_strides, float sm_scale,
+                 int split_size, int dtype, void* stream) {
   if (batch == 0 || n_head == 0) return 0;
   if (!q || !k_cache || !v_cache || !o || !workspace || batch < 0 ||
       n_head < 0 || n_kv_head < 1 || n_head % n_kv_head != 0 || max_ctx < 1 ||
@@ -721,4 +808,4 @@ int tl_attention_decode(const void* q, const void* k_cache, const void* v_cache,
   }
 }
 
-}  // extern "C"
+}  // namespace
