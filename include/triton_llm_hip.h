@@ -69,6 +69,21 @@ int tl_event_record(void* event, void* stream);
 int tl_event_synchronize(void* event);
 int tl_event_elapsed_ms(float* ms, void* start, void* stop);
 
+/* HIP graphs of a sequence of calls (no counterpart in the reference, whose
+ * every call goes through the Python launcher).  tl_graph_capture_begin
+ * starts recording `stream` (NULL: the library stream); every tl_* launch
+ * and device-to-device copy issued to it until tl_graph_capture_end is
+ * recorded, not run.  Calls that synchronise (tl_memcpy_htod / _dtoh,
+ * tl_synchronize) and tl_memset must not be issued while recording.
+ * tl_graph_capture_end returns an executable graph; tl_graph_launch replays
+ * it on a stream with the pointers and sizes it was recorded with.  A
+ * decode step of a serving loop is a few small kernels whose host launch
+ * cost exceeds their run time: replaying it as one graph keeps the GPU busy. */
+int tl_graph_capture_begin(void* stream);
+int tl_graph_capture_end(void* stream, void** exec);
+int tl_graph_launch(void* exec, void* stream);
+int tl_graph_destroy(void* exec);
+
 /* ---------------------------------------------------------------------------
  * RoPE, in place.  Replaces apply_rope (triton_llm/kernels/rope.py:153-222)
  * and its _rope_kernel (rope.py:25-70): half-split pairing (i, i + d_k/2),

@@ -1,0 +1,74 @@
+"""HIP graph capture and replay (tl_graph_*, gpu.capture): a recorded decode
+step and a recorded prefill call, replayed several times with eager work
+and synchronisation between the replays, give exactly the eager result every
+time (the kernels are deterministic, so bit-equal)."""
+
+import numpy as np
+import pytest
+
+from oracle import inputs as oi
+from tests import _helpers as H
+from triton_llm import gpu
+from triton_llm.kernels import attention_decode, flash_attention, rope_kv_append
+from triton_llm.kernels.decode import decode_workspace
+
+pytestmark = pytest.mark.gpu
+
+
+def _eager_noise():
+    # unrelated eager work on the same stream between replays
+    a = gpu.to_device(np.arange(4096, dtype=np.float32))
+    b = gpu.allocate((4096,), np.float32)
+    gpu.copy_(b, a)
+    gpu.synchronize()
+
+
+def test_graph_replays_decode_step():
+    cfg = oi.scaled(oi.CONFIGS["4"], batch=6, max_ctx=640, lo=1, hi=600, seed=41)
+    dt = cfg.dtype
+    B, Hq, Hkv, D = cfg.batch, cfg.n_head, cfg.n_kv_head, cfg.d_k
+    print(f"[case] graph decode B={B} Hq={Hq} Hkv={Hkv} D={D} {dt}", flush=True)
+    d = oi.make_decode(cfg, fill="zero")
+    cos, sin = oi.rope_tables(cfg)
+    q0 = H.upload(d["q"], dt)
+    q = H.upload(d["q"], dt)
+    kn, vn = H.upload(d["k_new"], dt), H.upload(d["v_new"], dt)
+    kc, vc = H.upload(d["k_cache"], dt), H.upload(d["v_cache"], dt)
+    lens = gpu.to_device(d["lens"])
+    cos_d, sin_d = gpu.to_device(cos), gpu.to_device(sin)
+    out = gpu.allocate((B, Hq, D), q.dtype)
+    ws = decode_workspace(B, Hq, Hkv, cfg.max_ctx, D)
+
+    def step():
+        gpu.copy_(q, q0)  # RoPE rotates q in place: start every step from the same q
+        rope_kv_append(q, kn, vn, kc, vc, lens, cos_d, sin_d)
+        attention_decode(q, kc, vc, lens, Hq, Hkv, sm_scale=cfg.scale, len_add=1, out=out, workspace=ws)
+
+    step()
+    want = H.download(out).copy()
+    with gpu.capture() as g:
+        step()
+    for rep in range(4):
+        gpu.copy_(out, gpu.zeros(out.shape, out.dtype))
+        g.replay()
+        got = H.download(out)
+        np.testing.assert_array_equal(got, want, err_msg=f"replay {rep}")
+        _eager_noise()
+
+
+def test_graph_replays_prefill():
+    dt = "bfloat16"
+    cfg = oi.Config("graph-prefill", "prefill", dt, 1, 6, 2, 128, 43, 0.088, seq=700)
+    raw = oi.make_prefill_raw(cfg)
+    print(f"[case] graph prefill S={cfg.seq} {dt}", flush=True)
+    q, k, v = H.upload(raw["q"], dt), H.upload(raw["k"], dt), H.upload(raw["v"], dt)
+    out = gpu.allocate(q.shape, q.dtype)
+    flash_attention(q, k, v, causal=True, sm_scale=cfg.scale, out=out)
+    want = H.download(out).copy()
+    with gpu.capture() as g:
+        flash_attention(q, k, v, causal=True, sm_scale=cfg.scale, out=out)
+    for rep in range(4):
+        gpu.copy_(out, gpu.zeros(out.shape, out.dtype))
+        g.replay()
+        np.testing.assert_array_equal(H.download(out), want, err_msg=f"replay {rep}")
+        _eager_noise()

@@ -109,6 +109,36 @@ int tl_synchronize(void) {
   return (int)hipDeviceSynchronize();
 }
 
+int tl_graph_capture_begin(void* stream) {
+  // Relaxed mode: calls on other threads (and cached-block allocations on
+  // this one) stay legal while the stream records.
+  return (int)hipStreamBeginCapture(tl_resolve_stream(stream), hipStreamCaptureModeRelaxed);
+}
+
+int tl_graph_capture_end(void* stream, void** exec) {
+  if (!exec) return TL_ERR_INVALID;
+  *exec = nullptr;
+  hipGraph_t graph = nullptr;
+  hipError_t e = hipStreamEndCapture(tl_resolve_stream(stream), &graph);
+  if (e != hipSuccess) return (int)e;
+  hipGraphExec_t ge = nullptr;
+  e = hipGraphInstantiate(&ge, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  if (e != hipSuccess) return (int)e;
+  *exec = (void*)ge;
+  return 0;
+}
+
+int tl_graph_launch(void* exec, void* stream) {
+  if (!exec) return TL_ERR_INVALID;
+  return (int)hipGraphLaunch((hipGraphExec_t)exec, tl_resolve_stream(stream));
+}
+
+int tl_graph_destroy(void* exec) {
+  if (!exec) return 0;
+  return (int)hipGraphExecDestroy((hipGraphExec_t)exec);
+}
+
 const char* tl_error_string(int status) {
   if (status == 0) return "success";
   return hipGetErrorString((hipError_t)status);

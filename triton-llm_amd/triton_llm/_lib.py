@@ -43,6 +43,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tl_event_record": (_c_int, [_vp, _vp]),
     "tl_event_synchronize": (_c_int, [_vp]),
     "tl_event_elapsed_ms": (_c_int, [ctypes.POINTER(_c_float), _vp, _vp]),
+    "tl_graph_capture_begin": (_c_int, [_vp]),
+    "tl_graph_capture_end": (_c_int, [_vp, ctypes.POINTER(_vp)]),
+    "tl_graph_launch": (_c_int, [_vp, _vp]),
+    "tl_graph_destroy": (_c_int, [_vp]),
     "tl_rope_inplace": (
         _c_int,
         [_vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _vp],

@@ -284,6 +284,49 @@ def view(tensor: DeviceTensor, new_shape: tuple) -> DeviceTensor:
     return DeviceTensor(tensor.ptr, new_shape, tensor.dtype, tensor.nbytes, defer_free=False)
 
 
+class Graph:
+    """An executable HIP graph recorded by :func:`capture`; ``replay()``
+    runs the recorded launches again on the library stream (same pointers,
+    same sizes).  No sync."""
+
+    def __init__(self):
+        self.exec = ctypes.c_void_p()
+
+    def replay(self):
+        _initialize()
+        if not self.exec.value:
+            raise RuntimeError("graph was not captured")
+        check_error(_rt.tl_graph_launch(self.exec, None))
+
+    def __del__(self):
+        try:
+            if self.exec.value and _rt is not None:
+                _rt.tl_graph_destroy(self.exec)
+        except Exception:
+            pass
+
+
+class capture:
+    """``with gpu.capture() as g: <launches>`` records the launches on the
+    library stream into ``g`` instead of running them; ``g.replay()`` runs
+    them.  Inside, only stream-ordered launches and device copies are
+    legal: no host copies, no synchronize, no memset.  Allocations are
+    legal but are not recorded, so make them (or warm the block cache)
+    before capturing."""
+
+    def __enter__(self) -> Graph:
+        _initialize()
+        self.graph = Graph()
+        check_error(_rt.tl_graph_capture_begin(None))
+        return self.graph
+
+    def __exit__(self, exc_type, exc, tb):
+        err = _rt.tl_graph_capture_end(None, ctypes.byref(self.graph.exec))
+        if exc_type is None:
+            check_error(err)
+        return False
+
+
 def copy_(dst: DeviceTensor, src: DeviceTensor):
     """Device-to-device copy of ``src`` into ``dst`` (same byte size), stream ordered."""
     _initialize()

@@ -28,6 +28,49 @@ def check_status(status: int, what: str) -> None:
         raise RuntimeError(f"GPU runtime error (hip): {status} ({_lib.error_string(status)}) in {what}")
 
 
+# ---- launchers: a wrapper call's C-ABI launches, replayable without Python
+# validation (serving loops, benchmarks) ---------------------------------------
+_recording: list | None = None
+
+
+def launch(fn, *args, what: str) -> None:
+    """Issue one C-ABI launch, or record it while :func:`record` runs."""
+    if _recording is not None:
+        _recording.append((fn, args, what))
+        return
+    check_status(fn(*args), what)
+
+
+class Launcher:
+    """The C-ABI launches one wrapper call made, replayed with the same
+    arguments: no Python validation, no shape logic, one ctypes call per
+    kernel launch.  Valid while every buffer the call used is alive and
+    unmoved (pass explicit workspaces and outputs to the recorded call)."""
+
+    def __init__(self, calls, keep):
+        self.calls = calls
+        self._keep = keep  # the recorded call's result (e.g. an output it allocated)
+
+    def __call__(self) -> None:
+        for fn, args, what in self.calls:
+            st = fn(*args)
+            if st:
+                check_status(st, what)
+
+
+def record(thunk) -> Launcher:
+    """Run ``thunk`` (wrapper calls) recording instead of issuing their
+    launches; returns a :class:`Launcher` that issues them."""
+    global _recording
+    prev, _recording = _recording, []
+    try:
+        keep = thunk()
+        calls = _recording
+    finally:
+        _recording = prev
+    return Launcher(calls, keep)
+
+
 def same_dtype(*tensors) -> int:
     """Dtype code shared by all tensors; ValueError if they differ."""
     names = {gpu.dtype_name(t.dtype) for t in tensors}

@@ -23,7 +23,7 @@ from __future__ import annotations
 import numpy as np
 
 from triton_llm import gpu
-from ._common import check_status, default_scale, same_dtype, shared_workspace, vp
+from ._common import launch, check_status, default_scale, same_dtype, shared_workspace, vp
 from triton_llm import _lib
 
 DECODE_D = (64, 128)
@@ -101,13 +101,11 @@ def attention_gqa(
         lib = gpu.runtime()
         ws_bytes = lib.tl_attention_fwd_workspace_bytes(1, n_kv_head, seq_k, d_k, code)
         ws = shared_workspace("attention_gqa.prefill", ws_bytes)
-        status = lib.tl_attention_fwd(
-            vp(q_dev), vp(k_dev), vp(v_dev), vp(o_dev), vp(ws), ws_bytes,
+        launch(lib.tl_attention_fwd, vp(q_dev), vp(k_dev), vp(v_dev), vp(o_dev), vp(ws), ws_bytes,
             1, n_head, n_kv_head, seq_q, seq_k, d_k,
             q_str, kv_str, kv_str, q_str,
             float(sm_scale), 1 if causal else 0, code, None,
-        )
-        check_status(status, "attention_gqa")
+            what="attention_gqa")
     return o_dev
 
 
@@ -124,9 +122,7 @@ def _decode_one(q_dev, k_dev, v_dev, o_dev, n_head, n_kv_head, seq_k, d_k, sm_sc
     ws = shared_workspace("attention_gqa.decode", ws_bytes)
     qo = _lib.strides(n_head * d_k, d_k)
     kv = _lib.strides(n_kv_head * seq_k * d_k, seq_k * d_k, d_k)
-    status = lib.tl_attention_decode(
-        vp(q_dev), vp(k_dev), vp(v_dev), None, seq_k, vp(o_dev), vp(ws), ws.nbytes,
+    launch(lib.tl_attention_decode, vp(q_dev), vp(k_dev), vp(v_dev), None, seq_k, vp(o_dev), vp(ws), ws.nbytes,
         1, n_head, n_kv_head, seq_k, d_k, qo, kv, kv, qo,
         float(sm_scale), split, code, None,
-    )
-    check_status(status, "attention_gqa(decode)")
+        what="attention_gqa(decode)")

@@ -28,7 +28,7 @@ import numpy as np
 
 from triton_llm import gpu
 from triton_llm import _lib
-from ._common import check_status, default_scale, same_dtype, scratch, vp
+from ._common import launch, check_status, default_scale, same_dtype, scratch, vp
 
 
 def allocate_kv_cache(batch: int, n_kv_head: int, max_ctx: int, d_k: int, dtype=np.float32,
@@ -102,12 +102,10 @@ def rope_kv_append(q_dev, k_new, v_new, k_cache, v_cache, cache_lens,
     kv_str = _lib.strides(n_new * n_kv * d_k, n_kv * d_k, d_k)
     q_str = _lib.strides(n_new * n_head * d_k, n_head * d_k, d_k)
     c_str = _lib.strides(n_kv * max_ctx * d_k, max_ctx * d_k, d_k)
-    status = gpu.runtime().tl_rope_kv_append(
-        vp(q_dev), vp(k_new), vp(v_new), vp(k_cache), vp(v_cache), vp(cache_lens),
+    launch(gpu.runtime().tl_rope_kv_append, vp(q_dev), vp(k_new), vp(v_new), vp(k_cache), vp(v_cache), vp(cache_lens),
         vp(cos_dev), vp(sin_dev), rope_rows, batch, n_new, n_head, n_kv, max_ctx, d_k,
         q_str, kv_str, kv_str, c_str, c_str, code, None,
-    )
-    check_status(status, "rope_kv_append")
+        what="rope_kv_append")
     return q_dev
 
 
@@ -157,13 +155,11 @@ def attention_decode(q_dev, k_cache, v_cache, cache_lens, n_head: int, n_kv_head
     ws = scratch(ws_bytes, workspace, key="decode")
     qo = _lib.strides(n_head * d_k, d_k)
     c_str = _lib.strides(n_kv * max_ctx * d_k, max_ctx * d_k, d_k)
-    status = gpu.runtime().tl_attention_decode(
-        vp(q_dev), vp(k_cache), vp(v_cache), vp(cache_lens), int(len_add), vp(out), vp(ws),
+    launch(gpu.runtime().tl_attention_decode, vp(q_dev), vp(k_cache), vp(v_cache), vp(cache_lens), int(len_add), vp(out), vp(ws),
         ws.nbytes if ws is not None else 0,
         batch, n_head, n_kv_head, max_ctx, d_k, qo, c_str, c_str, qo,
         float(sm_scale), split, code, None,
-    )
-    check_status(status, "attention_decode")
+        what="attention_decode")
     return out
 
 

@@ -20,7 +20,7 @@ import numpy as np
 
 from triton_llm import gpu
 from triton_llm import _lib
-from ._common import check_status, contiguous_strides, default_scale, same_dtype, scratch, vp
+from ._common import launch, check_status, contiguous_strides, default_scale, same_dtype, scratch, vp
 
 
 def flash_workspace_bytes(batch: int, n_kv_head: int, seq_k: int, d_k: int, dtype) -> int:
@@ -46,13 +46,11 @@ def flash_attention_strided(q, k, v, out, *, batch, n_head, n_kv_head, seq_q, se
     lib = gpu.runtime()
     ws_bytes = lib.tl_attention_fwd_workspace_bytes(batch, n_kv_head, seq_k, d_k, code)
     ws = scratch(ws_bytes, workspace, key="flash")
-    status = lib.tl_attention_fwd(
-        vp(q), vp(k), vp(v), vp(out), vp(ws), ws.nbytes if ws is not None else 0,
+    launch(lib.tl_attention_fwd, vp(q), vp(k), vp(v), vp(out), vp(ws), ws.nbytes if ws is not None else 0,
         batch, n_head, n_kv_head, seq_q, seq_k, d_k,
         _lib.strides(*q_strides), _lib.strides(*k_strides), _lib.strides(*v_strides),
         _lib.strides(*o_strides), float(sm_scale), 1 if causal else 0, code, None,
-    )
-    check_status(status, "flash_attention")
+        what="flash_attention")
     return out
 
 

@@ -15,7 +15,7 @@ from __future__ import annotations
 import numpy as np
 
 from triton_llm import gpu
-from ._common import check_status, same_dtype, vp
+from ._common import launch, check_status, same_dtype, vp
 
 # Workspace of the few-row path, kept across calls and grown on demand: every
 # call runs on the library stream, so consecutive calls are ordered and may
@@ -52,7 +52,6 @@ def gemm(h_dev: "gpu.DeviceTensor", w_dev: "gpu.DeviceTensor",
     if workspace is not None and need and workspace.nbytes < need:
         raise ValueError(f"workspace holds {workspace.nbytes} bytes, {need} required")
     ws = workspace if workspace is not None else _workspace(need)
-    status = lib.tl_gemm(vp(h_dev), vp(w_dev), vp(out_dev), M, N, K, K, N, N, vp(ws),
-                         ws.nbytes if ws is not None else 0, code, None)
-    check_status(status, "gemm")
+    launch(lib.tl_gemm, vp(h_dev), vp(w_dev), vp(out_dev), M, N, K, K, N, N, vp(ws),
+           ws.nbytes if ws is not None else 0, code, None, what="gemm")
     return out_dev

@@ -19,7 +19,7 @@ import numpy as np
 
 from triton_llm import gpu
 from triton_llm import _lib
-from ._common import check_status, vp
+from ._common import launch, check_status, vp
 
 
 def precompute_cos_sin(
@@ -103,9 +103,7 @@ def apply_rope(
     code = gpu.dtype_code(x_dev.dtype)
 
     lib = gpu.runtime()
-    status = lib.tl_rope_inplace(
-        vp(x_dev), vp(cos_dev), vp(sin_dev),
+    launch(lib.tl_rope_inplace, vp(x_dev), vp(cos_dev), vp(sin_dev),
         n_rows, d_k, d_k, seq_len, position_offset, code, None,
-    )
-    check_status(status, "apply_rope")
+        what="apply_rope")
     return x_dev
