@@ -326,7 +326,7 @@ def bench_gemm(steps, warmup, cpu=True, models=("llama3.2-3b", "smollm2-360m"), 
                     "gbs": tot_bytes / (tot_ms * 1e-3) / 1e9, "frac_hbm": tot_bytes / (tot_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
                 })
                 log(f"gemm {model} {dt} M={M}: {tot_ms*1e3:.1f} us/layer, {rows[-1]['tflops']:.1f} TFLOP/s, {rows[-1]['gbs']:.0f} GB/s")
-    res = {"metric": "projection GEMMs per layer (tl_gemm, rocBLAS)", "rows": rows}
+    res = {"metric": "projection GEMMs per layer (tl_gemm)", "rows": rows}
     res["layers"] = bench_layers(steps, warmup)
     res["sample"] = bench_sample(steps, warmup, cpu=cpu)
     if cpu:

@@ -201,8 +201,9 @@ int tl_rope_kv_append(void* q, const void* k_new, const void* v_new,
  * :360-363, :375).  k = 0 writes zeros; m = 0 or n = 0 does nothing.
  * m <= 8 (a decoded token) runs a hand-written HBM-streaming kernel whose
  * K-slice partial sums need tl_gemm_workspace_bytes(m, n, k, dtype) bytes of
- * workspace (0 otherwise); larger m goes to rocBLAS (one handle per device,
- * created on first use, which holds rocBLAS's own workspace).
+ * workspace (0 otherwise); larger m runs a hand-written MFMA kernel
+ * (128 x 128 tiles of C; rows of A and B must be 16-byte aligned, otherwise a
+ * simple FMA kernel takes the product) and needs no workspace.
  * ------------------------------------------------------------------------- */
 size_t tl_gemm_workspace_bytes(int m, int n, int k, int dtype);
 int tl_gemm(const void* a, const void* b, void* c, int m, int n, int k, int64_t lda,

@@ -2,8 +2,9 @@
 reference's own cases (tests/test_gemm.py of the reference: seeded shapes,
 non-block-aligned shapes, empty dimensions, mismatched K) and on the
 projection shapes of SmolLM2-360M and Llama-3.2-3B for one decoded token,
-a few tokens (the hand-written streaming kernel, up to 8 rows) and a short
-prompt (rocBLAS).  Tolerances: fp32 2e-3 max-abs (the reference's own
+a few tokens (the hand-written streaming kernel, up to 8 rows) and prompts
+(the hand-written MFMA kernel; the simple FMA kernel for rows that are not
+16-byte aligned).  Tolerances: fp32 2e-3 max-abs (the reference's own
 bar is allclose(rtol 1e-2, atol 5e-2)); 16-bit outputs within their
 rounding, rtol 8e-3 + atol 1e-2.
 """
@@ -88,7 +89,7 @@ def test_gemm_lm_head_shapes(dtype, M, K, N):
 def test_gemm_few_rows_odd_shapes(M, K, N):
     """Few-row products on shapes the streaming kernel handles partly (a
     ragged last K-slice or column tile) or not at all (N not a multiple of
-    the 16-byte chunk: rocBLAS), against the oracle."""
+    the 16-byte chunk: the simple FMA kernel), against the oracle."""
     rng = np.random.default_rng(M * 1000 + K + N)
     a = rng.standard_normal((M, K), dtype=np.float32)
     b = rng.standard_normal((K, N), dtype=np.float32)
@@ -126,3 +127,56 @@ def test_gemm_reference_performance_bound():
     for _ in range(10):
         gemm_cpu(a, b)
     assert (time.perf_counter() - t0) / 10 * 1e3 < 50
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
+@pytest.mark.parametrize("M,K,N", [(128, 3072, 1024), (300, 960, 2560), (517, 2560, 960), (2048, 3072, 3072),
+                                   (64, 8192, 3072), (9, 136, 200)])
+def test_gemm_prompt_shapes_mfma(dtype, M, K, N):
+    """Prompt-sized products on the matrix-core kernel: the models' projection
+    shapes, ragged tiles in M and N, K not a multiple of the LDS stage."""
+    print(f"[case] gemm mfma {dtype} {M}x{K}@{K}x{N}", flush=True)
+    rng = np.random.default_rng(M + 3 * K + 7 * N)
+    a = on.to_storage(rng.standard_normal((M, K), dtype=np.float32), dtype)
+    b = on.to_storage(rng.standard_normal((K, N), dtype=np.float32) / np.sqrt(K), dtype)
+    got = on.from_storage(gemm_cpu(a, b, dtype), dtype)
+    exp = gemm_ref(on.from_storage(a, dtype), on.from_storage(b, dtype))
+    if dtype == "float32":
+        err = H.max_abs(got, exp)
+        H.report(f"mfma {dtype} {M}x{K}@{K}x{N}", err, 2e-3)
+        assert err <= 2e-3
+    else:
+        np.testing.assert_allclose(got, exp, rtol=8e-3, atol=1e-2)
+
+
+@pytest.mark.parametrize("dtype,K", [("bfloat16", 136), ("float16", 72), ("float32", 132), ("float32", 20)])
+def test_gemm_strided_operands_keep_padding_out(dtype, K):
+    """Row strides past the logical sizes, with NaN in every padding element:
+    lda = K + 8 (the last LDS stage reads past K into the padding, which must
+    not reach C), ldb = N + 8, ldc = N + 4 (padding of C left untouched)."""
+    M, N = 150, 200
+    print(f"[case] gemm strided {dtype} K={K}", flush=True)
+    rng = np.random.default_rng(K)
+    a = rng.standard_normal((M, K), dtype=np.float32)
+    b = rng.standard_normal((K, N), dtype=np.float32) / np.sqrt(K)
+    a_pad = np.full((M, K + 8), np.nan, np.float32)
+    a_pad[:, :K] = a
+    b_pad = np.full((K, N + 8), np.nan, np.float32)
+    b_pad[:, :N] = b
+    a_s, b_s = on.to_storage(a_pad, dtype), on.to_storage(b_pad, dtype)
+    ldc = N + 4
+    c_dev = H.upload(on.to_storage(np.full((M, ldc), 3.0, np.float32), dtype), dtype)
+    lib = gpu.runtime()
+    code = gpu.dtype_code(H.GPU_DTYPES[dtype])
+    st = lib.tl_gemm(H.upload(a_s, dtype).ptr, H.upload(b_s, dtype).ptr, c_dev.ptr, M, N, K, K + 8, N + 8, ldc,
+                     None, 0, code, None)
+    assert st == 0
+    c = on.from_storage(H.download(c_dev), dtype)
+    exp = gemm_ref(on.from_storage(a_s, dtype)[:, :K], on.from_storage(b_s, dtype)[:, :N])
+    if dtype == "float32":
+        err = H.max_abs(c[:, :N], exp)
+        H.report(f"strided {dtype} K={K}", err, 2e-3)
+        assert err <= 2e-3
+    else:  # output rounding of 16-bit C; NaN anywhere fails
+        np.testing.assert_allclose(c[:, :N], exp, rtol=8e-3, atol=1e-2)
+    assert (c[:, N:] == 3.0).all()

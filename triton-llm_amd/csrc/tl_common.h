@@ -132,3 +132,67 @@ hipStream_t tl_resolve_stream(void* stream);
 // environment variable TRITON_LLM_HIP_MAX_CUS when set (tests use it to force
 // multi-round schedules on small problems).
 int tl_device_cus();
+
+// ---- matrix-core and LDS helpers shared by the MFMA kernels -------------
+
+// 32x32x16 MFMA (fp32 accumulation) for the 16-bit storage types.
+template <typename T>
+struct Mfma;
+
+template <>
+struct Mfma<BF16> {
+  typedef bf16x8 frag;
+  static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ frag pack(const float* x) {
+    frag r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = (__bf16)x[i];
+    return r;
+  }
+};
+
+template <>
+struct Mfma<F16> {
+  typedef f16x8 frag;
+  static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ frag pack(const float* x) {
+    frag r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = (_Float16)x[i];
+    return r;
+  }
+};
+
+// Two fp32 values -> one 32-bit word of two 16-bit values (low half first),
+// rounded to nearest even.
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(const float (&x)[2]);
+template <>
+__device__ __forceinline__ uint32_t pack2<BF16>(const float (&x)[2]) {
+  const bf16x2 v = {(__bf16)x[0], (__bf16)x[1]};
+  return __builtin_bit_cast(uint32_t, v);
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<F16>(const float (&x)[2]) {
+  const f16x2 v = {(_Float16)x[0], (_Float16)x[1]};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// s_waitcnt vmcnt(N) (gfx9 encoding; expcnt and lgkmcnt left unconstrained).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier that orders LDS only (global prefetches stay in flight).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+

@@ -5,11 +5,10 @@
 // projection of the model (q/k/v/o, gate/up/down, lm_head).
 //
 // Two regimes:
-//   * a prompt (m > kSkinnyMaxM rows) is a plain compute-bound GEMM: it goes
-//     to rocBLAS (Tensile's gfx950 MFMA kernels), fp32 accumulation.
-//     Row-major operands map onto column-major rocBLAS as C^T = B^T . A^T
-//     with no copies.  rocBLAS keeps one handle per device (created on first
-//     use), which owns rocBLAS's own small device workspace.
+//   * a prompt (m > kSkinnyMaxM rows) is a compute-bound GEMM on the matrix
+//     cores: gemm_mfma_kernel (128 x 128 tiles, LDS-DMA staging, fp32
+//     accumulation); shapes whose rows are not 16-byte aligned take the
+//     simple fp32-FMA gemm_simple_kernel;
 //   * a decoded token (m <= kSkinnyMaxM rows) reads every weight once for a
 //     handful of multiply-adds per element: an HBM-bound skinny product,
 //     where rocBLAS measured 0.4-0.7 TB/s.  skinny_partial_kernel cuts B
@@ -18,10 +17,6 @@
 //     partial sums go to the workspace and skinny_reduce_kernel adds the
 //     K-slices and rounds to the output type.
 #include "tl_common.h"
-
-#include <rocblas/rocblas.h>
-
-#include <mutex>
 
 namespace {
 
@@ -32,18 +27,6 @@ constexpr int kSkMaxTk = 1024;     // rows per K-slice at most (A's slice is sta
 constexpr int kSkRowsPerStep = 16; // rows one workgroup load instruction round covers
 constexpr int kSkTargetTiles = 1024;
 constexpr int kAuxNt = 2;          // buffer-load cache policy: nontemporal (weights are read once)
-
-constexpr int kMaxDevices = 64;
-rocblas_handle g_handles[kMaxDevices] = {};
-std::mutex g_handle_mu;
-
-rocblas_handle device_handle() {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
-  std::lock_guard<std::mutex> lock(g_handle_mu);
-  if (!g_handles[dev] && rocblas_create_handle(&g_handles[dev]) != rocblas_status_success) g_handles[dev] = nullptr;
-  return g_handles[dev];
-}
 
 bool fits_int(int64_t x) { return x >= 0 && x <= INT32_MAX; }
 
@@ -234,6 +217,328 @@ int launch_skinny(const void* a, const void* b, void* c, int m, int n, int k, in
   return tl_launch_status();
 }
 
+// ---------------------------------------------------------------------------
+// Prompt-sized products on the matrix cores (m > kSkinnyMaxM).
+//
+// Workgroup tile 128 x 128 of C, 4 waves in 2 x 2, each wave 64 x 64 (2 x 2
+// blocks of 32 x 32).  K is walked in LDS stages (16-bit: 32 k, fp32: 16 k),
+// three stages in flight, every tile moved global -> LDS by LDS-DMA
+// (buffer_load ... lds: no register round trip), every wave loading a
+// quarter.  Each wave computes the transposed block C^T = B^T . A^T with
+// the MFMA, so a lane ends up owning one row of C and 4 consecutive columns
+// per accumulator group: stores are 8 (16-bit) or 16 (fp32) contiguous bytes.
+//
+// Operand layouts in LDS (rows unpadded, 16-byte chunks XOR-swizzled so that
+// every operand read is conflict-free):
+//   A stage: 128 rows (m) x 64 bytes (k), chunk c of row r at slot
+//            c ^ ((r >> 2) & 3).  A fragment: lane (l % 32, h = l / 32) reads
+//            one 16-byte chunk of row l % 32 of its block: 8 consecutive k
+//            (16-bit) or 4 (fp32).
+//   B stage, 16-bit: 32 rows (k) x 256 bytes (n), chunk c of row r at slot
+//            c ^ (4 (r % 4)).  The MFMA wants 8 consecutive k of one column
+//            per lane, i.e. B read down a column: two ds_read_b64_tr_b16.
+//            That instruction transposes within each 16-lane group: output
+//            lane j, element e is element j % 4 of what lane 4 e + j / 4 of
+//            the group read.  So lane 4 e + p of group g reads row
+//            8 (g / 2) + 4 t + e, columns n0 + 16 (g % 2) + 4 p .. + 3, and
+//            lane 16 g + j receives column n0 + 16 (g % 2) + j, rows
+//            8 (g / 2) + 4 t + 0..3 (t = 0, 1: the two reads).
+//   B stage, fp32: 16 rows (k) x 512 bytes (n), chunk c of row r at slot
+//            c ^ (8 ((r >> 2) & 1)); a lane reads one float of its column.
+// fp32 uses v_mfma_f32_32x32x2f32 with the k order permuted: in k-group q
+// (8 k), step s, lane half h uses k = 8 q + 4 h + s, so one 16-byte A read
+// feeds 4 steps.
+// ---------------------------------------------------------------------------
+constexpr int kGmTile = 128;
+constexpr int kGmThreads = 256;
+constexpr int kGmStages = 3;
+constexpr int kGmStageA = 8192;  // bytes of one A stage (128 rows x 64 bytes)
+constexpr int kGmStageB = 8192;  // bytes of one B stage
+
+struct GemmParams {
+  const void* a;
+  const void* b;
+  void* c;
+  int m, n, k;
+  int64_t lda, ldb, ldc;
+  int tiles_m, tiles_n, per_xcd;
+  int vec_store;  // C rows and base allow 4-column vector stores
+};
+
+// Tile of workgroup L: each XCD (workgroups are dealt to the 8 XCDs in turn)
+// takes a contiguous run of tiles, row tiles fastest, so the workgroups an
+// XCD runs at once share their B column tiles and A row tiles in its L2.
+__device__ __forceinline__ bool gemm_tile(const GemmParams& p, int& tm, int& tn) {
+  const int L = blockIdx.x;
+  const int t = (L % 8) * p.per_xcd + L / 8;
+  if (t >= p.tiles_m * p.tiles_n) return false;
+  tm = t % p.tiles_m;
+  tn = t / p.tiles_m;
+  return true;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) {
+  constexpr bool F32 = T::size == 4;
+  constexpr int BK = F32 ? 16 : 32;           // k per stage
+  constexpr int BROW = kGmTile * T::size;     // bytes per B row in LDS
+  constexpr int NQ = F32 ? BK / 8 : BK / 16;  // fp32 k-groups / 16-bit k-steps per stage
+  using Bits = typename T::bits;
+  __shared__ __attribute__((aligned(1024))) char smem[kGmStages * (kGmStageA + kGmStageB)];
+
+  int tm, tn;
+  if (!gemm_tile(p, tm, tn)) return;
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int wm = wave & 1, wn = wave >> 1;  // this wave's 64 x 64 quadrant
+  const int m_tile = tm * kGmTile, n_tile = tn * kGmTile;
+  __attribute__((address_space(3))) char* const lds_base = (__attribute__((address_space(3))) char*)smem;
+  const uint32_t lds0 = (uint32_t)(size_t)lds_base;
+  const uint32_t lds_a = lds0, lds_b = lds0 + kGmStages * kGmStageA;
+
+  // Buffer resources over all of A (rows < m) and B (rows < k): rows past
+  // them read as zeros with no memory access.
+  auto rsrc = [](const void* base, uint64_t bytes) __attribute__((always_inline)) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+                 __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu)),
+                 __builtin_amdgcn_readfirstlane((int)(uint32_t)bytes), kBufRsrcWord3};
+  };
+  const uint32_t lda2 = (uint32_t)(p.lda * T::size), ldb2 = (uint32_t)(p.ldb * T::size);
+  const i32x4 ra = rsrc(p.a, (uint64_t)p.m * lda2);
+  const i32x4 rb = rsrc(p.b, (uint64_t)p.k * ldb2);
+  auto dma = [&](const i32x4& rs, uint32_t voff, uint32_t la) __attribute__((always_inline)) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(la), "v"(voff), "s"(rs)
+                 : "memory");
+  };
+  // DMA lane offsets (bytes, stage k0 = 0).  A: region R (16 rows of 64
+  // bytes) is filled by wave R % 4; lane i -> row 16 R + i / 4, slot i % 4.
+  // The slot swizzle depends only on i / 16, so one offset serves every region.
+  const uint32_t a_off = (uint32_t)(m_tile + 16 * wave + lane / 4) * lda2 +
+                         (uint32_t)(((lane % 4) ^ ((lane / 16) & 3)) * 16);
+  // B, 16-bit: regions of 4 rows of 256 bytes, lane i -> row 4 R + i / 16,
+  // slot i % 16 (swizzle 4 (row % 4) = 4 (i / 16)).  fp32: regions of 2 rows
+  // of 512 bytes, lane i -> row 2 R + i / 32, slot i % 32 (swizzle
+  // 8 ((row >> 2) & 1) = 8 ((R >> 1) & 1), and R = wave + 4 j keeps that bit).
+  uint32_t b_off;
+  if constexpr (!F32)
+    b_off = (uint32_t)(4 * wave + lane / 16) * ldb2 + (uint32_t)(n_tile * 2) +
+            (uint32_t)(((lane % 16) ^ (4 * (lane / 16))) * 16);
+  else
+    b_off = (uint32_t)(2 * wave + lane / 32) * ldb2 + (uint32_t)(n_tile * 4) +
+            (uint32_t)(((lane % 32) ^ (8 * ((wave >> 1) & 1))) * 16);
+  constexpr int A_REG = kGmStageA / 1024 / 4;  // regions per wave per stage
+  constexpr int B_REG = kGmStageB / 1024 / 4;
+  constexpr int B_RPR = 1024 / BROW;           // B rows per region
+  auto load_stage = [&](int kt, int buf) __attribute__((always_inline)) {
+    const uint32_t ka = (uint32_t)(kt * BK * T::size);  // A: column bytes of the stage
+    const uint32_t kb = (uint32_t)(kt * BK) * ldb2;     // B: row offset of the stage
+#pragma unroll
+    for (int j = 0; j < A_REG; ++j)
+      dma(ra, a_off + ka + (uint32_t)(64 * j) * lda2, lds_a + buf * kGmStageA + (wave + 4 * j) * 1024);
+#pragma unroll
+    for (int j = 0; j < B_REG; ++j)
+      dma(rb, b_off + kb + (uint32_t)(4 * B_RPR * j) * ldb2, lds_b + buf * kGmStageB + (wave + 4 * j) * 1024);
+  };
+
+  f32x16 acc[2][2];  // [m block][n block], C^T layout
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  // Operand read offsets inside a stage.
+  const int lq = lane & 31, h = lane >> 5;
+  // A: row 64 wm + 32 mb + lq, chunk c (slot c ^ ((row >> 2) & 3)).
+  const int a_row0 = 64 * wm + lq;  // + 32 mb
+  auto a_addr = [&](int mb, int c) __attribute__((always_inline)) {
+    const int row = a_row0 + 32 * mb;
+    return row * 64 + ((c ^ ((row >> 2) & 3)) << 4);
+  };
+  const int n_kt = (p.k + BK - 1) / BK;
+  const int k_rem = p.k - (n_kt - 1) * BK;  // valid k of the last stage
+
+#pragma unroll
+  for (int s = 0; s < kGmStages - 1; ++s)
+    if (s < n_kt) load_stage(s, s);
+
+  for (int kt = 0; kt < n_kt; ++kt) {
+    // stage kt has landed (this wave's loads; the barrier covers the others')
+    if (kt + 1 < n_kt) wait_vmcnt<A_REG + B_REG>();
+    else wait_vmcnt<0>();
+    lds_barrier();
+    if (kt + kGmStages - 1 < n_kt) load_stage(kt + kGmStages - 1, (kt + kGmStages - 1) % kGmStages);
+    const int buf = kt % kGmStages;
+    const char* sa = smem + buf * kGmStageA;
+    const char* sb = smem + kGmStages * kGmStageA + buf * kGmStageB;
+    const bool tail = kt == n_kt - 1 && k_rem < BK;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      if constexpr (!F32) {
+        // k-step q: k = 16 q + 8 h + 0..7 of the stage.
+        bf16x8 af[2];
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+          u32x4 raw = *(const u32x4*)(sa + a_addr(mb, 2 * q + h));
+          if (tail) {
+            uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              if (16 * q + 8 * h + e >= k_rem) w[e / 2] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
+            raw = u32x4{w[0], w[1], w[2], w[3]};
+          }
+          af[mb] = __builtin_bit_cast(bf16x8, raw);
+        }
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          // lane 16 g + 4 e + p reads row 16 q + 8 (g / 2) + 4 t + e, column
+          // chunk of n = 64 wn + 32 nb + 16 (g % 2) + 4 p.
+          const int g = lane >> 4, e = (lane >> 2) & 3, pp = lane & 3;
+          const int row = 16 * q + 8 * (g >> 1) + e;
+          const int n = 64 * wn + 32 * nb + 16 * (g & 1) + 4 * pp;
+          const int addr = row * BROW + ((((n >> 3)) ^ (4 * (row & 3))) << 4) + 8 * ((n >> 2) & 1);
+          typedef short v4s __attribute__((ext_vector_type(4)));
+          typedef __attribute__((address_space(3))) v4s lds_v4s;
+          const int boff = kGmStages * kGmStageA + buf * kGmStageB + addr;
+          const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(lds_base + boff));
+          const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(lds_base + boff + 4 * BROW));
+          const u32x4 braw = u32x4{__builtin_bit_cast(u32x2, lo).x, __builtin_bit_cast(u32x2, lo).y,
+                                   __builtin_bit_cast(u32x2, hi).x, __builtin_bit_cast(u32x2, hi).y};
+#pragma unroll
+          for (int mb = 0; mb < 2; ++mb)
+            acc[mb][nb] = Mfma<T>::mma(__builtin_bit_cast(typename Mfma<T>::frag, braw),
+                                       __builtin_bit_cast(typename Mfma<T>::frag, af[mb]), acc[mb][nb]);
+        }
+      } else {
+        // k-group q: k = 8 q + 4 h + s, s = 0..3.
+        f32x4 af[2];
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+          f32x4 v = *(const f32x4*)(sa + a_addr(mb, 2 * q + h));
+          if (tail) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+              if (8 * q + 4 * h + s >= k_rem) v[s] = 0.f;
+          }
+          af[mb] = v;
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int row = 8 * q + 4 * h + s;
+#pragma unroll
+          for (int nb = 0; nb < 2; ++nb) {
+            const int byte = (64 * wn + 32 * nb + lq) * 4;
+            const float bv = *(const float*)(sb + row * BROW + (byte ^ (128 * ((row >> 2) & 1))));
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+              acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(bv, af[mb][s], acc[mb][nb], 0, 0, 0);
+          }
+        }
+      }
+    }
+  }
+  wait_vmcnt<0>();
+
+  // lane (lq, h) holds row m = m_tile + 64 wm + 32 mb + lq and, for a = 0..3,
+  // columns n = n_tile + 64 wn + 32 nb + 8 a + 4 h + 0..3.
+  Bits* cbase = (Bits*)p.c;
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb) {
+    const int m = m_tile + 64 * wm + 32 * mb + lq;
+    if (m >= p.m) continue;
+    Bits* crow = cbase + (int64_t)m * p.ldc;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const int n = n_tile + 64 * wn + 32 * nb + 8 * a + 4 * h;
+        const float v[4] = {acc[mb][nb][4 * a], acc[mb][nb][4 * a + 1], acc[mb][nb][4 * a + 2],
+                            acc[mb][nb][4 * a + 3]};
+        if (p.vec_store && n + 3 < p.n) {
+          if constexpr (F32) {
+            *(f32x4*)(crow + n) = f32x4{v[0], v[1], v[2], v[3]};
+          } else {
+            const float x0[2] = {v[0], v[1]}, x1[2] = {v[2], v[3]};
+            *(u32x2*)(crow + n) = u32x2{pack2<T>(x0), pack2<T>(x1)};
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < p.n) crow[n + e] = from_f32<T>(v[e]);
+        }
+      }
+  }
+}
+
+// Any shape and alignment (the MFMA kernel needs 16-byte aligned rows):
+// 64 x 64 tiles of C, 256 threads with 4 x 4 outputs each, fp32 FMA over
+// 16-deep K slices staged in LDS with bounds checks.  Used for small or odd
+// shapes only.
+template <typename T>
+__global__ __launch_bounds__(256) void gemm_simple_kernel(GemmParams p) {
+  using Bits = typename T::bits;
+  __shared__ float sa[16][65];
+  __shared__ float sb[16][65];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < p.k; k0 += 16) {
+    for (int i = threadIdx.x; i < 16 * 64; i += 256) {
+      const int kk = i / 64, mm = i % 64;
+      const int m = m0 + mm, k = k0 + kk;
+      sa[kk][mm] = (m < p.m && k < p.k) ? to_f32<T>(((const Bits*)p.a)[(int64_t)m * p.lda + k]) : 0.f;
+      const int n = n0 + mm;
+      sb[kk][mm] = (n < p.n && k < p.k) ? to_f32<T>(((const Bits*)p.b)[(int64_t)k * p.ldb + n]) : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(sa[kk][ty * 4 + i], sb[kk][tx * 4 + j], acc[i][j]);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = m0 + ty * 4 + i, n = n0 + tx * 4 + j;
+      if (m < p.m && n < p.n) ((Bits*)p.c)[(int64_t)m * p.ldc + n] = from_f32<T>(acc[i][j]);
+    }
+}
+
+template <typename T>
+int launch_gemm(const void* a, const void* b, void* c, int m, int n, int k, int64_t lda, int64_t ldb, int64_t ldc,
+                hipStream_t st) {
+  GemmParams p{};
+  p.a = a; p.b = b; p.c = c;
+  p.m = m; p.n = n; p.k = k;
+  p.lda = lda; p.ldb = ldb; p.ldc = ldc;
+  const int64_t esize = T::size;
+  const int64_t vec = 16 / esize;  // elements per 16-byte chunk
+  const bool aligned = lda % vec == 0 && ldb % vec == 0 && n % vec == 0 && ((uintptr_t)a % 16) == 0 &&
+                       ((uintptr_t)b % 16) == 0;
+  // 32-bit buffer offsets: all of A and all of B must be addressable.
+  // (stage reads run up to one tile past the last row / k of each operand)
+  const bool fits = ((int64_t)m + kGmTile + 1) * lda * esize < ((int64_t)1 << 32) &&
+                    ((int64_t)k + 64 + 1) * ldb * esize < ((int64_t)1 << 32);
+  if (aligned && fits) {
+    p.tiles_m = (m + kGmTile - 1) / kGmTile;
+    p.tiles_n = (n + kGmTile - 1) / kGmTile;
+    const int tiles = p.tiles_m * p.tiles_n;
+    p.per_xcd = (tiles + 7) / 8;
+    p.vec_store = ldc % 4 == 0 && ((uintptr_t)c % (4 * esize)) == 0;
+    hipLaunchKernelGGL((gemm_mfma_kernel<T>), dim3((unsigned)(8 * p.per_xcd)), dim3(kGmThreads), 0, st, p);
+    return tl_launch_status();
+  }
+  dim3 grid((unsigned)((n + 63) / 64), (unsigned)((m + 63) / 64));
+  hipLaunchKernelGGL((gemm_simple_kernel<T>), grid, dim3(256), 0, st, p);
+  return tl_launch_status();
+}
+
 }  // namespace
 
 extern "C" {
@@ -267,19 +572,11 @@ int tl_gemm(const void* a, const void* b, void* c, int m, int n, int k, int64_t 
       }
     }
   }
-  rocblas_handle h = device_handle();
-  if (!h) return TL_ERR_INVALID;
-  if (rocblas_set_stream(h, st) != rocblas_status_success) return TL_ERR_INVALID;
-  const float alpha = 1.f, beta = 0.f;
-  const rocblas_datatype t = dtype == TL_DTYPE_F32   ? rocblas_datatype_f32_r
-                             : dtype == TL_DTYPE_F16 ? rocblas_datatype_f16_r
-                                                     : rocblas_datatype_bf16_r;
-  // Column-major view: C^T (n x m, ld ldc) = B^T (n x k, ld ldb) . A^T (k x m, ld lda).
-  const rocblas_status s = rocblas_gemm_ex(h, rocblas_operation_none, rocblas_operation_none, n, m, k, &alpha, b, t,
-                                           (rocblas_int)ldb, a, t, (rocblas_int)lda, &beta, c, t, (rocblas_int)ldc, c,
-                                           t, (rocblas_int)ldc, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-  if (s != rocblas_status_success) return s == rocblas_status_invalid_size ? TL_ERR_UNSUPPORTED : TL_ERR_INVALID;
-  return tl_launch_status();
+  switch (dtype) {
+    case TL_DTYPE_F32: return launch_gemm<F32>(a, b, c, m, n, k, lda, ldb, ldc, st);
+    case TL_DTYPE_F16: return launch_gemm<F16>(a, b, c, m, n, k, lda, ldb, ldc, st);
+    default: return launch_gemm<BF16>(a, b, c, m, n, k, lda, ldb, ldc, st);
+  }
 }
 
 }  // extern "C"

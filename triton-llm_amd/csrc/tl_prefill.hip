@@ -64,36 +64,6 @@ struct FlashParams {
   int q_triple;    // first three rounds use the balanced-triple order
 };
 
-template <typename T>
-struct Mfma;
-
-template <>
-struct Mfma<BF16> {
-  typedef bf16x8 frag;
-  static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ frag pack(const float* x) {
-    frag r;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) r[i] = (__bf16)x[i];
-    return r;
-  }
-};
-
-template <>
-struct Mfma<F16> {
-  typedef f16x8 frag;
-  static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ frag pack(const float* x) {
-    frag r;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) r[i] = (_Float16)x[i];
-    return r;
-  }
-};
 
 __device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32); }
 
@@ -163,20 +133,6 @@ __device__ __forceinline__ int lds_swz(int r) {
   else return 4 * ((r >> 1) & 1) + ((r >> 2) & 3);
 }
 
-// Two fp32 values -> one 32-bit word of two 16-bit values (low half first),
-// rounded to nearest even.
-template <typename T>
-__device__ __forceinline__ uint32_t pack2(const float (&x)[2]);
-template <>
-__device__ __forceinline__ uint32_t pack2<BF16>(const float (&x)[2]) {
-  const bf16x2 v = {(__bf16)x[0], (__bf16)x[1]};
-  return __builtin_bit_cast(uint32_t, v);
-}
-template <>
-__device__ __forceinline__ uint32_t pack2<F16>(const float (&x)[2]) {
-  const f16x2 v = {(_Float16)x[0], (_Float16)x[1]};
-  return __builtin_bit_cast(uint32_t, v);
-}
 
 __device__ __forceinline__ float max_xor32(float x) {
   const uint32_t u = __float_as_uint(x);
@@ -190,19 +146,6 @@ __device__ __forceinline__ float sum_xor32(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// s_waitcnt vmcnt(N) (gfx9 encoding; expcnt and lgkmcnt left unconstrained).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
-}
-
-// Workgroup barrier that orders LDS only (global prefetches stay in flight).
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 // ---------------------------------------------------------------------------
 // Persistence: one workgroup per CU walks a static list of query tiles.

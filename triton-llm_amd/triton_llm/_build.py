@@ -40,9 +40,8 @@ HIPCC_FLAGS = [
 ]
 
 
-# rocBLAS carries the model's plain projection GEMMs (tl_gemm.hip).
-ROCM_LIB = "/opt/rocm/lib"
-LINK_LIBS = [f"-L{ROCM_LIB}", "-lrocblas", f"-Wl,-rpath,{ROCM_LIB}"]
+# Only the HIP runtime is linked (hipcc adds it); every kernel is this library's own.
+LINK_LIBS: list[str] = []
 
 
 def _hipcc() -> str:

@@ -6,8 +6,8 @@ asserts and empty-dimension handling (triton_llm/kernels/gemm.py:53-108): h
 The reference is fp32 only; float16 and bfloat16 are accepted as well, with
 fp32 accumulation.  ``K == 0`` gives zeros (the reference leaves the fresh
 output unwritten).  ``tl_gemm`` streams the weights with a hand-written
-kernel for up to 8 rows (a decoded token) and hands larger products to
-rocBLAS.
+kernel for up to 8 rows (a decoded token) and runs larger products on the
+matrix cores with a hand-written MFMA kernel.
 """
 
 from __future__ import annotations
