@@ -221,8 +221,8 @@ int launch_skinny(const void* a, const void* b, void* c, int m, int n, int k, in
 // Prompt-sized products on the matrix cores (m > kSkinnyMaxM).
 //
 // Workgroup tile 128 x 128 of C, 4 waves in 2 x 2, each wave 64 x 64 (2 x 2
-// blocks of 32 x 32).  K is walked in LDS stages (16-bit: 32 k, fp32: 16 k),
-// three stages in flight, every tile moved global -> LDS by LDS-DMA
+// blocks of 32 x 32).  K is walked in LDS stages (16-bit: 64 k in two
+// stages; fp32: 16 k in three), every tile moved global -> LDS by LDS-DMA
 // (buffer_load ... lds: no register round trip), every wave loading a
 // quarter.  Each wave computes the transposed block C^T = B^T . A^T with
 // the MFMA, so a lane ends up owning one row of C and 4 consecutive columns
@@ -230,11 +230,11 @@ int launch_skinny(const void* a, const void* b, void* c, int m, int n, int k, in
 //
 // Operand layouts in LDS (rows unpadded, 16-byte chunks XOR-swizzled so that
 // every operand read is conflict-free):
-//   A stage: 128 rows (m) x 64 bytes (k), chunk c of row r at slot
-//            c ^ ((r >> 2) & 3).  A fragment: lane (l % 32, h = l / 32) reads
+//   A stage: 128 rows (m) x BKB bytes (k), chunk c of row r at slot
+//            c ^ a_swz(r).  A fragment: lane (l % 32, h = l / 32) reads
 //            one 16-byte chunk of row l % 32 of its block: 8 consecutive k
 //            (16-bit) or 4 (fp32).
-//   B stage, 16-bit: 32 rows (k) x 256 bytes (n), chunk c of row r at slot
+//   B stage, 16-bit: 64 rows (k) x 256 bytes (n), chunk c of row r at slot
 //            c ^ (4 (r % 4)).  The MFMA wants 8 consecutive k of one column
 //            per lane, i.e. B read down a column: two ds_read_b64_tr_b16.
 //            That instruction transposes within each 16-lane group: output
@@ -251,9 +251,6 @@ int launch_skinny(const void* a, const void* b, void* c, int m, int n, int k, in
 // ---------------------------------------------------------------------------
 constexpr int kGmTile = 128;
 constexpr int kGmThreads = 256;
-constexpr int kGmStages = 3;
-constexpr int kGmStageA = 8192;  // bytes of one A stage (128 rows x 64 bytes)
-constexpr int kGmStageB = 8192;  // bytes of one B stage
 
 struct GemmParams {
   const void* a;
@@ -277,15 +274,27 @@ __device__ __forceinline__ bool gemm_tile(const GemmParams& p, int& tm, int& tn)
   return true;
 }
 
-template <typename T>
+// BKB: bytes of k per A row per stage (64 or 128); NST: stages in LDS.
+template <typename T, int BKB, int NST>
 __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) {
   constexpr bool F32 = T::size == 4;
-  constexpr int BK = F32 ? 16 : 32;           // k per stage
+  constexpr int BK = BKB / T::size;           // k per stage
+  constexpr int ACH = BKB / 16;               // 16-byte chunks per A row (4 or 8)
   constexpr int BROW = kGmTile * T::size;     // bytes per B row in LDS
   constexpr int NQ = F32 ? BK / 8 : BK / 16;  // fp32 k-groups / 16-bit k-steps per stage
+  constexpr int kGmStages = NST;
+  constexpr int kGmStageA = kGmTile * BKB;    // bytes of one A stage
+  constexpr int kGmStageB = BK * BROW;        // bytes of one B stage
+  static_assert(kGmStageA == kGmStageB, "A and B stages are the same size");
   using Bits = typename T::bits;
   __shared__ __attribute__((aligned(1024))) char smem[kGmStages * (kGmStageA + kGmStageB)];
 
+  // 16 lanes read one chunk of 16 consecutive A rows: the XOR spreads them
+  // over all 16 four-bank groups (64-byte rows: bits 2-3 of the row; 128-byte
+  // rows: bits 1-3).
+  auto a_swz = [](int row) __attribute__((always_inline)) {
+    return ACH == 4 ? (row >> 2) & 3 : (row >> 1) & 7;
+  };
   int tm, tn;
   if (!gemm_tile(p, tm, tn)) return;
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
@@ -311,11 +320,14 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) 
     asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(la), "v"(voff), "s"(rs)
                  : "memory");
   };
-  // DMA lane offsets (bytes, stage k0 = 0).  A: region R (16 rows of 64
-  // bytes) is filled by wave R % 4; lane i -> row 16 R + i / 4, slot i % 4.
-  // The slot swizzle depends only on i / 16, so one offset serves every region.
-  const uint32_t a_off = (uint32_t)(m_tile + 16 * wave + lane / 4) * lda2 +
-                         (uint32_t)(((lane % 4) ^ ((lane / 16) & 3)) * 16);
+  // DMA lane offsets (bytes, stage k0 = 0).  A: region R (1 KiB: 1024 / BKB
+  // rows) is filled by wave R % 4; lane i -> row R * (1024 / BKB) + i / ACH,
+  // slot i % ACH.  The slot swizzle (see a_swz) depends on bits of the row
+  // that the region step 4 j does not change, so one offset serves every
+  // region of this wave.
+  constexpr int A_RPR = 1024 / BKB;
+  const int a_row0 = A_RPR * wave + lane / ACH;
+  const uint32_t a_off = (uint32_t)(m_tile + a_row0) * lda2 + (uint32_t)(((lane % ACH) ^ a_swz(a_row0)) * 16);
   // B, 16-bit: regions of 4 rows of 256 bytes, lane i -> row 4 R + i / 16,
   // slot i % 16 (swizzle 4 (row % 4) = 4 (i / 16)).  fp32: regions of 2 rows
   // of 512 bytes, lane i -> row 2 R + i / 32, slot i % 32 (swizzle
@@ -335,7 +347,7 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) 
     const uint32_t kb = (uint32_t)(kt * BK) * ldb2;     // B: row offset of the stage
 #pragma unroll
     for (int j = 0; j < A_REG; ++j)
-      dma(ra, a_off + ka + (uint32_t)(64 * j) * lda2, lds_a + buf * kGmStageA + (wave + 4 * j) * 1024);
+      dma(ra, a_off + ka + (uint32_t)(4 * A_RPR * j) * lda2, lds_a + buf * kGmStageA + (wave + 4 * j) * 1024);
 #pragma unroll
     for (int j = 0; j < B_REG; ++j)
       dma(rb, b_off + kb + (uint32_t)(4 * B_RPR * j) * ldb2, lds_b + buf * kGmStageB + (wave + 4 * j) * 1024);
@@ -351,11 +363,10 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) 
 
   // Operand read offsets inside a stage.
   const int lq = lane & 31, h = lane >> 5;
-  // A: row 64 wm + 32 mb + lq, chunk c (slot c ^ ((row >> 2) & 3)).
-  const int a_row0 = 64 * wm + lq;  // + 32 mb
+  // A: row 64 wm + 32 mb + lq, chunk c at slot c ^ a_swz(row).
   auto a_addr = [&](int mb, int c) __attribute__((always_inline)) {
-    const int row = a_row0 + 32 * mb;
-    return row * 64 + ((c ^ ((row >> 2) & 3)) << 4);
+    const int row = 64 * wm + 32 * mb + lq;
+    return row * BKB + ((c ^ a_swz(row)) << 4);
   };
   const int n_kt = (p.k + BK - 1) / BK;
   const int k_rem = p.k - (n_kt - 1) * BK;  // valid k of the last stage
@@ -365,9 +376,19 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) 
     if (s < n_kt) load_stage(s, s);
 
   for (int kt = 0; kt < n_kt; ++kt) {
-    // stage kt has landed (this wave's loads; the barrier covers the others')
-    if (kt + 1 < n_kt) wait_vmcnt<A_REG + B_REG>();
-    else wait_vmcnt<0>();
+    // stage kt has landed (this wave's loads; the barrier covers the others'):
+    // the stages issued after it, up to NST - 2 of them, may stay in flight
+    constexpr int PER = A_REG + B_REG;
+    if constexpr (NST >= 4) {
+      if (kt + 2 < n_kt) wait_vmcnt<2 * PER>();
+      else if (kt + 1 < n_kt) wait_vmcnt<PER>();
+      else wait_vmcnt<0>();
+    } else if constexpr (NST == 3) {
+      if (kt + 1 < n_kt) wait_vmcnt<PER>();
+      else wait_vmcnt<0>();
+    } else {
+      wait_vmcnt<0>();
+    }
     lds_barrier();
     if (kt + kGmStages - 1 < n_kt) load_stage(kt + kGmStages - 1, (kt + kGmStages - 1) % kGmStages);
     const int buf = kt % kGmStages;
@@ -531,7 +552,15 @@ int launch_gemm(const void* a, const void* b, void* c, int m, int n, int k, int6
     const int tiles = p.tiles_m * p.tiles_n;
     p.per_xcd = (tiles + 7) / 8;
     p.vec_store = ldc % 4 == 0 && ((uintptr_t)c % (4 * esize)) == 0;
-    hipLaunchKernelGGL((gemm_mfma_kernel<T>), dim3((unsigned)(8 * p.per_xcd)), dim3(kGmThreads), 0, st, p);
+    // Measured at the models' prompt shapes (2048 rows): 16-bit runs best
+    // with 64 k per stage in two stages (729 against 645 TFLOP/s with 32 k
+    // in three, 691 with 32 k in four, 507 with 64 k in three); fp32 is
+    // within 1% across those and keeps 16 k in three stages.
+    const dim3 grid((unsigned)(8 * p.per_xcd));
+    if constexpr (T::size == 2)
+      hipLaunchKernelGGL((gemm_mfma_kernel<T, 128, 2>), grid, dim3(kGmThreads), 0, st, p);
+    else
+      hipLaunchKernelGGL((gemm_mfma_kernel<T, 64, 3>), grid, dim3(kGmThreads), 0, st, p);
     return tl_launch_status();
   }
   dim3 grid((unsigned)((n + 63) / 64), (unsigned)((m + 63) / 64));
