@@ -270,62 +270,74 @@ FP32_PEAK_TFLOPS = 157.3
 
 
 def bench_gemm(steps, warmup, cpu=True, models=("llama3.2-3b", "smollm2-360m"), prompt=2048):
-    """Time every projection of one layer (q, k, v, o, gate, up, down) of
-    each model for one decoded token (M = 1, weight-bandwidth bound) and for
-    a prompt (M = prompt, MFMA bound), fp32 as the reference runs them and
-    bf16.  Weights rotate over replicas totalling >= 1 GB so each call reads
-    them from HBM, not MALL.  The CPU baseline is NumPy float32 matmul on
-    the host (a bounded sample: one pass per shape, M = 1 and 128)."""
+    """Time the projections of one layer (q, k, v, o, gate, up, down) of each
+    model for one decoded token (M = 1, weight-bandwidth bound) and for a
+    prompt (M = prompt, MFMA bound), fp32 as the reference runs them and bf16,
+    two ways: seven gemm calls, and the grouped form a layer step uses
+    (gemm_grouped for q/k/v and for gate/up, gemm for o and down: four
+    launches, plus a split-K reduce each for M = 1).  Each layer's launches
+    are recorded once and replayed back to back between two events.  For
+    M = 1 the weights rotate over copies totalling >= 1 GB so each layer
+    reads them from HBM, not MALL.  The CPU baseline is NumPy float32 matmul
+    on the host (a bounded sample: one pass per shape, M = 1 and 128)."""
     from triton_llm import gpu
-    from triton_llm.kernels import gemm
+    from triton_llm.kernels import gemm, gemm_grouped
+    from triton_llm.kernels._common import record
 
     lib = gpu.runtime()
     rows = []
     for model in models:
         e, q, kv, inter = GEMM_MODELS[model]
-        shapes = [("q", e, q), ("k", e, kv), ("v", e, kv), ("o", q, e), ("gate", e, inter), ("up", e, inter), ("down", inter, e)]
-        for dt, gdt, esz, peak in (("float32", np.float32, 4, FP32_PEAK_TFLOPS), ("bfloat16", gpu.bfloat16, 2, PEAK_TFLOPS["bfloat16"])):
-            acc = {M: [0.0, 0, 0] for M in (1, prompt)}  # ms, flops, bytes per layer
-            for name, K, N in shapes:
-                wbytes = K * N * esz
-                rng = np.random.default_rng(K + N)
-                wh = rng.standard_normal((K, N), dtype=np.float32)
-                if dt == "bfloat16":
-                    wh = (wh.view(np.uint32) >> 16).astype(np.uint16)
-                w0 = gpu.to_device(wh, gdt)
-                for M in (1, prompt):
-                    # one token reads the whole weight: rotate copies past MALL
-                    reps = max(1, int(np.ceil(1e9 / wbytes))) if M == 1 else 1
-                    ws = [w0]
-                    for _ in range(reps - 1):
-                        w = gpu.allocate((K, N), gdt)
-                        gpu.copy_(w, w0)
-                        ws.append(w)
-                    hh = rng.standard_normal((M, K), dtype=np.float32)
-                    if dt == "bfloat16":
-                        hh = (hh.view(np.uint32) >> 16).astype(np.uint16)
-                    h = gpu.to_device(hh, gdt)
-                    out = gpu.allocate((M, N), gdt)
-                    for i in range(warmup):
-                        gemm(h, ws[i % reps], out_dev=out)
-                    ev = Events(lib, 2)
-                    ev.record(0)
-                    for i in range(steps):
-                        gemm(h, ws[i % reps], out_dev=out)
-                    ev.record(1)
-                    ms = ev.ms(0, 1) / steps
-                    ev.close()
-                    acc[M][0] += ms
-                    acc[M][1] += 2 * M * K * N
-                    acc[M][2] += wbytes + (M * K + M * N) * esz
-                    del ws
-            for M, (tot_ms, tot_flops, tot_bytes) in acc.items():
-                rows.append({
-                    "model": model, "dtype": dt, "M": M, "ms_per_layer": tot_ms,
-                    "tflops": tot_flops / (tot_ms * 1e-3) / 1e12, "frac_mfma": tot_flops / (tot_ms * 1e-3) / 1e12 / peak,
-                    "gbs": tot_bytes / (tot_ms * 1e-3) / 1e9, "frac_hbm": tot_bytes / (tot_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                })
-                log(f"gemm {model} {dt} M={M}: {tot_ms*1e3:.1f} us/layer, {rows[-1]['tflops']:.1f} TFLOP/s, {rows[-1]['gbs']:.0f} GB/s")
+        shapes = {"q": (e, q), "k": (e, kv), "v": (e, kv), "o": (q, e), "gate": (e, inter), "up": (e, inter),
+                  "down": (inter, e)}
+        for dt, gdt, esz, peak in (("float32", np.float32, 4, FP32_PEAK_TFLOPS),
+                                   ("bfloat16", gpu.bfloat16, 2, PEAK_TFLOPS["bfloat16"])):
+            rng = np.random.default_rng(len(model))
+
+            def host(shape):
+                x = rng.standard_normal(shape, dtype=np.float32)
+                return (x.view(np.uint32) >> 16).astype(np.uint16) if dt == "bfloat16" else x
+
+            layer_w = sum(K * N for K, N in shapes.values()) * esz
+            w0 = {name: gpu.to_device(host(shape), gdt) for name, shape in shapes.items()}
+            for M in (1, prompt):
+                reps = max(1, int(np.ceil(1e9 / layer_w))) if M == 1 else 1
+                W = [w0]
+                for _ in range(reps - 1):
+                    copy = {}
+                    for name, (K, N) in shapes.items():
+                        copy[name] = gpu.allocate((K, N), gdt)
+                        gpu.copy_(copy[name], w0[name])
+                    W.append(copy)
+                x = {d: gpu.to_device(host((M, d)), gdt) for d in {e, q, inter}}
+                out = {name: gpu.allocate((M, N), gdt) for name, (K, N) in shapes.items()}
+
+                def separate(r):
+                    for name, (K, N) in shapes.items():
+                        gemm(x[K], W[r][name], out_dev=out[name])
+
+                def grouped(r):
+                    gemm_grouped(x[e], [W[r]["q"], W[r]["k"], W[r]["v"]], [out["q"], out["k"], out["v"]])
+                    gemm(x[q], W[r]["o"], out_dev=out["o"])
+                    gemm_grouped(x[e], [W[r]["gate"], W[r]["up"]], [out["gate"], out["up"]])
+                    gemm(x[inter], W[r]["down"], out_dev=out["down"])
+
+                flops = sum(2 * M * K * N for K, N in shapes.values())
+                nbytes = layer_w + sum((M * K + M * N) * esz for K, N in shapes.values())
+                for form, fn in (("seven gemm calls", separate), ("grouped", grouped)):
+                    for r in range(reps):
+                        fn(r)
+                    gpu.synchronize()
+                    calls = [record(lambda r=r: fn(r)) for r in range(reps)]
+                    ms, _, _ = time_calls(lib, calls, steps, warmup, 0.0)
+                    rows.append({
+                        "model": model, "dtype": dt, "M": M, "form": form, "ms_per_layer": ms,
+                        "tflops": flops / (ms * 1e-3) / 1e12, "frac_mfma": flops / (ms * 1e-3) / 1e12 / peak,
+                        "gbs": nbytes / (ms * 1e-3) / 1e9, "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                    })
+                    log(f"gemm {model} {dt} M={M} {form}: {ms * 1e3:.1f} us/layer, {rows[-1]['tflops']:.1f} TFLOP/s, "
+                        f"{rows[-1]['gbs']:.0f} GB/s")
+                del W
     res = {"metric": "projection GEMMs per layer (tl_gemm)", "rows": rows}
     res["layers"] = bench_layers(steps, warmup)
     res["sample"] = bench_sample(steps, warmup, cpu=cpu)

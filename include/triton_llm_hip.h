@@ -209,6 +209,18 @@ size_t tl_gemm_workspace_bytes(int m, int n, int k, int dtype);
 int tl_gemm(const void* a, const void* b, void* c, int m, int n, int k, int64_t lda,
             int64_t ldb, int64_t ldc, void* workspace, size_t workspace_bytes, int dtype,
             void* stream);
+/* Up to four products that share A, C_g = A . B_g with B_g (k, n[g]),
+ * in one launch (plus one split-K reduce launch for all of them when m <= 8):
+ * the q/k/v projections of a layer, or gate/up.  No reference counterpart as
+ * one call: the reference's model calls gemm (gemm.py:53-108) once per
+ * projection (smollm2_triton/model.py:285-287, :360-361).  Per group the
+ * arguments mean what tl_gemm's mean; groups with n[g] = 0 are skipped.
+ * Workspace: tl_gemm_grouped_workspace_bytes(m, k, count, n, dtype). */
+size_t tl_gemm_grouped_workspace_bytes(int m, int k, int count, const int* n, int dtype);
+int tl_gemm_grouped(const void* a, int m, int k, int64_t lda, int count,
+                    const void* const* b, void* const* c, const int* n,
+                    const int64_t* ldb, const int64_t* ldc, void* workspace,
+                    size_t workspace_bytes, int dtype, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Layers around the projections, contiguous rows, fp32 math in any dtype.

@@ -18,7 +18,7 @@ from oracle import numerics as on
 from oracle.gemm import gemm_ref
 from tests import _helpers as H
 from triton_llm import gpu
-from triton_llm.kernels import gemm
+from triton_llm.kernels import gemm, gemm_grouped
 
 pytestmark = pytest.mark.gpu
 
@@ -180,3 +180,30 @@ def test_gemm_strided_operands_keep_padding_out(dtype, K):
     else:  # output rounding of 16-bit C; NaN anywhere fails
         np.testing.assert_allclose(c[:, :N], exp, rtol=8e-3, atol=1e-2)
     assert (c[:, N:] == 3.0).all()
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+@pytest.mark.parametrize("M", [1, 3, 8, 37, 300])
+@pytest.mark.parametrize("K,Ns", [(3072, (3072, 1024, 1024)), (960, (2560, 2560)), (576, (576, 192, 192)),
+                                  (100, (40, 0, 24))])
+def test_gemm_grouped_matches_each_product(dtype, M, K, Ns):
+    """q/k/v (and gate/up) in one launch: every output against the oracle.
+    Few-row products share one K-slice plan and one reduce; prompts share one
+    MFMA tile space; a zero-width group is skipped; (100, (40, 0, 24)) has
+    rows that are not 16-byte aligned (the simple kernel, one grid layer per
+    group)."""
+    print(f"[case] gemm_grouped {dtype} M={M} K={K} N={Ns}", flush=True)
+    rng = np.random.default_rng(M + K + sum(Ns))
+    a = on.to_storage(rng.standard_normal((M, K), dtype=np.float32), dtype)
+    bs = [on.to_storage(rng.standard_normal((K, n), dtype=np.float32) / np.sqrt(K), dtype) for n in Ns]
+    outs = gemm_grouped(H.upload(a, dtype), [H.upload(b, dtype) for b in bs])
+    for b, o in zip(bs, outs):
+        got = on.from_storage(H.download(o), dtype)
+        exp = gemm_ref(on.from_storage(a, dtype), on.from_storage(b, dtype))
+        assert got.shape == exp.shape
+        if dtype == "float32":
+            err = H.max_abs(got, exp)
+            H.report(f"grouped {dtype} {M}x{K}@{K}x{b.shape[1]}", err, 2e-3)
+            assert err <= 2e-3
+        else:
+            np.testing.assert_allclose(got, exp, rtol=8e-3, atol=1e-2)

@@ -27,7 +27,8 @@ def rms_norm_cpu(x, w, eps=1e-5, dtype="float32"):
     return H.download(out).reshape(x.shape)
 
 
-@pytest.mark.parametrize("M,N", [(8, 64), (16, 128), (32, 576), (16, 960), (8, 2048), (16, 777), (4, 1), (3, 3072)])
+@pytest.mark.parametrize("M,N", [(8, 64), (16, 128), (32, 576), (16, 960), (8, 2048), (16, 777), (4, 1), (3, 3072),
+                                 (2, 8192), (2, 8193), (2, 10000)])
 def test_rms_norm_reference_cases(M, N):
     np.random.seed(42)
     x = np.random.randn(M, N).astype(np.float32)

@@ -42,10 +42,35 @@ struct SkinnyPlan {
   int ks;       // K-slices
 };
 
-SkinnyPlan skinny_plan(int n, int k, int esize) {
+// Products that share A (q/k/v, gate/up): C_g = A . B_g, B_g (k x n_g), for
+// g < count, run as one tile space in one launch.  tile0[g] is group g's
+// first tile in that space (tile0[count] = all tiles); col0[g] its first
+// column in the concatenated width (the split-K partials).
+constexpr int kMaxGroups = 4;
+struct GemmGroups {
+  int count;
+  const void* b[kMaxGroups];
+  void* c[kMaxGroups];
+  int n[kMaxGroups];
+  int64_t ldb[kMaxGroups], ldc[kMaxGroups];
+  int tile0[kMaxGroups + 1];
+  int col0[kMaxGroups + 1];
+};
+
+// The group whose tiles (or columns, with col0) include t.
+__device__ __forceinline__ int find_group(const int (&first)[kMaxGroups + 1], int count, int t) {
+  int g = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxGroups; ++i)
+    if (i < count && t >= first[i]) g = i;
+  return g;
+}
+
+SkinnyPlan skinny_plan(const GemmGroups& G, int k, int esize) {
   SkinnyPlan s;
   s.cols = 256 / esize;
-  s.n_tiles = (n + s.cols - 1) / s.cols;
+  s.n_tiles = 0;
+  for (int g = 0; g < G.count; ++g) s.n_tiles += (G.n[g] + s.cols - 1) / s.cols;
   const int step = kSkRowsPerStep;
   const int ks_target = kSkTargetTiles / s.n_tiles > 1 ? kSkTargetTiles / s.n_tiles : 1;
   int tk = (k + ks_target - 1) / ks_target;
@@ -56,9 +81,12 @@ SkinnyPlan skinny_plan(int n, int k, int esize) {
   return s;
 }
 
-size_t skinny_workspace_bytes(int m, int n, int k, int esize) {
-  const SkinnyPlan s = skinny_plan(n, k, esize);
-  return (size_t)s.ks * m * n * sizeof(float);
+size_t skinny_workspace_bytes(int m, const GemmGroups& G, int k, int esize) {
+  const SkinnyPlan s = skinny_plan(G, k, esize);
+  if (s.ks == 1) return 0;  // single K-slice: stored to C directly
+  size_t ntot = 0;
+  for (int g = 0; g < G.count; ++g) ntot += (size_t)G.n[g];
+  return (size_t)s.ks * m * ntot * sizeof(float);
 }
 
 template <typename T>
@@ -71,17 +99,16 @@ __device__ __forceinline__ void unpack_words(const u32x4& w, float (&f)[16 / T::
 }
 
 // One workgroup: K-slice blockIdx.y (rows [k0, k0 + tk)) x column tile
-// blockIdx.x.  Lane (wave w, row group r = lane / 16, chunk c = lane % 16)
+// blockIdx.x of the groups' tile space.  Lane (wave w, row group r = lane / 16, chunk c = lane % 16)
 // reads 16 bytes of row k0 + 16 i + 4 w + r, columns chunk c; its MT x CPC
 // sums cover the rows it read.  The four row groups of a wave, then the four
 // waves, are added up and the slice's partial product is stored.
 // With a single K-slice (gridDim.y == 1) the sums are the result: they are
 // rounded and stored to C directly, and no reduce pass follows.
 template <typename T, int MT>
-__global__ __launch_bounds__(kSkThreads) void skinny_partial_kernel(const void* __restrict__ a, const void* __restrict__ b,
-                                                                     float* __restrict__ ws, void* __restrict__ out,
-                                                                     int m, int n, int k, int64_t lda, int64_t ldb,
-                                                                     int64_t ldc, int tk) {
+__global__ __launch_bounds__(kSkThreads) void skinny_partial_kernel(const void* __restrict__ a, GemmGroups G,
+                                                                     float* __restrict__ ws, int m, int k, int64_t lda,
+                                                                     int ntot, int tk) {
   constexpr int CPC = 16 / T::size;  // columns per 16-byte chunk
   constexpr int COLS = 16 * CPC;     // columns per tile
   using Bits = typename T::bits;
@@ -92,11 +119,15 @@ __global__ __launch_bounds__(kSkThreads) void skinny_partial_kernel(const void* 
   const int r = lane >> 4, c = lane & 15;
   const int k0 = blockIdx.y * tk;
   const int k1 = min(k, k0 + tk);
+  const int grp = find_group(G.tile0, G.count, blockIdx.x);
+  const void* b = G.b[grp];
+  const int n = G.n[grp];
+  const int64_t ldb = G.ldb[grp];
   // The tile's rows of B as one buffer that ends at the last row's last
   // column inside the matrix: loads of rows past the slice read zeros with no
   // memory access.  (Chunks past column n of earlier rows read the next
   // row's data; those columns are never stored.)
-  const int tile_col0 = blockIdx.x * COLS;
+  const int tile_col0 = (blockIdx.x - G.tile0[grp]) * COLS;
   const Bits* bbase = (const Bits*)b + (int64_t)k0 * ldb + tile_col0;
   const int rows = k1 - k0;
   const int last_cols = min(COLS, n - tile_col0);
@@ -161,26 +192,28 @@ __global__ __launch_bounds__(kSkThreads) void skinny_partial_kernel(const void* 
   __syncthreads();
   for (int idx = tid; idx < MT * COLS; idx += kSkThreads) {
     const int mi = idx / COLS, cc = idx % COLS;
-    const int col = blockIdx.x * COLS + cc;
+    const int col = tile_col0 + cc;
     if (mi < m && col < n) {
       const float v = s_sum[0][mi][cc] + s_sum[1][mi][cc] + s_sum[2][mi][cc] + s_sum[3][mi][cc];
       if (gridDim.y == 1)
-        ((Bits*)out)[(int64_t)mi * ldc + col] = from_f32<T>(v);
+        ((Bits*)G.c[grp])[(int64_t)mi * G.ldc[grp] + col] = from_f32<T>(v);
       else
-        ws[((int64_t)blockIdx.y * m + mi) * n + col] = v;
+        ws[((int64_t)blockIdx.y * m + mi) * ntot + G.col0[grp] + col] = v;
     }
   }
 }
 
-// C[mi][col] = sum over K-slices of the partials, rounded to T.  Eight
-// slices' loads are in flight at a time (the sum is latency-bound).
+// C_g[mi][col] = sum over K-slices of the partials, rounded to T, for every
+// column of the concatenated width.  Eight slices' loads are in flight at a
+// time (the sum is latency-bound).
 template <typename T>
-__global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restrict__ ws, void* __restrict__ c, int m,
-                                                            int n, int64_t ldc, int ks) {
+__global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restrict__ ws, GemmGroups G, int m, int ntot,
+                                                            int ks) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= (int64_t)m * n) return;
-  const int mi = (int)(idx / n), col = (int)(idx % n);
-  const int64_t stride = (int64_t)m * n;
+  if (idx >= (int64_t)m * ntot) return;
+  const int mi = (int)(idx / ntot), colg = (int)(idx % ntot);
+  const int grp = find_group(G.col0, G.count, colg);
+  const int64_t stride = (int64_t)m * ntot;
   float s = 0.f;
   for (int q0 = 0; q0 < ks; q0 += 8) {
     float v[8];
@@ -189,31 +222,35 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restr
 #pragma unroll
     for (int j = 0; j < 8; ++j) s += v[j];
   }
-  ((typename T::bits*)c)[(int64_t)mi * ldc + col] = from_f32<T>(s);
+  ((typename T::bits*)G.c[grp])[(int64_t)mi * G.ldc[grp] + (colg - G.col0[grp])] = from_f32<T>(s);
 }
 
 template <typename T>
-int launch_skinny(const void* a, const void* b, void* c, int m, int n, int k, int64_t lda, int64_t ldb, int64_t ldc,
-                  void* ws, hipStream_t st) {
-  const SkinnyPlan s = skinny_plan(n, k, T::size);
+int launch_skinny(const void* a, GemmGroups G, int m, int k, int64_t lda, void* ws, hipStream_t st) {
+  const SkinnyPlan s = skinny_plan(G, k, T::size);
+  int ntot = 0;
+  G.tile0[0] = 0;
+  G.col0[0] = 0;
+  for (int g = 0; g < G.count; ++g) {
+    G.tile0[g + 1] = G.tile0[g] + (G.n[g] + s.cols - 1) / s.cols;
+    G.col0[g + 1] = G.col0[g] + G.n[g];
+    ntot += G.n[g];
+  }
   dim3 grid((unsigned)s.n_tiles, (unsigned)s.ks);
+  float* w = (float*)ws;
   if (m <= 1)
-    hipLaunchKernelGGL((skinny_partial_kernel<T, 1>), grid, dim3(kSkThreads), 0, st, a, b, (float*)ws, c, m, n, k, lda, ldb,
-                       ldc, s.tk);
+    hipLaunchKernelGGL((skinny_partial_kernel<T, 1>), grid, dim3(kSkThreads), 0, st, a, G, w, m, k, lda, ntot, s.tk);
   else if (m <= 2)
-    hipLaunchKernelGGL((skinny_partial_kernel<T, 2>), grid, dim3(kSkThreads), 0, st, a, b, (float*)ws, c, m, n, k, lda, ldb,
-                       ldc, s.tk);
+    hipLaunchKernelGGL((skinny_partial_kernel<T, 2>), grid, dim3(kSkThreads), 0, st, a, G, w, m, k, lda, ntot, s.tk);
   else if (m <= 4)
-    hipLaunchKernelGGL((skinny_partial_kernel<T, 4>), grid, dim3(kSkThreads), 0, st, a, b, (float*)ws, c, m, n, k, lda, ldb,
-                       ldc, s.tk);
+    hipLaunchKernelGGL((skinny_partial_kernel<T, 4>), grid, dim3(kSkThreads), 0, st, a, G, w, m, k, lda, ntot, s.tk);
   else
-    hipLaunchKernelGGL((skinny_partial_kernel<T, 8>), grid, dim3(kSkThreads), 0, st, a, b, (float*)ws, c, m, n, k, lda, ldb,
-                       ldc, s.tk);
+    hipLaunchKernelGGL((skinny_partial_kernel<T, 8>), grid, dim3(kSkThreads), 0, st, a, G, w, m, k, lda, ntot, s.tk);
   int e = tl_launch_status();
   if (e || s.ks == 1) return e;
-  const int64_t outs = (int64_t)m * n;
+  const int64_t outs = (int64_t)m * ntot;
   hipLaunchKernelGGL((skinny_reduce_kernel<T>), dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, st,
-                     (const float*)ws, c, m, n, ldc, s.ks);
+                     (const float*)ws, G, m, ntot, s.ks);
   return tl_launch_status();
 }
 
@@ -254,23 +291,24 @@ constexpr int kGmThreads = 256;
 
 struct GemmParams {
   const void* a;
-  const void* b;
-  void* c;
-  int m, n, k;
-  int64_t lda, ldb, ldc;
-  int tiles_m, tiles_n, per_xcd;
-  int vec_store;  // C rows and base allow 4-column vector stores
+  int m, k;
+  int64_t lda;
+  GemmGroups G;   // tile0 counts 128 x 128 tiles of C
+  int tiles_m, per_xcd;
+  int vec_store;  // bit g: C_g's rows and base allow 4-column vector stores
 };
 
 // Tile of workgroup L: each XCD (workgroups are dealt to the 8 XCDs in turn)
 // takes a contiguous run of tiles, row tiles fastest, so the workgroups an
 // XCD runs at once share their B column tiles and A row tiles in its L2.
-__device__ __forceinline__ bool gemm_tile(const GemmParams& p, int& tm, int& tn) {
+__device__ __forceinline__ bool gemm_tile(const GemmParams& p, int& grp, int& tm, int& tn) {
   const int L = blockIdx.x;
   const int t = (L % 8) * p.per_xcd + L / 8;
-  if (t >= p.tiles_m * p.tiles_n) return false;
-  tm = t % p.tiles_m;
-  tn = t / p.tiles_m;
+  if (t >= p.G.tile0[p.G.count]) return false;
+  grp = find_group(p.G.tile0, p.G.count, t);
+  const int local = t - p.G.tile0[grp];
+  tm = local % p.tiles_m;
+  tn = local / p.tiles_m;
   return true;
 }
 
@@ -295,8 +333,10 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) 
   auto a_swz = [](int row) __attribute__((always_inline)) {
     return ACH == 4 ? (row >> 2) & 3 : (row >> 1) & 7;
   };
-  int tm, tn;
-  if (!gemm_tile(p, tm, tn)) return;
+  int grp, tm, tn;
+  if (!gemm_tile(p, grp, tm, tn)) return;
+  const int pn = p.G.n[grp];
+  const int64_t pldb = p.G.ldb[grp], pldc = p.G.ldc[grp];
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int wm = wave & 1, wn = wave >> 1;  // this wave's 64 x 64 quadrant
@@ -313,9 +353,9 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) 
                  __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu)),
                  __builtin_amdgcn_readfirstlane((int)(uint32_t)bytes), kBufRsrcWord3};
   };
-  const uint32_t lda2 = (uint32_t)(p.lda * T::size), ldb2 = (uint32_t)(p.ldb * T::size);
+  const uint32_t lda2 = (uint32_t)(p.lda * T::size), ldb2 = (uint32_t)(pldb * T::size);
   const i32x4 ra = rsrc(p.a, (uint64_t)p.m * lda2);
-  const i32x4 rb = rsrc(p.b, (uint64_t)p.k * ldb2);
+  const i32x4 rb = rsrc(p.G.b[grp], (uint64_t)p.k * ldb2);
   auto dma = [&](const i32x4& rs, uint32_t voff, uint32_t la) __attribute__((always_inline)) {
     asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(la), "v"(voff), "s"(rs)
                  : "memory");
@@ -464,12 +504,13 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) 
 
   // lane (lq, h) holds row m = m_tile + 64 wm + 32 mb + lq and, for a = 0..3,
   // columns n = n_tile + 64 wn + 32 nb + 8 a + 4 h + 0..3.
-  Bits* cbase = (Bits*)p.c;
+  Bits* cbase = (Bits*)p.G.c[grp];
+  const bool vec = (p.vec_store >> grp) & 1;
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb) {
     const int m = m_tile + 64 * wm + 32 * mb + lq;
     if (m >= p.m) continue;
-    Bits* crow = cbase + (int64_t)m * p.ldc;
+    Bits* crow = cbase + (int64_t)m * pldc;
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
@@ -477,7 +518,7 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) 
         const int n = n_tile + 64 * wn + 32 * nb + 8 * a + 4 * h;
         const float v[4] = {acc[mb][nb][4 * a], acc[mb][nb][4 * a + 1], acc[mb][nb][4 * a + 2],
                             acc[mb][nb][4 * a + 3]};
-        if (p.vec_store && n + 3 < p.n) {
+        if (vec && n + 3 < pn) {
           if constexpr (F32) {
             *(f32x4*)(crow + n) = f32x4{v[0], v[1], v[2], v[3]};
           } else {
@@ -487,23 +528,28 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) 
         } else {
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            if (n + e < p.n) crow[n + e] = from_f32<T>(v[e]);
+            if (n + e < pn) crow[n + e] = from_f32<T>(v[e]);
         }
       }
   }
 }
 
 // Any shape and alignment (the MFMA kernel needs 16-byte aligned rows):
-// 64 x 64 tiles of C, 256 threads with 4 x 4 outputs each, fp32 FMA over
-// 16-deep K slices staged in LDS with bounds checks.  Used for small or odd
-// shapes only.
+// 64 x 64 tiles of C_g (g = blockIdx.z), 256 threads with 4 x 4 outputs
+// each, fp32 FMA over 16-deep K slices staged in LDS with bounds checks.
+// Used for small or odd shapes only.
 template <typename T>
 __global__ __launch_bounds__(256) void gemm_simple_kernel(GemmParams p) {
   using Bits = typename T::bits;
   __shared__ float sa[16][65];
   __shared__ float sb[16][65];
+  const int grp = blockIdx.z;
+  const int n_g = p.G.n[grp];
+  const Bits* bg = (const Bits*)p.G.b[grp];
+  const int64_t ldb = p.G.ldb[grp];
   const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
   const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  if (n0 >= n_g) return;  // the grid spans the widest group
   float acc[4][4] = {};
   for (int k0 = 0; k0 < p.k; k0 += 16) {
     for (int i = threadIdx.x; i < 16 * 64; i += 256) {
@@ -511,7 +557,7 @@ __global__ __launch_bounds__(256) void gemm_simple_kernel(GemmParams p) {
       const int m = m0 + mm, k = k0 + kk;
       sa[kk][mm] = (m < p.m && k < p.k) ? to_f32<T>(((const Bits*)p.a)[(int64_t)m * p.lda + k]) : 0.f;
       const int n = n0 + mm;
-      sb[kk][mm] = (n < p.n && k < p.k) ? to_f32<T>(((const Bits*)p.b)[(int64_t)k * p.ldb + n]) : 0.f;
+      sb[kk][mm] = (n < n_g && k < p.k) ? to_f32<T>(bg[(int64_t)k * ldb + n]) : 0.f;
     }
     __syncthreads();
 #pragma unroll
@@ -522,36 +568,46 @@ __global__ __launch_bounds__(256) void gemm_simple_kernel(GemmParams p) {
         for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(sa[kk][ty * 4 + i], sb[kk][tx * 4 + j], acc[i][j]);
     __syncthreads();
   }
+  Bits* cg = (Bits*)p.G.c[grp];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int m = m0 + ty * 4 + i, n = n0 + tx * 4 + j;
-      if (m < p.m && n < p.n) ((Bits*)p.c)[(int64_t)m * p.ldc + n] = from_f32<T>(acc[i][j]);
+      if (m < p.m && n < n_g) cg[(int64_t)m * p.G.ldc[grp] + n] = from_f32<T>(acc[i][j]);
     }
 }
 
 template <typename T>
-int launch_gemm(const void* a, const void* b, void* c, int m, int n, int k, int64_t lda, int64_t ldb, int64_t ldc,
-                hipStream_t st) {
+int launch_gemm(const void* a, const GemmGroups& G, int m, int k, int64_t lda, hipStream_t st) {
   GemmParams p{};
-  p.a = a; p.b = b; p.c = c;
-  p.m = m; p.n = n; p.k = k;
-  p.lda = lda; p.ldb = ldb; p.ldc = ldc;
+  p.a = a;
+  p.m = m;
+  p.k = k;
+  p.lda = lda;
+  p.G = G;
   const int64_t esize = T::size;
   const int64_t vec = 16 / esize;  // elements per 16-byte chunk
-  const bool aligned = lda % vec == 0 && ldb % vec == 0 && n % vec == 0 && ((uintptr_t)a % 16) == 0 &&
-                       ((uintptr_t)b % 16) == 0;
-  // 32-bit buffer offsets: all of A and all of B must be addressable.
-  // (stage reads run up to one tile past the last row / k of each operand)
-  const bool fits = ((int64_t)m + kGmTile + 1) * lda * esize < ((int64_t)1 << 32) &&
-                    ((int64_t)k + 64 + 1) * ldb * esize < ((int64_t)1 << 32);
-  if (aligned && fits) {
+  // Every operand's rows must be 16-byte aligned for the LDS-DMA staging, and
+  // all of A and each B addressable with 32-bit offsets (stage reads run up
+  // to one stage past the last row / k).
+  bool aligned = lda % vec == 0 && ((uintptr_t)a % 16) == 0 &&
+                 ((int64_t)m + kGmTile + 1) * lda * esize < ((int64_t)1 << 32);
+  int widest = 0;
+  for (int g = 0; g < G.count; ++g) {
+    aligned = aligned && G.ldb[g] % vec == 0 && G.n[g] % vec == 0 && ((uintptr_t)G.b[g] % 16) == 0 &&
+              ((int64_t)k + 64 + 1) * G.ldb[g] * esize < ((int64_t)1 << 32);
+    widest = G.n[g] > widest ? G.n[g] : widest;
+  }
+  if (aligned) {
     p.tiles_m = (m + kGmTile - 1) / kGmTile;
-    p.tiles_n = (n + kGmTile - 1) / kGmTile;
-    const int tiles = p.tiles_m * p.tiles_n;
-    p.per_xcd = (tiles + 7) / 8;
-    p.vec_store = ldc % 4 == 0 && ((uintptr_t)c % (4 * esize)) == 0;
+    p.G.tile0[0] = 0;
+    p.vec_store = 0;
+    for (int g = 0; g < G.count; ++g) {
+      p.G.tile0[g + 1] = p.G.tile0[g] + p.tiles_m * ((G.n[g] + kGmTile - 1) / kGmTile);
+      if (G.ldc[g] % 4 == 0 && ((uintptr_t)G.c[g] % (4 * esize)) == 0) p.vec_store |= 1 << g;
+    }
+    p.per_xcd = (p.G.tile0[G.count] + 7) / 8;
     // Measured at the models' prompt shapes (2048 rows): 16-bit runs best
     // with 64 k per stage in two stages (729 against 645 TFLOP/s with 32 k
     // in three, 691 with 32 k in four, 507 with 64 k in three); fp32 is
@@ -563,9 +619,92 @@ int launch_gemm(const void* a, const void* b, void* c, int m, int n, int k, int6
       hipLaunchKernelGGL((gemm_mfma_kernel<T, 64, 3>), grid, dim3(kGmThreads), 0, st, p);
     return tl_launch_status();
   }
-  dim3 grid((unsigned)((n + 63) / 64), (unsigned)((m + 63) / 64));
+  dim3 grid((unsigned)((widest + 63) / 64), (unsigned)((m + 63) / 64), (unsigned)G.count);
   hipLaunchKernelGGL((gemm_simple_kernel<T>), grid, dim3(256), 0, st, p);
   return tl_launch_status();
+}
+
+// Checks shared by both entry points; fills the group table.
+int make_groups(GemmGroups& G, int count, const void* const* b, void* const* c, const int* n, const int64_t* ldb,
+                const int64_t* ldc) {
+  if (count < 1 || count > kMaxGroups || !b || !c || !n || !ldb || !ldc) return TL_ERR_INVALID;
+  G = GemmGroups{};
+  G.count = count;
+  for (int g = 0; g < count; ++g) {
+    G.b[g] = b[g];
+    G.c[g] = c[g];
+    G.n[g] = n[g];
+    G.ldb[g] = ldb[g];
+    G.ldc[g] = ldc[g];
+  }
+  return 0;
+}
+
+int gemm_groups(const void* a, const GemmGroups& G, int m, int k, int64_t lda, void* workspace,
+                size_t workspace_bytes, int dtype, void* stream) {
+  if (m < 0 || k < 0) return TL_ERR_INVALID;
+  if (dtype != TL_DTYPE_F32 && dtype != TL_DTYPE_F16 && dtype != TL_DTYPE_BF16) return TL_ERR_INVALID;
+  if (m == 0) return 0;
+  for (int g = 0; g < G.count; ++g) {
+    if (G.n[g] < 0) return TL_ERR_INVALID;
+    if (G.n[g] == 0) continue;
+    if (!G.c[g] || G.ldc[g] < G.n[g] || (k > 0 && (!G.b[g] || G.ldb[g] < G.n[g]))) return TL_ERR_INVALID;
+    if (!fits_int(G.ldb[g]) || !fits_int(G.ldc[g])) return TL_ERR_UNSUPPORTED;
+  }
+  if (k > 0 && (!a || lda < k)) return TL_ERR_INVALID;
+  if (!fits_int(lda)) return TL_ERR_UNSUPPORTED;
+  const size_t esize = dtype == TL_DTYPE_F32 ? 4 : 2;
+  hipStream_t st = tl_resolve_stream(stream);
+  // Groups with no columns take no part.
+  GemmGroups live{};
+  for (int g = 0; g < G.count; ++g) {
+    if (G.n[g] == 0) continue;
+    const int i = live.count++;
+    live.b[i] = G.b[g];
+    live.c[i] = G.c[g];
+    live.n[i] = G.n[g];
+    live.ldb[i] = G.ldb[g];
+    live.ldc[i] = G.ldc[g];
+  }
+  if (live.count == 0) return 0;
+  if (k == 0) {  // empty sum: zeros, row by row when C is a strided view
+    for (int g = 0; g < live.count; ++g) {
+      const hipError_t e = hipMemset2DAsync(live.c[g], (size_t)live.ldc[g] * esize, 0, (size_t)live.n[g] * esize,
+                                            (size_t)m, st);
+      if (e != hipSuccess) return (int)e;
+    }
+    return 0;
+  }
+  if (m <= kSkinnyMaxM) {
+    bool ok = true;
+    const int cpc = 16 / (int)esize;
+    for (int g = 0; g < live.count; ++g)
+      ok = ok && live.n[g] % cpc == 0 && live.ldb[g] % cpc == 0 && ((uintptr_t)live.b[g] % 16) == 0 &&
+           (int64_t)(k - 1) * live.ldb[g] * (int64_t)esize < INT32_MAX;
+    if (ok) {
+      const size_t need = skinny_workspace_bytes(m, live, k, (int)esize);
+      if (need && (!workspace || workspace_bytes < need)) return TL_ERR_INVALID;
+      switch (dtype) {
+        case TL_DTYPE_F32: return launch_skinny<F32>(a, live, m, k, lda, workspace, st);
+        case TL_DTYPE_F16: return launch_skinny<F16>(a, live, m, k, lda, workspace, st);
+        default: return launch_skinny<BF16>(a, live, m, k, lda, workspace, st);
+      }
+    }
+  }
+  switch (dtype) {
+    case TL_DTYPE_F32: return launch_gemm<F32>(a, live, m, k, lda, st);
+    case TL_DTYPE_F16: return launch_gemm<F16>(a, live, m, k, lda, st);
+    default: return launch_gemm<BF16>(a, live, m, k, lda, st);
+  }
+}
+
+size_t groups_workspace_bytes(int m, int k, const GemmGroups& G, int dtype) {
+  if (m <= 0 || k <= 0 || m > kSkinnyMaxM) return 0;
+  GemmGroups live{};
+  for (int g = 0; g < G.count; ++g)
+    if (G.n[g] > 0) live.n[live.count++] = G.n[g];
+  if (live.count == 0) return 0;
+  return skinny_workspace_bytes(m, live, k, dtype == TL_DTYPE_F32 ? 4 : 2);
 }
 
 }  // namespace
@@ -573,39 +712,36 @@ int launch_gemm(const void* a, const void* b, void* c, int m, int n, int k, int6
 extern "C" {
 
 size_t tl_gemm_workspace_bytes(int m, int n, int k, int dtype) {
-  if (m <= 0 || n <= 0 || k <= 0 || m > kSkinnyMaxM) return 0;
-  return skinny_workspace_bytes(m, n, k, dtype == TL_DTYPE_F32 ? 4 : 2);
+  GemmGroups G{};
+  G.count = 1;
+  G.n[0] = n;
+  return groups_workspace_bytes(m, k, G, dtype);
 }
 
 int tl_gemm(const void* a, const void* b, void* c, int m, int n, int k, int64_t lda, int64_t ldb, int64_t ldc,
             void* workspace, size_t workspace_bytes, int dtype, void* stream) {
-  if (m < 0 || n < 0 || k < 0) return TL_ERR_INVALID;
-  if (dtype != TL_DTYPE_F32 && dtype != TL_DTYPE_F16 && dtype != TL_DTYPE_BF16) return TL_ERR_INVALID;
-  if (m == 0 || n == 0) return 0;
-  if (!c || ldc < n || (k > 0 && (!a || !b || lda < k || ldb < n))) return TL_ERR_INVALID;
-  if (!fits_int(lda) || !fits_int(ldb) || !fits_int(ldc)) return TL_ERR_UNSUPPORTED;
-  const size_t esize = dtype == TL_DTYPE_F32 ? 4 : 2;
-  hipStream_t st = tl_resolve_stream(stream);
-  if (k == 0) {  // empty sum: zeros, row by row when C is a strided view
-    return (int)hipMemset2DAsync(c, (size_t)ldc * esize, 0, (size_t)n * esize, (size_t)m, st);
-  }
-  if (m <= kSkinnyMaxM) {
-    if (!workspace || workspace_bytes < tl_gemm_workspace_bytes(m, n, k, dtype)) return TL_ERR_INVALID;
-    // 16-byte row chunks: the row stride and the row length must keep chunks aligned.
-    const int cpc = 16 / (int)esize;
-    if (n % cpc == 0 && ldb % cpc == 0 && ((uintptr_t)b % 16) == 0 && (int64_t)(k - 1) * ldb * esize < INT32_MAX) {
-      switch (dtype) {
-        case TL_DTYPE_F32: return launch_skinny<F32>(a, b, c, m, n, k, lda, ldb, ldc, workspace, st);
-        case TL_DTYPE_F16: return launch_skinny<F16>(a, b, c, m, n, k, lda, ldb, ldc, workspace, st);
-        default: return launch_skinny<BF16>(a, b, c, m, n, k, lda, ldb, ldc, workspace, st);
-      }
-    }
-  }
-  switch (dtype) {
-    case TL_DTYPE_F32: return launch_gemm<F32>(a, b, c, m, n, k, lda, ldb, ldc, st);
-    case TL_DTYPE_F16: return launch_gemm<F16>(a, b, c, m, n, k, lda, ldb, ldc, st);
-    default: return launch_gemm<BF16>(a, b, c, m, n, k, lda, ldb, ldc, st);
-  }
+  if (n < 0) return TL_ERR_INVALID;
+  GemmGroups G{};
+  const int st = make_groups(G, 1, &b, &c, &n, &ldb, &ldc);
+  if (st) return st;
+  return gemm_groups(a, G, m, k, lda, workspace, workspace_bytes, dtype, stream);
+}
+
+size_t tl_gemm_grouped_workspace_bytes(int m, int k, int count, const int* n, int dtype) {
+  if (count < 1 || count > kMaxGroups || !n) return 0;
+  GemmGroups G{};
+  G.count = count;
+  for (int g = 0; g < count; ++g) G.n[g] = n[g];
+  return groups_workspace_bytes(m, k, G, dtype);
+}
+
+int tl_gemm_grouped(const void* a, int m, int k, int64_t lda, int count, const void* const* b, void* const* c,
+                    const int* n, const int64_t* ldb, const int64_t* ldc, void* workspace, size_t workspace_bytes,
+                    int dtype, void* stream) {
+  GemmGroups G{};
+  const int st = make_groups(G, count, b, c, n, ldb, ldc);
+  if (st) return st;
+  return gemm_groups(a, G, m, k, lda, workspace, workspace_bytes, dtype, stream);
 }
 
 }  // extern "C"

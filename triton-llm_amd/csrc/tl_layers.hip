@@ -44,8 +44,42 @@ __device__ __forceinline__ float block_sum(float v, float* s_red) {
   return t;
 }
 
-// One workgroup per row.  With b != nullptr the row is a + b, written to h
-// first (the residual for the next add), then normalised from h.
+// One workgroup per row, the row held in registers (VPT elements per
+// thread, element tid + 256 j), so it is read from memory once.  With
+// b != nullptr the row is a + b, written to h (the residual for the next add)
+// and normalised as stored, i.e. after rounding to T, as a separate add then
+// RMSNorm would.  Rows longer than 256 * 32 take rms_norm_kernel below.
+template <typename T, int VPT>
+__global__ __launch_bounds__(kRowThreads) void rms_norm_row_kernel(const void* a, const void* b, void* h, const void* w,
+                                                                   void* y, int n, float eps) {
+  __shared__ float s_red[kRowThreads / 64];
+  const int64_t row = (int64_t)blockIdx.x * n;
+  float x[VPT];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int i = threadIdx.x + kRowThreads * j;
+    float v = 0.f;
+    if (i < n) {
+      v = ld<T>(a, row + i);
+      if (b) {
+        const typename T::bits r = from_f32<T>(v + ld<T>(b, row + i));
+        ((typename T::bits*)h)[row + i] = r;
+        v = to_f32<T>(r);
+      }
+    }
+    x[j] = v;
+    ss += v * v;
+  }
+  const float rms = sqrtf(block_sum(ss, s_red) / (float)n + eps);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int i = threadIdx.x + kRowThreads * j;
+    if (i < n) st<T>(y, row + i, (x[j] / rms) * ld<T>(w, i));
+  }
+}
+
+// Any row length: two passes over the row (the second mostly from L2).
 template <typename T>
 // No __restrict__: callers may update the residual in place (h == a) or
 // normalise in place (y == x); every element is read before it is written by
@@ -106,7 +140,17 @@ int by_dtype(int dtype, Args... args) {
 template <typename T>
 struct RmsLaunch {
   static int run(const void* a, const void* b, void* h, const void* w, void* y, int m, int n, float eps, hipStream_t st) {
-    hipLaunchKernelGGL((rms_norm_kernel<T>), dim3((unsigned)m), dim3(kRowThreads), 0, st, a, b, h, w, y, n, eps);
+    const dim3 grid((unsigned)m), block(kRowThreads);
+    if (n <= kRowThreads * 4)
+      hipLaunchKernelGGL((rms_norm_row_kernel<T, 4>), grid, block, 0, st, a, b, h, w, y, n, eps);
+    else if (n <= kRowThreads * 8)
+      hipLaunchKernelGGL((rms_norm_row_kernel<T, 8>), grid, block, 0, st, a, b, h, w, y, n, eps);
+    else if (n <= kRowThreads * 16)
+      hipLaunchKernelGGL((rms_norm_row_kernel<T, 16>), grid, block, 0, st, a, b, h, w, y, n, eps);
+    else if (n <= kRowThreads * 32)
+      hipLaunchKernelGGL((rms_norm_row_kernel<T, 32>), grid, block, 0, st, a, b, h, w, y, n, eps);
+    else
+      hipLaunchKernelGGL((rms_norm_kernel<T>), grid, block, 0, st, a, b, h, w, y, n, eps);
     return tl_launch_status();
   }
 };

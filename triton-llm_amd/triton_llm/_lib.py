@@ -91,6 +91,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_vp, _vp, _vp, _c_int, _c_int, _c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
          _vp, _c_size, _c_int, _vp],
     ),
+    "tl_gemm_grouped_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, ctypes.POINTER(_c_int), _c_int]),
+    "tl_gemm_grouped": (
+        _c_int,
+        [_vp, _c_int, _c_int, ctypes.c_int64, _c_int, ctypes.POINTER(_vp), ctypes.POINTER(_vp),
+         ctypes.POINTER(_c_int), _i64p, _i64p, _vp, _c_size, _c_int, _vp],
+    ),
     "tl_sample_max_vocab": (_c_int, []),
     "tl_sample_workspace_bytes": (_c_size, [_c_int, _c_int]),
     "tl_sample": (_c_int, [_vp, _c_int, _c_int, _c_i64, _c_float, _c_int, _vp, _vp, _vp, _c_size, _c_int, _vp]),

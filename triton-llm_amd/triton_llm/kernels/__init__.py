@@ -15,7 +15,7 @@ from .attention import attention
 from .attention_gqa import attention_gqa
 from .rope import apply_rope, precompute_cos_sin, precompute_cos_sin_device
 from .flash import flash_attention, flash_attention_strided
-from .gemm import gemm
+from .gemm import gemm, gemm_grouped
 from .rms_norm import add_rms_norm, rms_norm
 from .swiglu import swiglu
 from .add import add
@@ -42,6 +42,7 @@ __all__ = [
     "decode_step",
     "decode_workspace",
     "gemm",
+    "gemm_grouped",
     "rms_norm",
     "add_rms_norm",
     "swiglu",
