@@ -78,7 +78,7 @@ def test_gemm_lm_head_shapes(dtype, M, K, N):
     c_dev = H.upload(on.to_storage(pad, dtype), dtype)
     a_dev, b_dev = H.upload(a, dtype), H.upload(b, dtype)
     nws = lib.tl_gemm_workspace_bytes(M, N, K, code)
-    ws = gpu.allocate((max(nws, 1),), np.uint8)
+    ws = gpu.zeros((max(nws, 1),), np.uint8)
     assert lib.tl_gemm(a_dev.ptr, b_dev.ptr, c_dev.ptr, M, N, K, K, N, ldc, ws.ptr, nws, code, None) == 0
     c = on.from_storage(H.download(c_dev), dtype)
     np.testing.assert_allclose(c[:, :N], exp, atol=tol[0], rtol=tol[1])
@@ -207,3 +207,22 @@ def test_gemm_grouped_matches_each_product(dtype, M, K, Ns):
             assert err <= 2e-3
         else:
             np.testing.assert_allclose(got, exp, rtol=8e-3, atol=1e-2)
+
+
+def test_gemm_few_rows_mixed_shapes_share_workspace():
+    """Few-row products of different tilings, one after another and repeated,
+    through the one module-wide workspace: each comes out right whatever ran
+    before it."""
+    rng = np.random.default_rng(5)
+    shapes = [(1, 3072, 5120), (4, 8192, 3072), (1, 3072, 5120), (2, 3072, 16384), (8, 1000, 100), (1, 8192, 3072)]
+    cases = []
+    for M, K, N in shapes:
+        a = rng.standard_normal((M, K), dtype=np.float32)
+        b = (rng.standard_normal((K, N), dtype=np.float32) / np.sqrt(K)).astype(np.float32)
+        cases.append((gpu.to_device(a), gpu.to_device(b), gemm_ref(a, b)))
+    for rep in range(3):
+        outs = [gemm(a, b) for a, b, _ in cases]
+        for (M, K, N), out, (_, _, exp) in zip(shapes, outs, cases):
+            err = H.max_abs(out.to_numpy(), exp)
+            H.report(f"mixed shapes rep {rep} {M}x{K}@{K}x{N}", err, 2e-3)
+            assert err <= 2e-3

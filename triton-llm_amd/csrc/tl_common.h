@@ -35,11 +35,13 @@ struct F16 {
   using bits = uint16_t;
   static constexpr int code = TL_DTYPE_F16;
   static constexpr int size = 2;
+  static constexpr uint32_t one_pair = 0x3C003C00u;  // two 1.0 values in one word
 };
 struct BF16 {
   using bits = uint16_t;
   static constexpr int code = TL_DTYPE_BF16;
   static constexpr int size = 2;
+  static constexpr uint32_t one_pair = 0x3F803F80u;  // two 1.0 values in one word
 };
 
 // ---- scalar conversions -------------------------------------------------

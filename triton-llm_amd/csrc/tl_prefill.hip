@@ -102,8 +102,12 @@ __device__ __forceinline__ void decode_block(const FlashParams& p, int& b, int& 
 // buffers each for K and V^T (128 KiB at d_k 128).
 //
 // S^T accumulators are seeded with -m_run (Q is pre-scaled by
-// sm_scale * log2 e), so P = exp2(S) directly; the row sum is kept in fp32
-// per lane (v_dot2 would not co-execute with the other wave's MFMAs).  The
+// sm_scale * log2 e), so P = exp2(S) directly.  The row sum: at d_k 128
+// (MFMA-bound) it is kept in fp32 per lane with VALU adds (v_dot2 would not
+// co-execute with the other wave's MFMAs); at d_k 64 the softmax VALU work is
+// the limit and the MFMA pipe has slack, so the row sum is one more MFMA per
+// 16 keys, ones . P^T, in the G phase -- the sum of the rounded P that the
+// PV product uses.  The
 // running offset m_run is raised (and O rescaled) only when a tile's max
 // exceeds it by more than kRescaleLog2 (log2 units), which bounds P by
 // 2^kRescaleLog2.
@@ -316,6 +320,10 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
   frag qf[NKS];  // Q pre-scaled by sm_scale * log2 e
   f32x16 o_acc[NDB];
   float m_run, l4[4];
+  constexpr bool kMfmaRowSum = D == 64;  // row sums on the matrix cores
+  f32x16 l_acc;                           // every register: the lane's row sum
+  const frag ones = __builtin_bit_cast(
+      frag, u32x4{T::one_pair, T::one_pair, T::one_pair, T::one_pair});
   bool fresh;
   f32x16 s_init;
   f32x16 s[NMB];      // S_t (relative scores)
@@ -389,6 +397,8 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
     fresh = true;
 #pragma unroll
     for (int k = 0; k < 4; ++k) l4[k] = 0.f;
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) l_acc[rr] = 0.f;
 
     // G(t): job g = PV job g of tile t-1 (keys 16 (g / NDB).., d-block
     // g % NDB; none for t = 0) and S job g of tile t.  S jobs fill key blocks
@@ -456,6 +466,9 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
         if constexpr (DO_PV) {
           const int tt = g / NDB, db = g % NDB;
           o_acc[db] = M::mma(__builtin_bit_cast(frag, vfr[g]), __builtin_bit_cast(frag, pw[tt]), o_acc[db]);
+          if constexpr (kMfmaRowSum) {
+            if (db == 0) l_acc = M::mma(ones, __builtin_bit_cast(frag, pw[tt]), l_acc);
+          }
         }
         if constexpr (DO_S) {
           const int ks = s_ks(g), mb = s_mb(g);
@@ -522,6 +535,10 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
         fresh = fresh && (mx == -INFINITY);
 #pragma unroll
         for (int k = 0; k < 4; ++k) l4[k] *= alpha;
+        if constexpr (kMfmaRowSum) {
+#pragma unroll
+          for (int rr = 0; rr < 16; ++rr) l_acc[rr] *= alpha;
+        }
 #pragma unroll
         for (int i = 0; i < NDB; ++i)
 #pragma unroll
@@ -542,7 +559,7 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
           float pr2[2] = {fast_exp2(s[tt >> 1][8 * (tt & 1) + 2 * j2]),
                           fast_exp2(s[tt >> 1][8 * (tt & 1) + 2 * j2 + 1])};
           pw[tt][j2] = pack2<T>(pr2);
-          l4[j2] += pr2[0] + pr2[1];
+          if constexpr (!kMfmaRowSum) l4[j2] += pr2[0] + pr2[1];
         }
       __builtin_amdgcn_sched_barrier(0);
     };
@@ -593,7 +610,7 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
     //    and stores them row-contiguously (16 lanes per 256-byte row), so each
     //    store instruction writes whole cache lines.  The stores are not
     //    waited for here.
-    const float inv = 1.f / sum_xor32((l4[0] + l4[1]) + (l4[2] + l4[3]));
+    const float inv = kMfmaRowSum ? 1.f / l_acc[0] : 1.f / sum_xor32((l4[0] + l4[1]) + (l4[2] + l4[3]));
     const int ntb = (tb + n_kt + 1) & 1;  // where the next K_0 went
     const Tile nxt = make_tile(has_next ? nrank : rank);
     // the next Q rows: group 0's in K buffer (tb + n_kt) & 1, group 1's in
@@ -831,36 +848,68 @@ __global__ __launch_bounds__(kThreads, D == 128 ? 1 : 2) void flash_fwd_f32(Flas
 //     position 16 u + 8 h + j  <-  key 16 u + 8 (j / 4) + 4 h + (j % 4)
 // which is the key order of the PV MFMA's k-index for lane half h (the S^T
 // accumulator layout puts keys 8 a + 4 h + b, b < 4, in lane half h), so a
-// lane's 8 keys are contiguous.  One workgroup per (64-key tile, kv head, b).
+// lane's 8 keys are contiguous.
+//
+// Tiles of 64 keys of one (b, kv head), numbered key tile fastest; workgroup
+// w takes tiles w, w + gridDim.x, ...  A tile goes global -> registers ->
+// LDS -> (transposed) global; the next tile's loads are issued before the
+// current one is transposed, and the two LDS buffers alternate, so each
+// workgroup keeps a tile of loads in flight (the copy is otherwise bound by
+// load latency, one tile per workgroup).  In LDS the 16-byte chunk c of key
+// row r sits at slot c ^ f(r), f(r) = ((r >> 4) & 3) | (((r >> 2) & 1) << 2):
+// the 8 keys one transposing read instruction covers (16 u + 4 h + const)
+// then fall in 8 different slots, 32 distinct banks for 64 lanes.
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(256) void vt_pack_kernel(const uint16_t* __restrict__ v,
                                                       uint16_t* __restrict__ vt, int seq_k,
-                                                      int sk_pad, int n_kv, int64_t v_sb,
+                                                      int sk_pad, int n_kv, int n_tiles, int64_t v_sb,
                                                       int64_t v_sh, int64_t v_ss) {
-  constexpr int TROW = D + 8;  // LDS row (elements), 16-byte aligned
-  __shared__ __attribute__((aligned(16))) uint16_t tile[64 * TROW];
-  const int kt = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z;
-  const uint16_t* src = v + b * v_sb + hkv * v_sh;
-  for (int c = threadIdx.x; c < 64 * D / 8; c += 256) {
-    const int r = c / (D / 8), col = c % (D / 8);
-    const int key = kt * 64 + r;
-    u32x4 val = {0u, 0u, 0u, 0u};
-    if (key < seq_k) val = *(const u32x4*)(src + (int64_t)key * v_ss + col * 8);
-    *(u32x4*)(tile + r * TROW + col * 8) = val;
-  }
-  __syncthreads();
-  uint16_t* dst = vt + ((int64_t)b * n_kv + hkv) * D * sk_pad + kt * 64;
-  for (int c = threadIdx.x; c < D * 8; c += 256) {
-    const int d = c / 8, ch = c % 8;
-    const int u = ch >> 1, h = ch & 1;
-    uint32_t w[4];
+  constexpr int PER = 64 * D / 8 / 256;  // 16-byte chunks each thread loads per tile
+  constexpr int CPR = D / 8;             // chunks per key row
+  __shared__ __attribute__((aligned(16))) uint16_t tile[2][64 * D];
+  const int kts = sk_pad / 64;
+  auto swz = [](int r) { return ((r >> 4) & 3) | (((r >> 2) & 1) << 2); };
+  auto load = [&](int t, u32x4 (&val)[PER]) {
+    const int kt = t % kts, bh = t / kts;
+    const uint16_t* src = v + (bh / n_kv) * v_sb + (bh % n_kv) * v_sh;
 #pragma unroll
-    for (int j = 0; j < 8; j += 2) {
-      const int k0 = 16 * u + 8 * (j / 4) + 4 * h + (j % 4);
-      w[j / 2] = (uint32_t)tile[k0 * TROW + d] | ((uint32_t)tile[(k0 + 1) * TROW + d] << 16);
+    for (int i = 0; i < PER; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      const int r = c / CPR, col = c % CPR;
+      const int key = kt * 64 + r;
+      val[i] = key < seq_k ? *(const u32x4*)(src + (int64_t)key * v_ss + col * 8) : u32x4{0u, 0u, 0u, 0u};
     }
-    *(u32x4*)(dst + (int64_t)d * sk_pad + ch * 8) = u32x4{w[0], w[1], w[2], w[3]};
+  };
+  u32x4 val[PER];
+  int t = blockIdx.x;
+  if (t >= n_tiles) return;
+  load(t, val);
+  for (int buf = 0; t < n_tiles; t += gridDim.x, buf ^= 1) {
+    uint16_t* tl = tile[buf];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      const int r = c / CPR, col = c % CPR;
+      *(u32x4*)(tl + r * D + ((col ^ swz(r)) << 3)) = val[i];
+    }
+    if (t + (int)gridDim.x < n_tiles) load(t + gridDim.x, val);
+    __syncthreads();
+    const int kt = t % kts, bh = t / kts;
+    uint16_t* dst = vt + (int64_t)bh * D * sk_pad + kt * 64;
+    for (int c = threadIdx.x; c < D * 8; c += 256) {
+      const int d = c / 8, ch = c % 8;
+      const int u = ch >> 1, h = ch & 1;
+      uint32_t w[4];
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        const int k0 = 16 * u + 8 * (j / 4) + 4 * h + (j % 4);
+        const int e0 = k0 * D + (((d >> 3) ^ swz(k0)) << 3) + (d & 7);
+        const int e1 = (k0 + 1) * D + (((d >> 3) ^ swz(k0 + 1)) << 3) + (d & 7);
+        w[j / 2] = (uint32_t)tl[e0] | ((uint32_t)tl[e1] << 16);
+      }
+      *(u32x4*)(dst + (int64_t)d * sk_pad + ch * 8) = u32x4{w[0], w[1], w[2], w[3]};
+    }
   }
 }
 
@@ -953,9 +1002,10 @@ int launch_flash_16(FlashParams& p, void* ws, bool causal, hipStream_t st) {
   p.q_machines = min((tl_device_cus() + p.n_queues - 1) / p.n_queues, p.q_tiles);
   const int rounds = p.q_tiles / p.q_machines;
   p.q_triple = (p.q_tiles % p.q_machines == 0 && rounds % 2 == 1 && rounds >= 3 && p.q_machines % 2 == 0) ? 1 : 0;
-  dim3 tg(p.sk_pad / 64, p.n_kv, p.batch);
-  hipLaunchKernelGGL(vt_pack_kernel<D>, tg, dim3(256), 0, st, (const uint16_t*)p.v, (uint16_t*)ws,
-                     p.seq_k, p.sk_pad, p.n_kv, p.v_sb, p.v_sh, p.v_ss);
+  const int vt_tiles = p.sk_pad / 64 * p.n_kv * p.batch;
+  const int vt_grid = min(vt_tiles, 2 * tl_device_cus());
+  hipLaunchKernelGGL(vt_pack_kernel<D>, dim3(vt_grid), dim3(256), 0, st, (const uint16_t*)p.v, (uint16_t*)ws,
+                     p.seq_k, p.sk_pad, p.n_kv, vt_tiles, p.v_sb, p.v_sh, p.v_ss);
   int e = tl_launch_status();
   if (e) return e;
   dim3 grid((unsigned)(p.q_machines * p.n_queues));
