@@ -555,6 +555,39 @@ def copy_probe(mib):
 SAMPLE_MODES = {"greedy": (0.0, 0), "t0.8": (0.8, 0), "t0.8_k50": (0.8, 50)}
 
 
+def bench_gemm_case(model, dt, M, steps):
+    """One GEMM layer case only, for rocprofv3: ``steps`` grouped one-layer
+    projection passes (gemm_grouped q/k/v, gemm o, gemm_grouped gate/up, gemm
+    down) of ``model`` in ``dt`` at M rows, weights rotated over >= 1 GB of
+    copies for M = 1 as in bench_gemm."""
+    from triton_llm import gpu
+    from triton_llm.kernels import gemm, gemm_grouped
+
+    e, q, kv, inter = GEMM_MODELS[model]
+    shapes = {"q": (e, q), "k": (e, kv), "v": (e, kv), "o": (q, e), "gate": (e, inter), "up": (e, inter),
+              "down": (inter, e)}
+    gdt, esz = (np.float32, 4) if dt == "float32" else (gpu.bfloat16, 2)
+    rng = np.random.default_rng(0)
+
+    def host(shape):
+        x = rng.standard_normal(shape, dtype=np.float32)
+        return (x.view(np.uint32) >> 16).astype(np.uint16) if dt == "bfloat16" else x
+
+    layer_w = sum(K * N for K, N in shapes.values()) * esz
+    reps = max(1, int(np.ceil(1e9 / layer_w))) if M == 1 else 1
+    W = [{name: gpu.to_device(host(shape), gdt) for name, shape in shapes.items()} for _ in range(reps)]
+    x = {d: gpu.to_device(host((M, d)), gdt) for d in {e, q, inter}}
+    out = {name: gpu.allocate((M, N), gdt) for name, (K, N) in shapes.items()}
+    for i in range(steps):
+        w = W[i % reps]
+        gemm_grouped(x[e], [w["q"], w["k"], w["v"]], [out["q"], out["k"], out["v"]])
+        gemm(x[q], w["o"], out_dev=out["o"])
+        gemm_grouped(x[e], [w["gate"], w["up"]], [out["gate"], out["up"]])
+        gemm(x[inter], w["down"], out_dev=out["down"])
+    gpu.synchronize()
+    log(f"gemm case {model} {dt} M={M}: {steps} grouped layers")
+
+
 def bench_sample_case(vocab, rows, mode, steps):
     """One sampling case only, for rocprofv3: ``steps`` calls of
     sample_rows on fp32 logits (rows, vocab)."""
@@ -658,6 +691,9 @@ def main():
     ap.add_argument("--sample-case", default="",
                     help="VOCAB,ROWS,MODE (mode: greedy, t0.8, t0.8_k50): run only --steps calls "
                          "of that sampling case (for rocprofv3) and exit")
+    ap.add_argument("--gemm-case", default="",
+                    help="MODEL,DTYPE,M (e.g. llama3.2-3b,float32,1): run only --steps grouped "
+                         "projection layers of that case (for rocprofv3) and exit")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="only run 5 device-to-device copies of this many MiB (the known-size "
                          "reference for calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -681,6 +717,10 @@ def main():
     if args.sample_case:
         vocab, rows, mode = args.sample_case.split(",")
         bench_sample_case(int(vocab), int(rows), mode, args.steps)
+        return
+    if args.gemm_case:
+        model, dt, m = args.gemm_case.split(",")
+        bench_gemm_case(model, dt, int(m), args.steps)
         return
     if args.sample:
         print(json.dumps(bench_sample(min(args.steps, 50), min(args.warmup, 5), cpu=cpu)))
