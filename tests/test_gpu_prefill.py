@@ -141,13 +141,16 @@ def test_prefill_reads_cache_layout_and_seq_major_rows():
     (24, 1536, 256, 16, 8, True),    # bottom-right causal: tiles with no visible key between others
     (8, 768, 768, 6, 2, True),       # 2 (batch, kv) units: one list, 3 workgroups
 ])
-def test_prefill_persistent_schedules(monkeypatch, cus, seq_q, seq_k, n_head, n_kv, causal):
+@pytest.mark.parametrize("d_k", [64, 128])
+def test_prefill_persistent_schedules(monkeypatch, cus, seq_q, seq_k, n_head, n_kv, causal, d_k):
     """The persistent kernel walks several query tiles per workgroup (forced by capping the CU
-    count), switching tiles with prefetched Q / K and, after a tile with no visible key, cold."""
+    count), switching tiles with prefetched Q / K and, after a tile with no visible key, cold;
+    d_k 64 and 128 (different LDS tile sizes and load slots)."""
     monkeypatch.setenv("TRITON_LLM_HIP_MAX_CUS", str(cus))
-    dtype, d_k = "bfloat16", 128
+    dtype = "bfloat16"
     cfg = oi.Config("sched", "prefill", dtype, 1, n_head, n_kv, d_k, 77, 1 / np.sqrt(d_k), seq=seq_q)
-    print(f"[case] persistent cus={cus} sq={seq_q} sk={seq_k} Hq={n_head} Hkv={n_kv} causal={causal}", flush=True)
+    print(f"[case] persistent cus={cus} sq={seq_q} sk={seq_k} Hq={n_head} Hkv={n_kv} causal={causal} "
+          f"d_k={d_k}", flush=True)
     rng = np.random.default_rng(cus + seq_q + seq_k)
     q = on.to_storage(rng.standard_normal((1, n_head, seq_q, d_k), dtype=np.float32), dtype)
     k = on.to_storage(rng.standard_normal((1, n_kv, seq_k, d_k), dtype=np.float32), dtype)
