@@ -72,3 +72,45 @@ def test_graph_replays_prefill():
         g.replay()
         np.testing.assert_array_equal(H.download(out), want, err_msg=f"replay {rep}")
         _eager_noise()
+
+
+def test_recorded_and_captured_launches_keep_their_workspace():
+    """A recorded launcher and a captured graph hold raw pointers to the shared
+    few-row GEMM workspace.  A later, larger product grows (replaces) that
+    workspace; the old buffer must stay with the launcher / graph, so their
+    replays still compute the right product and do not write into memory the
+    larger product's call now uses."""
+    from oracle.gemm import gemm_ref
+    from triton_llm.kernels import gemm
+    from triton_llm.kernels._common import record, shared_workspace
+
+    rng = np.random.default_rng(8)
+    print("[case] workspace keep-alive: launcher and graph, then a growing gemm", flush=True)
+    a = rng.standard_normal((1, 3072), dtype=np.float32)
+    b = (rng.standard_normal((3072, 1024), dtype=np.float32) / 64).astype(np.float32)
+    a_d, b_d = gpu.to_device(a), gpu.to_device(b)
+    out_l = gpu.allocate((1, 1024), np.float32)
+    out_g = gpu.allocate((1, 1024), np.float32)
+    gemm(a_d, b_d, out_dev=out_l)  # warm
+    launcher = record(lambda: gemm(a_d, b_d, out_dev=out_l))
+    with gpu.capture() as g:
+        gemm(a_d, b_d, out_dev=out_g)
+    before = shared_workspace("gemm", 1).ptr.value
+    # a product whose split-K partials need far more workspace: the shared
+    # buffer is replaced by a larger one
+    big_a = rng.standard_normal((8, 8192), dtype=np.float32)
+    big_b = (rng.standard_normal((8192, 16384), dtype=np.float32) / 90).astype(np.float32)
+    big_a_d, big_b_d = gpu.to_device(big_a), gpu.to_device(big_b)
+    big_out = gemm(big_a_d, big_b_d)
+    assert shared_workspace("gemm", 1).ptr.value != before, "the workspace did not grow"
+    exp = gemm_ref(a, b)
+    for rep in range(3):
+        launcher()
+        g.replay()
+        big_out2 = gemm(big_a_d, big_b_d)
+        gpu.synchronize()
+        for name, t in (("launcher", out_l), ("graph", out_g)):
+            err = H.max_abs(t.to_numpy(), exp)
+            H.report(f"keep-alive {name} rep {rep}", err, 2e-3)
+            assert err <= 2e-3
+        np.testing.assert_array_equal(big_out2.to_numpy(), big_out.to_numpy())

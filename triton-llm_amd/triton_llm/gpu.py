@@ -217,6 +217,20 @@ class DeviceTensor:
         return int(np.prod(self.shape)) if self.shape else 1
 
 
+# Keep-alive lists of the active graph captures and launcher recordings
+# (kernels._common.record): a recorded launch holds raw pointers, so every
+# buffer allocated or handed out as a shared workspace while one is active is
+# held by it until the graph or launcher itself is dropped; otherwise a freed
+# buffer could be reused while a replay still writes into it.
+_keepers: list[list] = []
+
+
+def keep_alive(obj) -> None:
+    """Hold ``obj`` for every active capture / launcher recording."""
+    for k in _keepers:
+        k.append(obj)
+
+
 def allocate(shape, dtype=np.float32):
     """Allocate (uninitialised) memory on the GPU: a cached block of the same
     rounded size if one is free, else ``hipMalloc``."""
@@ -228,14 +242,18 @@ def allocate(shape, dtype=np.float32):
     size = _block_size(nbytes)
     addr = _take_block(size)
     if addr is not None:
-        return DeviceTensor(ctypes.c_void_p(addr), shape, dtype, nbytes)
-    ptr = ctypes.c_void_p()
-    err = _rt.tl_malloc(ctypes.byref(ptr), size)
-    if err != CUDA_SUCCESS and _pool_bytes:
-        empty_cache()  # out of memory with blocks cached: give them back, try once more
+        t = DeviceTensor(ctypes.c_void_p(addr), shape, dtype, nbytes)
+    else:
+        ptr = ctypes.c_void_p()
         err = _rt.tl_malloc(ctypes.byref(ptr), size)
-    check_error(err)
-    return DeviceTensor(ptr, shape, dtype, nbytes)
+        if err != CUDA_SUCCESS and _pool_bytes:
+            empty_cache()  # out of memory with blocks cached: give them back, try once more
+            err = _rt.tl_malloc(ctypes.byref(ptr), size)
+        check_error(err)
+        t = DeviceTensor(ptr, shape, dtype, nbytes)
+    if _keepers:
+        keep_alive(t)
+    return t
 
 
 def zeros(shape, dtype=np.float32):
@@ -287,10 +305,12 @@ def view(tensor: DeviceTensor, new_shape: tuple) -> DeviceTensor:
 class Graph:
     """An executable HIP graph recorded by :func:`capture`; ``replay()``
     runs the recorded launches again on the library stream (same pointers,
-    same sizes).  No sync."""
+    same sizes).  No sync.  Holds every buffer allocated, or handed out as a
+    shared workspace, during the capture."""
 
     def __init__(self):
         self.exec = ctypes.c_void_p()
+        self.keep: list = []
 
     def replay(self):
         _initialize()
@@ -318,9 +338,11 @@ class capture:
         _initialize()
         self.graph = Graph()
         check_error(_rt.tl_graph_capture_begin(None))
+        _keepers.append(self.graph.keep)
         return self.graph
 
     def __exit__(self, exc_type, exc, tb):
+        _keepers.remove(self.graph.keep)
         err = _rt.tl_graph_capture_end(None, ctypes.byref(self.graph.exec))
         if exc_type is None:
             check_error(err)

@@ -44,12 +44,13 @@ def launch(fn, *args, what: str) -> None:
 class Launcher:
     """The C-ABI launches one wrapper call made, replayed with the same
     arguments: no Python validation, no shape logic, one ctypes call per
-    kernel launch.  Valid while every buffer the call used is alive and
-    unmoved (pass explicit workspaces and outputs to the recorded call)."""
+    kernel launch.  It holds the recorded call's result and every buffer
+    allocated or handed out as a shared workspace while recording; buffers
+    the caller passed in must stay alive as long as the launcher is used."""
 
     def __init__(self, calls, keep):
         self.calls = calls
-        self._keep = keep  # the recorded call's result (e.g. an output it allocated)
+        self._keep = keep  # the call's result and the buffers it used
 
     def __call__(self) -> None:
         for fn, args, what in self.calls:
@@ -63,12 +64,15 @@ def record(thunk) -> Launcher:
     launches; returns a :class:`Launcher` that issues them."""
     global _recording
     prev, _recording = _recording, []
+    held: list = []
+    gpu._keepers.append(held)
     try:
-        keep = thunk()
+        result = thunk()
         calls = _recording
     finally:
         _recording = prev
-    return Launcher(calls, keep)
+        gpu._keepers.remove(held)
+    return Launcher(calls, (result, held))
 
 
 def same_dtype(*tensors) -> int:
@@ -124,4 +128,5 @@ def shared_workspace(key: str, nbytes: int):
         _shared.pop(key, None)
         ws = gpu.allocate((size,), np.uint8)
         _shared[key] = ws
+    gpu.keep_alive(ws)  # a recorded launch using it outlives a later growth
     return ws

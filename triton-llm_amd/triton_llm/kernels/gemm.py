@@ -12,26 +12,16 @@ matrix cores with a hand-written MFMA kernel.
 
 from __future__ import annotations
 
-import numpy as np
-
 import ctypes
 
 from triton_llm import gpu
-from ._common import launch, same_dtype, vp
+from ._common import launch, same_dtype, shared_workspace, vp
 
 # Workspace of the few-row path, kept across calls and grown on demand: every
 # call runs on the library stream, so consecutive calls are ordered and may
 # share it (hipMalloc per call would cost more than the product).
-_shared_ws: "gpu.DeviceTensor | None" = None
-
-
 def _workspace(nbytes: int):
-    global _shared_ws
-    if nbytes == 0:
-        return None
-    if _shared_ws is None or _shared_ws.nbytes < nbytes:
-        _shared_ws = gpu.allocate((max(nbytes, 1 << 20),), np.uint8)
-    return _shared_ws
+    return shared_workspace("gemm", nbytes)
 
 
 def gemm(h_dev: "gpu.DeviceTensor", w_dev: "gpu.DeviceTensor",
