@@ -74,7 +74,8 @@ int tl_event_elapsed_ms(float* ms, void* start, void* stop);
  * starts recording `stream` (NULL: the library stream); every tl_* launch
  * and device-to-device copy issued to it until tl_graph_capture_end is
  * recorded, not run.  Calls that synchronise (tl_memcpy_htod / _dtoh,
- * tl_synchronize) and tl_memset must not be issued while recording.
+ * tl_synchronize) must not be issued while recording; tl_memset (a fill
+ * kernel on the library stream) may.
  * tl_graph_capture_end returns an executable graph; tl_graph_launch replays
  * it on a stream with the pointers and sizes it was recorded with.  A
  * decode step of a serving loop is a few small kernels whose host launch

@@ -9,6 +9,7 @@ bar is allclose(rtol 1e-2, atol 5e-2)); 16-bit outputs within their
 rounding, rtol 8e-3 + atol 1e-2.
 """
 
+import ctypes
 import time
 
 import numpy as np
@@ -226,3 +227,29 @@ def test_gemm_few_rows_mixed_shapes_share_workspace():
             err = H.max_abs(out.to_numpy(), exp)
             H.report(f"mixed shapes rep {rep} {M}x{K}@{K}x{N}", err, 2e-3)
             assert err <= 2e-3
+
+
+def test_gemm_zero_k_strided_output_keeps_padding():
+    """K = 0 writes zeros into the (M, N) view only: a strided C (ldc > N)
+    keeps its padding columns, through the C ABI, for the single and the
+    grouped entry points."""
+    lib = gpu.runtime()
+    M, N, ldc = 5, 40, 56
+    print("[case] gemm K=0 strided", flush=True)
+    c_dev = gpu.to_device(np.full((M, ldc), 7.0, np.float32))
+    a_dev = gpu.allocate((M, 1), np.float32)
+    b_dev = gpu.allocate((1, N), np.float32)
+    assert lib.tl_gemm(a_dev.ptr, b_dev.ptr, c_dev.ptr, M, N, 0, 1, N, ldc, None, 0, 0, None) == 0
+    c = c_dev.to_numpy()
+    assert not c[:, :N].any() and (c[:, N:] == 7.0).all()
+    c2 = gpu.to_device(np.full((M, ldc), 7.0, np.float32))
+    ns = (ctypes.c_int * 2)(N, 8)
+    bs = (ctypes.c_void_p * 2)(b_dev.ptr.value, b_dev.ptr.value)
+    cs = (ctypes.c_void_p * 2)(c_dev.ptr.value, c2.ptr.value)
+    lds_b = (ctypes.c_int64 * 2)(N, 8)
+    lds_c = (ctypes.c_int64 * 2)(ldc, ldc)
+    c_dev.from_numpy(np.full((M, ldc), 7.0, np.float32))
+    assert lib.tl_gemm_grouped(a_dev.ptr, M, 0, 1, 2, bs, cs, ns, lds_b, lds_c, None, 0, 0, None) == 0
+    c, c2h = c_dev.to_numpy(), c2.to_numpy()
+    assert not c[:, :N].any() and (c[:, N:] == 7.0).all()
+    assert not c2h[:, :8].any() and (c2h[:, 8:] == 7.0).all()

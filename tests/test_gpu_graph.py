@@ -3,6 +3,8 @@ step and a recorded prefill call, replayed several times with eager work
 and synchronisation between the replays, give exactly the eager result every
 time (the kernels are deterministic, so bit-equal)."""
 
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -114,3 +116,38 @@ def test_recorded_and_captured_launches_keep_their_workspace():
             H.report(f"keep-alive {name} rep {rep}", err, 2e-3)
             assert err <= 2e-3
         np.testing.assert_array_equal(big_out2.to_numpy(), big_out.to_numpy())
+
+
+def test_memset_fills_bytes_at_any_alignment():
+    """tl_memset is a fill kernel (16-byte stores over the aligned middle,
+    single bytes for an unaligned head and tail): every offset and length
+    sets exactly its bytes."""
+    rt = gpu.runtime()
+    base = gpu.allocate((4096,), np.uint8)
+    print("[case] memset offsets/lengths", flush=True)
+    for off in (0, 1, 3, 15, 16, 17):
+        for n in (1, 7, 15, 16, 17, 100, 1000, 3000):
+            base.from_numpy(np.zeros(4096, np.uint8))
+            ptr = ctypes.c_void_p(base.ptr.value + off)
+            assert rt.tl_memset(ptr, 0xAB, n) == 0
+            got = base.to_numpy()
+            exp = np.zeros(4096, np.uint8)
+            exp[off:off + n] = 0xAB
+            np.testing.assert_array_equal(got, exp, err_msg=f"offset {off} length {n}")
+
+
+def test_graph_replays_fill():
+    """A fill recorded in a graph is a kernel node: each replay zeroes the
+    buffer again after eager work dirtied it."""
+    rt = gpu.runtime()
+    buf = gpu.allocate((1 << 16,), np.float32)
+    ones = np.ones(1 << 16, np.float32)
+    print("[case] graph fill", flush=True)
+    buf.from_numpy(ones)
+    with gpu.capture() as g:
+        assert rt.tl_memset(buf.ptr, 0, buf.nbytes) == 0
+    for rep in range(3):
+        buf.from_numpy(ones)
+        g.replay()
+        assert not buf.to_numpy().any(), f"replay {rep}"
+        _eager_noise()

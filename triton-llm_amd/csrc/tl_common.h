@@ -130,6 +130,10 @@ static inline int tl_launch_status() { return (int)hipGetLastError(); }
 // Resolve the stream argument of an entry point: NULL means the library stream.
 hipStream_t tl_resolve_stream(void* stream);
 
+// Fill nbytes at dst with value on stream st by a kernel (capturable in a
+// HIP graph as a kernel node).
+int tl_fill_bytes(void* dst, unsigned char value, size_t nbytes, hipStream_t st);
+
 // Compute units of the current device (cached per device), capped by the
 // environment variable TRITON_LLM_HIP_MAX_CUS when set (tests use it to force
 // multi-round schedules on small problems).

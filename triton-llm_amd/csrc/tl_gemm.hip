@@ -669,9 +669,16 @@ int gemm_groups(const void* a, const GemmGroups& G, int m, int k, int64_t lda, v
   if (live.count == 0) return 0;
   if (k == 0) {  // empty sum: zeros, row by row when C is a strided view
     for (int g = 0; g < live.count; ++g) {
-      const hipError_t e = hipMemset2DAsync(live.c[g], (size_t)live.ldc[g] * esize, 0, (size_t)live.n[g] * esize,
-                                            (size_t)m, st);
-      if (e != hipSuccess) return (int)e;
+      if (live.ldc[g] == live.n[g]) {
+        const int e = tl_fill_bytes(live.c[g], 0, (size_t)m * live.n[g] * esize, st);
+        if (e) return e;
+        continue;
+      }
+      for (int r = 0; r < m; ++r) {
+        const int e = tl_fill_bytes((char*)live.c[g] + (size_t)r * live.ldc[g] * esize, 0,
+                                    (size_t)live.n[g] * esize, st);
+        if (e) return e;
+      }
     }
     return 0;
   }

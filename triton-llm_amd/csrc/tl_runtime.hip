@@ -9,7 +9,34 @@
 namespace {
 hipStream_t g_stream = nullptr;
 int g_device = -1;
+
+// Byte fill: 16-byte stores over the aligned middle, single bytes for the
+// unaligned head and tail (at most 15 each, taken by the first threads).
+__global__ __launch_bounds__(256) void fill_bytes_kernel(unsigned char* dst, unsigned char v, size_t n) {
+  const size_t head = min(n, (size_t)((16 - ((uintptr_t)dst & 15)) & 15));
+  const size_t words = (n - head) / 16;
+  const size_t tail = head + words * 16;
+  const uint32_t w = 0x01010101u * v;
+  const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  u32x4* body = (u32x4*)(dst + head);
+  for (size_t i = tid; i < words; i += stride) body[i] = u32x4{w, w, w, w};
+  if (tid < head) dst[tid] = v;
+  if (tid < n - tail) dst[tail + tid] = v;
+}
 }  // namespace
+
+// A kernel, not hipMemsetAsync, so that a fill issued while a caller records
+// a HIP graph becomes a kernel node (memset nodes have replayed wrongly).
+int tl_fill_bytes(void* dst, unsigned char value, size_t nbytes, hipStream_t st) {
+  if (nbytes == 0) return 0;
+  const size_t words = nbytes / 16 + 1;
+  size_t blocks = (words + 255) / 256;
+  blocks = blocks < 4096 ? blocks : 4096;
+  hipLaunchKernelGGL(fill_bytes_kernel, dim3((unsigned)blocks), dim3(256), 0, st, (unsigned char*)dst, value,
+                     nbytes);
+  return tl_launch_status();
+}
 
 hipStream_t tl_resolve_stream(void* stream) {
   return stream ? (hipStream_t)stream : g_stream;
@@ -100,7 +127,7 @@ int tl_memcpy_dtod(void* dst, const void* src, size_t nbytes) {
 int tl_memset(void* dst, int value, size_t nbytes) {
   if (nbytes == 0) return 0;
   if (!dst) return TL_ERR_INVALID;
-  return (int)hipMemsetAsync(dst, value, nbytes, g_stream);
+  return tl_fill_bytes(dst, (unsigned char)value, nbytes, g_stream);
 }
 
 int tl_synchronize(void) {

@@ -257,7 +257,7 @@ def allocate(shape, dtype=np.float32):
 
 
 def zeros(shape, dtype=np.float32):
-    """Allocate and zero-fill (stream-ordered memset)."""
+    """Allocate and zero-fill (a stream-ordered fill kernel)."""
     t = allocate(shape, dtype)
     if t.nbytes:
         check_error(_rt.tl_memset(t.ptr, 0, t.nbytes))
@@ -329,10 +329,10 @@ class Graph:
 class capture:
     """``with gpu.capture() as g: <launches>`` records the launches on the
     library stream into ``g`` instead of running them; ``g.replay()`` runs
-    them.  Inside, only stream-ordered launches and device copies are
-    legal: no host copies, no synchronize, no memset.  Allocations are
-    legal but are not recorded, so make them (or warm the block cache)
-    before capturing."""
+    them.  Inside, only stream-ordered launches, device copies and fills
+    (``zeros``, ``tl_memset``: a fill kernel) are legal: no host copies, no
+    synchronize.  Allocations are legal but are not recorded, so make them
+    (or warm the block cache) before capturing."""
 
     def __enter__(self) -> Graph:
         _initialize()
