@@ -163,3 +163,29 @@ def test_kv_cache_rejects_positions_past_the_rope_table(recording):
     with pytest.raises(ValueError, match=r"position_offset \(0\) \+ seq_len \(5\) exceeds cos/sin table size \(4\)"):
         cache.attention(0, q, k, v, cos, sin)
     assert not any(c.startswith("tl_rope") or c.startswith("tl_attention") for c in recording.calls)
+
+
+def test_kv_cache_advance_is_a_device_copy(recording):
+    """The cache length the kernels read moves by a stream-ordered device
+    copy from a table of lengths: advance() and reset() upload nothing and
+    never synchronise (the model advances once per generated token)."""
+    from triton_llm.kv_cache import GpuKVCache
+
+    copies = []
+
+    def dtod(dst, src, n):
+        copies.append((dst.value, src.value, n))
+        return 0
+
+    cache = GpuKVCache(2, 4, 2, 64, max_seq=32)
+    recording.tl_memcpy_dtod = dtod
+    table = cache._len_table.ptr.value
+    recording.calls.clear()
+    cache.advance(5)
+    cache.advance(1)
+    cache.reset()
+    assert copies == [(cache._lens.ptr.value, table + 4 * 5, 4), (cache._lens.ptr.value, table + 4 * 6, 4),
+                      (cache._lens.ptr.value, table, 4)]
+    for banned in ("tl_memcpy_htod", "tl_memcpy_dtoh", "tl_synchronize"):
+        assert banned not in recording.calls, recording.calls
+    assert cache.cache_len == 0

@@ -29,6 +29,8 @@ The validation and its messages follow model.py:197-214 and :256-268.
 
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 
 from triton_llm import gpu
@@ -87,6 +89,9 @@ class GpuKVCache:
             self.kv_cache_dev.append({"k": k, "v": v})
         self._cache_len = 0
         self._lens = gpu.zeros((1,), np.int32)  # cache_len on the device, read by the kernels
+        # 0 .. max_seq on the device: advance() and reset() copy the new length
+        # from here (a stream-ordered device copy, no host synchronisation)
+        self._len_table = gpu.to_device(np.arange(self.max_seq + 1, dtype=np.int32))
         self._decode_ws = decode_workspace(1, n_head, n_kv_head, self.max_seq, d_k)
         wsb = flash_workspace_bytes(1, n_kv_head, self.max_seq, d_k, dtype)
         self._prefill_ws = gpu.allocate((wsb,), np.uint8) if wsb else None
@@ -95,15 +100,20 @@ class GpuKVCache:
     def cache_len(self) -> int:
         return self._cache_len
 
+    def _set_lens(self, n: int):
+        src = ctypes.c_void_p(self._len_table.ptr.value + 4 * n)
+        gpu.check_error(gpu.runtime().tl_memcpy_dtod(self._lens.ptr, src, 4))
+
     def reset(self):
         """Forget the cached tokens (the cache rows are overwritten as it refills)."""
         self._cache_len = 0
-        self._lens.from_numpy(np.zeros(1, np.int32))
+        self._set_lens(0)
 
     def advance(self, seq: int):
-        """Count ``seq`` more cached tokens (after every layer of the step)."""
+        """Count ``seq`` more cached tokens (after every layer of the step).
+        Stream-ordered: no host synchronisation."""
         self._cache_len = check_step(self._cache_len, seq, self.max_seq)
-        self._lens.from_numpy(np.array([self._cache_len], np.int32))
+        self._set_lens(self._cache_len)
 
     def attention(self, layer: int, q_dev, k_dev, v_dev, cos_dev=None, sin_dev=None,
                   sm_scale: float | None = None):
