@@ -204,8 +204,10 @@ __global__ __launch_bounds__(kSkThreads) void skinny_partial_kernel(const void* 
 }
 
 // C_g[mi][col] = sum over K-slices of the partials, rounded to T, for every
-// column of the concatenated width.  Eight slices' loads are in flight at a
-// time (the sum is latency-bound).
+// column of the concatenated width.  The sum is latency-bound: up to
+// kReduceBatch slices' loads are in flight at once (one round trip for the
+// usual 4-24 slices), added in slice order.
+constexpr int kReduceBatch = 32;  // measured: SmolLM2-360M one-token layer 41.0 -> 37.5 us against 8
 template <typename T>
 __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restrict__ ws, GemmGroups G, int m, int ntot,
                                                             int ks) {
@@ -215,12 +217,12 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restr
   const int grp = find_group(G.col0, G.count, colg);
   const int64_t stride = (int64_t)m * ntot;
   float s = 0.f;
-  for (int q0 = 0; q0 < ks; q0 += 8) {
-    float v[8];
+  for (int q0 = 0; q0 < ks; q0 += kReduceBatch) {
+    float v[kReduceBatch];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = q0 + j < ks ? ws[(int64_t)(q0 + j) * stride + idx] : 0.f;
+    for (int j = 0; j < kReduceBatch; ++j) v[j] = q0 + j < ks ? ws[(int64_t)(q0 + j) * stride + idx] : 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) s += v[j];
+    for (int j = 0; j < kReduceBatch; ++j) s += v[j];
   }
   ((typename T::bits*)G.c[grp])[(int64_t)mi * G.ldc[grp] + (colg - G.col0[grp])] = from_f32<T>(s);
 }
