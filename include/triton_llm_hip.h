@@ -109,7 +109,8 @@ int tl_rope_inplace(void* x, const float* cos_table, const float* sin_table,
  * seq_q == seq_k).  Scores are (q . k) * sm_scale.
  * Requires seq_q >= 1, seq_k >= 1 (the Python layer returns the reference's
  * empty/zero results itself).  Workspace: tl_attention_fwd_workspace_bytes
- * (the 16-bit MFMA path stages a key-major copy of V there; 0 for fp32).
+ * (the 16-bit MFMA path at d_k 128 stages a key-major copy of V there; 0
+ * for d_k 64 and fp32, which read V in place; NULL is accepted when 0).
  * ------------------------------------------------------------------------- */
 size_t tl_attention_fwd_workspace_bytes(int batch, int n_kv_head, int seq_k,
                                         int d_k, int dtype);

@@ -37,7 +37,9 @@ def test_workspace_queries():
     # fp32 reads V in place; the 16-bit MFMA path stages V^T: B * Hkv * D * round_up(Sk, 128) * 2.
     assert lib.tl_attention_fwd_workspace_bytes(1, 8, 8192, 128, _lib.DTYPE_F32) == 0
     assert lib.tl_attention_fwd_workspace_bytes(1, 8, 8192, 128, _lib.DTYPE_BF16) == 8 * 128 * 8192 * 2
-    assert lib.tl_attention_fwd_workspace_bytes(2, 3, 100, 64, _lib.DTYPE_F16) == 2 * 3 * 64 * 128 * 2
+    # d_k 64 reads V in place: no V^T copy
+    assert lib.tl_attention_fwd_workspace_bytes(2, 3, 100, 64, _lib.DTYPE_F16) == 0
+    assert lib.tl_attention_fwd_workspace_bytes(2, 3, 100, 128, _lib.DTYPE_F16) == 2 * 3 * 128 * 128 * 2
     assert lib.tl_attention_fwd_workspace_bytes(1, 1, 100, 32, _lib.DTYPE_BF16) == 0  # generic path
     split = lib.tl_decode_split_size(64, 8, 16384)
     assert split % 16 == 0 and 64 <= split <= 4096

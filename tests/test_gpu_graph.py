@@ -83,9 +83,10 @@ def test_recorded_and_captured_launches_keep_their_workspace():
     replays still compute the right product and do not write into memory the
     larger product's call now uses."""
     from oracle.gemm import gemm_ref
-    from triton_llm.kernels import gemm
+    from triton_llm.kernels import _common, gemm
     from triton_llm.kernels._common import record, shared_workspace
 
+    _common._shared.pop("gemm", None)  # start from the smallest workspace, whatever ran before
     rng = np.random.default_rng(8)
     print("[case] workspace keep-alive: launcher and graph, then a growing gemm", flush=True)
     a = rng.standard_normal((1, 3072), dtype=np.float32)

@@ -213,6 +213,10 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
   constexpr int BN = K16_BN;
   constexpr int ROWB = D * 2;          // bytes per K / Q row in LDS
   constexpr int VROWB = BN * 2;        // bytes per V^T row in LDS (256)
+  // d_k 64 reads V in its natural layout (no V^T copy): its softmax VALU
+  // work, not LDS, limits a step, so the PV operand's transposing LDS reads
+  // (two ds_read_b64_tr_b16 per fragment) are affordable there.
+  constexpr bool VNAT = D == 64;
   constexpr int TILEB = BN * ROWB;     // bytes per K, V^T or 128-row Q tile
   constexpr int NSL = ROWB / 16;       // 16-byte slots per K row
   constexpr int RPR = 1024 / ROWB;     // K rows per 1 KiB region
@@ -252,6 +256,16 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
     const int row = 4 * wq + ln / 16;
     return ((uint32_t)row * (uint32_t)p.sk_pad + (uint32_t)(((ln % 16) ^ lds_swz<128>(row)) * 8)) * 2u;
   };
+  // Natural V rows (VNAT): like K rows, chunk c of key row r at slot
+  // c ^ vnat_swz(r), vnat_swz(r) = 2 ((r >> 1) & 1).  A transposing read
+  // covers 4 consecutive rows of a 16-lane group (4 lanes per row, 8 bytes
+  // each); rows 2 apart share banks, and the XOR moves one of them by 32
+  // bytes, so the group's 16 reads hit 32 distinct banks.
+  auto vnat_swz = [](int r) __attribute__((always_inline)) { return 2 * ((r >> 1) & 1); };
+  auto vnat_off = [&](int ln) __attribute__((always_inline)) {
+    const int row = wq * RPR + ln / NSL;
+    return ((uint32_t)row * (uint32_t)p.v_ss + (uint32_t)(((ln % NSL) ^ vnat_swz(row)) * 8)) * 2u;
+  };
   // Operand reads: lane (lq, h) reads row lq, chunk (2 ks + h) ^ swz(lq).
   auto k_lane_of = [&](int ln) __attribute__((always_inline)) {
     const int lq = ln & 31, h = ln >> 5;
@@ -268,12 +282,14 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
   const uint32_t q_ss2 = (uint32_t)p.q_ss * 2u;
   const uint32_t k_step = 4u * RPR * k_ss2;                // bytes of 4 regions of K rows
   const uint32_t q_step = 4u * RPR * q_ss2;                // bytes of 4 regions of Q rows
-  const uint32_t v_step = 16u * (uint32_t)p.sk_pad * 2u;  // bytes of 16 V^T rows
+  const uint32_t v_step = VNAT ? 4u * RPR * (uint32_t)p.v_ss * 2u    // bytes of 4 regions of V rows
+                                : 16u * (uint32_t)p.sk_pad * 2u;     // bytes of 16 V^T rows
 
   // ---- tile state --------------------------------------------------------------
   struct Tile {
     int b, hq, qt, n_kt, k_rows;
     const char* kg;
+    const char* vg;  // natural V of the tile's (batch, kv head) (VNAT)
   };
   auto make_tile = [&](int rank) __attribute__((always_inline)) {
     Tile tl;
@@ -284,6 +300,7 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
     tl.n_kt = (k_end + BN - 1) / BN;             // K tiles the workgroup loads
     tl.k_rows = min(p.seq_k, tl.n_kt * BN);      // keys the workgroup reads
     tl.kg = (const char*)((const Bits*)p.k + tl.b * p.k_sb + (tl.hq / p.group) * p.k_sh);
+    tl.vg = (const char*)((const Bits*)p.v + tl.b * p.v_sb + (tl.hq / p.group) * p.v_sh);
     return tl;
   };
 
@@ -303,10 +320,17 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
     const int rows = min(max(tl.k_rows - tk * BN, 0), BN);
     return rsrc_of(tl.kg + (int64_t)tk * BN * k_ss2, (uint32_t)rows * k_ss2);
   };
-  // V^T tile tv of a tile (nothing past its last K tile).
+  // V^T tile tv of a tile (nothing past its last K tile); with VNAT the
+  // tile's natural V rows, bounded like K's.
   auto v_rsrc = [&](const Tile& tl, int tv) __attribute__((always_inline)) {
-    const char* vg = (const char*)((const Bits*)p.vt + ((int64_t)tl.b * p.n_kv + tl.hq / p.group) * D * p.sk_pad);
-    return rsrc_of(vg + (int64_t)tv * BN * 2, tv < tl.n_kt ? (uint32_t)D * (uint32_t)p.sk_pad * 2u : 0u);
+    if constexpr (VNAT) {
+      const uint32_t v_ss2 = (uint32_t)p.v_ss * 2u;
+      const int rows = min(max(tl.k_rows - tv * BN, 0), BN);
+      return rsrc_of(tl.vg + (int64_t)tv * BN * v_ss2, (uint32_t)rows * v_ss2);
+    } else {
+      const char* vg = (const char*)((const Bits*)p.vt + ((int64_t)tl.b * p.n_kv + tl.hq / p.group) * D * p.sk_pad);
+      return rsrc_of(vg + (int64_t)tv * BN * 2, tv < tl.n_kt ? (uint32_t)D * (uint32_t)p.sk_pad * 2u : 0u);
+    }
   };
   // Q rows [128 g, 128 g + 128) of a tile (rows past seq_q read as zeros).
   auto q_rsrc = [&](const Tile& tl, int g) __attribute__((always_inline)) {
@@ -435,7 +459,7 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
         }
         if (t < n_kt) {
           rv = v_rsrc(cur, t);
-          vvo = v_off(ln);
+          vvo = VNAT ? vnat_off(ln) : v_off(ln);
         } else {
           rv = has_next ? q_rsrc(nxt, 1) : none;
           vvo = kq_off(ln, p.q_ss);
@@ -446,11 +470,33 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
       const int vbuf = (tb + t) & 1;      // V^T_t (or group 1's next Q)
       int kb_lane = k_lane_of(ln) + ((tb + t) & 1) * TILEB;              // K_t
       int vb_lane = v_lane_of(ln) + (2 + ((tb + t + 1) & 1)) * TILEB;   // V^T_{t-1}
+      // VNAT: lane 16 g + 4 e + q reads 8 bytes of key row 16 tt + 4 h + e
+      // (and + 8), columns 32 db + 16 (g % 2) + 4 q .. + 3 (h = g / 2); the
+      // transposing read hands lane l column 32 db + l % 32, keys 16 tt +
+      // 4 h + 0..3 (and + 8 ..): the PV operand's key order.
+      int vn_lane = 0;
+      if constexpr (VNAT) {
+        const int g16 = ln >> 4, e = (ln >> 2) & 3, q = ln & 3;
+        const int c0 = 2 * (g16 & 1) + (q >> 1);
+        vn_lane = (2 + ((tb + t + 1) & 1)) * TILEB + (4 * (g16 >> 1) + e) * ROWB +
+                  ((c0 ^ vnat_swz(e)) << 4) + 8 * (q & 1);
+      }
       u32x4 kfr[NG], vfr[NG];
       auto fetch = [&](int g) __attribute__((always_inline)) {
         if constexpr (DO_PV) {
           const int tt = g / NDB, db = g % NDB;
-          vfr[g] = *(const u32x4*)(smem + (vb_lane ^ (tt << 5)) + 32 * db * VROWB);
+          if constexpr (VNAT) {
+            typedef short v4s __attribute__((ext_vector_type(4)));
+            typedef __attribute__((address_space(3))) v4s lds_v4s;
+            __attribute__((address_space(3))) char* lds = (__attribute__((address_space(3))) char*)smem;
+            const int off = vn_lane + tt * 16 * ROWB + db * 64;
+            const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(lds + off));
+            const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(lds + off + 8 * ROWB));
+            vfr[g] = u32x4{__builtin_bit_cast(u32x2, lo).x, __builtin_bit_cast(u32x2, lo).y,
+                           __builtin_bit_cast(u32x2, hi).x, __builtin_bit_cast(u32x2, hi).y};
+          } else {
+            vfr[g] = *(const u32x4*)(smem + (vb_lane ^ (tt << 5)) + 32 * db * VROWB);
+          }
         }
         if constexpr (DO_S) {
           const int ks = s_ks(g), mb = s_mb(g);
@@ -1002,12 +1048,14 @@ int launch_flash_16(FlashParams& p, void* ws, bool causal, hipStream_t st) {
   p.q_machines = min((tl_device_cus() + p.n_queues - 1) / p.n_queues, p.q_tiles);
   const int rounds = p.q_tiles / p.q_machines;
   p.q_triple = (p.q_tiles % p.q_machines == 0 && rounds % 2 == 1 && rounds >= 3 && p.q_machines % 2 == 0) ? 1 : 0;
-  const int vt_tiles = p.sk_pad / 64 * p.n_kv * p.batch;
-  const int vt_grid = min(vt_tiles, 2 * tl_device_cus());
-  hipLaunchKernelGGL(vt_pack_kernel<D>, dim3(vt_grid), dim3(256), 0, st, (const uint16_t*)p.v, (uint16_t*)ws,
-                     p.seq_k, p.sk_pad, p.n_kv, vt_tiles, p.v_sb, p.v_sh, p.v_ss);
-  int e = tl_launch_status();
-  if (e) return e;
+  if constexpr (D != 64) {  // d_k 64 reads V in place
+    const int vt_tiles = p.sk_pad / 64 * p.n_kv * p.batch;
+    const int vt_grid = min(vt_tiles, 2 * tl_device_cus());
+    hipLaunchKernelGGL(vt_pack_kernel<D>, dim3(vt_grid), dim3(256), 0, st, (const uint16_t*)p.v, (uint16_t*)ws,
+                       p.seq_k, p.sk_pad, p.n_kv, vt_tiles, p.v_sb, p.v_sh, p.v_ss);
+    const int e = tl_launch_status();
+    if (e) return e;
+  }
   dim3 grid((unsigned)(p.q_machines * p.n_queues));
   if (causal)
     hipLaunchKernelGGL((flash_fwd_16<T, D, true>), grid, dim3(K16_THREADS), 0, st, p);
@@ -1049,6 +1097,8 @@ bool mfma_shape_ok(const FlashParams& p, int d_k, int dtype) {
     if (p.k_ss < d_k || (128 * p.k_ss + d_k) * 2 >= ((int64_t)1 << 32) || p.q_ss < d_k ||
         (128 * p.q_ss + d_k) * 2 >= ((int64_t)1 << 32) || (int64_t)d_k * sk_pad * 2 >= ((int64_t)1 << 32))
       return false;
+    // d_k 64 reads V tiles in place, bounded like K's
+    if (d_k == 64 && (p.v_ss < d_k || (128 * p.v_ss + d_k) * 2 >= ((int64_t)1 << 32))) return false;
   }
   return aligned16(p.q) && aligned16(p.k) && aligned16(p.v) && aligned16(p.o);
 }
@@ -1059,10 +1109,9 @@ extern "C" {
 
 size_t tl_attention_fwd_workspace_bytes(int batch, int n_kv_head, int seq_k, int d_k,
                                         int dtype) {
-  // 16-bit MFMA path: the permuted key-major V^T copy.  fp32 and the generic
-  // kernel read V in place.
-  if (dtype == TL_DTYPE_F32 || batch <= 0 || n_kv_head <= 0 || seq_k <= 0 ||
-      (d_k != 64 && d_k != 128))
+  // 16-bit MFMA path at d_k 128: the permuted key-major V^T copy.  d_k 64,
+  // fp32 and the generic kernel read V in place.
+  if (dtype == TL_DTYPE_F32 || batch <= 0 || n_kv_head <= 0 || seq_k <= 0 || d_k != 128)
     return 0;
   return vt_bytes(batch, n_kv_head, seq_k, d_k);
 }
@@ -1102,9 +1151,8 @@ int tl_attention_fwd(const void* q, const void* k, const void* v, void* o, void*
     if (dtype == TL_DTYPE_F32) {
       return d_k == 64 ? launch_flash_f32<64>(p, cz, st) : launch_flash_f32<128>(p, cz, st);
     }
-    if (!workspace || !aligned16(workspace) ||
-        workspace_bytes < tl_attention_fwd_workspace_bytes(batch, n_kv_head, seq_k, d_k, dtype))
-      return TL_ERR_INVALID;
+    const size_t need = tl_attention_fwd_workspace_bytes(batch, n_kv_head, seq_k, d_k, dtype);
+    if (need && (!workspace || !aligned16(workspace) || workspace_bytes < need)) return TL_ERR_INVALID;
     if (dtype == TL_DTYPE_BF16)
       return d_k == 64 ? launch_flash_16<BF16, 64>(p, workspace, cz, st)
                        : launch_flash_16<BF16, 128>(p, workspace, cz, st);
