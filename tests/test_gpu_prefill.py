@@ -79,12 +79,14 @@ def test_prefill_ragged_shapes(dtype, d_k, causal):
     compare(f"ragged {dtype} d{d_k} causal={causal}", got, exp, TOL[dtype])
 
 
-@pytest.mark.parametrize("sq,sk", [(1, 1), (1, 300), (37, 300), (130, 129), (64, 64), (5, 3)])
-def test_prefill_seq_q_ne_seq_k(sq, sk):
-    """Bottom-right causal alignment; sq > sk leaves the first rows fully masked (NaN)."""
+@pytest.mark.parametrize("d_k", [64, 128])
+@pytest.mark.parametrize("sq,sk", [(1, 1), (1, 300), (37, 300), (130, 129), (64, 64), (5, 3), (300, 700)])
+def test_prefill_seq_q_ne_seq_k(sq, sk, d_k):
+    """Bottom-right causal alignment; sq > sk leaves the first rows fully masked (NaN).
+    d_k 64 reads V in place, d_k 128 through its V^T copy."""
     dt = "bfloat16"
-    rng = np.random.default_rng(sq * 1000 + sk)
-    B, Hq, Hkv, D = 1, 4, 2, 64
+    rng = np.random.default_rng(sq * 1000 + sk + d_k)
+    B, Hq, Hkv, D = 1, 4, 2, d_k
     q = on.to_storage(rng.standard_normal((B, Hq, sq, D), dtype=np.float32), dt)
     k = on.to_storage(rng.standard_normal((B, Hkv, sk, D), dtype=np.float32), dt)
     v = on.to_storage(rng.standard_normal((B, Hkv, sk, D), dtype=np.float32), dt)
@@ -105,14 +107,15 @@ def test_prefill_generic_head_sizes(d_k):
     compare(f"generic d{d_k}", got, exp, TOL[dt])
 
 
+@pytest.mark.parametrize("d_k", [64, 128])
 @pytest.mark.parametrize("group", [1, 2, 3, 4, 8])
-def test_prefill_gqa_groups(group):
+def test_prefill_gqa_groups(group, d_k):
     dt = "bfloat16"
-    cfg = oi.Config("groups", "prefill", dt, 1, 2 * group, 2, 128, 30 + group, 0.088, seq=256)
+    cfg = oi.Config("groups", "prefill", dt, 1, 2 * group, 2, d_k, 30 + group, 1 / np.sqrt(d_k), seq=256)
     raw = oi.make_prefill_raw(cfg)
     got = gpu_prefill(cfg, raw)
     exp = oa.attention_bhsd(raw["q"], raw["k"], raw["v"], causal=True, sm_scale=cfg.scale, dtype=dt)
-    compare(f"group{group}", got, exp, TOL[dt])
+    compare(f"group{group} d{d_k}", got, exp, TOL[dt])
 
 
 def test_prefill_reads_cache_layout_and_seq_major_rows():
