@@ -150,6 +150,27 @@ def test_gemm_prompt_shapes_mfma(dtype, M, K, N):
         np.testing.assert_allclose(got, exp, rtol=8e-3, atol=1e-2)
 
 
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("M,K,Ns", [(1900, 136, (16456,)), (2048, 264, (16384,)), (2000, 72, (8192, 8200))])
+def test_gemm_prompt_wide_tiles(dtype, M, K, Ns):
+    """Products with at least four 256-row tiles per CU take the 256 x 128
+    tile kernel (16-bit): ragged M and N, K tails inside a 32-k stage, and
+    the grouped form."""
+    print(f"[case] gemm wide {dtype} {M}x{K} -> {Ns}", flush=True)
+    rng = np.random.default_rng(M + K + sum(Ns))
+    a = on.to_storage(rng.standard_normal((M, K), dtype=np.float32), dtype)
+    bs = [on.to_storage(rng.standard_normal((K, n), dtype=np.float32) / np.sqrt(K), dtype) for n in Ns]
+    a_dev = H.upload(a, dtype)
+    if len(Ns) == 1:
+        outs = [gemm(a_dev, H.upload(bs[0], dtype))]
+    else:
+        outs = gemm_grouped(a_dev, [H.upload(b, dtype) for b in bs])
+    for b, o in zip(bs, outs):
+        got = on.from_storage(H.download(o), dtype)
+        exp = gemm_ref(on.from_storage(a, dtype), on.from_storage(b, dtype))
+        np.testing.assert_allclose(got, exp, rtol=8e-3, atol=1e-2)
+
+
 @pytest.mark.parametrize("dtype,K", [("bfloat16", 136), ("float16", 72), ("float32", 132), ("float32", 20)])
 def test_gemm_strided_operands_keep_padding_out(dtype, K):
     """Row strides past the logical sizes, with NaN in every padding element:

@@ -314,18 +314,21 @@ __device__ __forceinline__ bool gemm_tile(const GemmParams& p, int& grp, int& tm
   return true;
 }
 
-// BKB: bytes of k per A row per stage (64 or 128); NST: stages in LDS.
-template <typename T, int BKB, int NST>
+// BKB: bytes of k per A row per stage (64 or 128); NST: stages in LDS; MBW:
+// 32-row blocks per wave along m (2: 128 x 128 tiles, 4: 256 x 128 tiles,
+// where each B fragment a wave reads feeds four MFMAs instead of two).
+template <typename T, int BKB, int NST, int MBW>
 __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) {
   constexpr bool F32 = T::size == 4;
+  constexpr int TM = 64 * MBW;                // rows of C per tile
   constexpr int BK = BKB / T::size;           // k per stage
   constexpr int ACH = BKB / 16;               // 16-byte chunks per A row (4 or 8)
   constexpr int BROW = kGmTile * T::size;     // bytes per B row in LDS
   constexpr int NQ = F32 ? BK / 8 : BK / 16;  // fp32 k-groups / 16-bit k-steps per stage
   constexpr int kGmStages = NST;
-  constexpr int kGmStageA = kGmTile * BKB;    // bytes of one A stage
+  constexpr int kGmStageA = TM * BKB;         // bytes of one A stage
   constexpr int kGmStageB = BK * BROW;        // bytes of one B stage
-  static_assert(kGmStageA == kGmStageB, "A and B stages are the same size");
+  static_assert(kGmStageA % 4096 == 0 && kGmStageB % 4096 == 0, "every wave loads whole 1 KiB regions");
   using Bits = typename T::bits;
   __shared__ __attribute__((aligned(1024))) char smem[kGmStages * (kGmStageA + kGmStageB)];
 
@@ -341,8 +344,8 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) 
   const int64_t pldb = p.G.ldb[grp], pldc = p.G.ldc[grp];
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  const int wm = wave & 1, wn = wave >> 1;  // this wave's 64 x 64 quadrant
-  const int m_tile = tm * kGmTile, n_tile = tn * kGmTile;
+  const int wm = wave & 1, wn = wave >> 1;  // this wave's (32 MBW) x 64 block
+  const int m_tile = tm * TM, n_tile = tn * kGmTile;
   __attribute__((address_space(3))) char* const lds_base = (__attribute__((address_space(3))) char*)smem;
   const uint32_t lds0 = (uint32_t)(size_t)lds_base;
   const uint32_t lds_a = lds0, lds_b = lds0 + kGmStages * kGmStageA;
@@ -395,9 +398,9 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) 
       dma(rb, b_off + kb + (uint32_t)(4 * B_RPR * j) * ldb2, lds_b + buf * kGmStageB + (wave + 4 * j) * 1024);
   };
 
-  f32x16 acc[2][2];  // [m block][n block], C^T layout
+  f32x16 acc[MBW][2];  // [m block][n block], C^T layout
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < MBW; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -405,9 +408,9 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) 
 
   // Operand read offsets inside a stage.
   const int lq = lane & 31, h = lane >> 5;
-  // A: row 64 wm + 32 mb + lq, chunk c at slot c ^ a_swz(row).
+  // A: row 32 MBW wm + 32 mb + lq, chunk c at slot c ^ a_swz(row).
   auto a_addr = [&](int mb, int c) __attribute__((always_inline)) {
-    const int row = 64 * wm + 32 * mb + lq;
+    const int row = 32 * MBW * wm + 32 * mb + lq;
     return row * BKB + ((c ^ a_swz(row)) << 4);
   };
   const int n_kt = (p.k + BK - 1) / BK;
@@ -441,9 +444,9 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) 
     for (int q = 0; q < NQ; ++q) {
       if constexpr (!F32) {
         // k-step q: k = 16 q + 8 h + 0..7 of the stage.
-        bf16x8 af[2];
+        bf16x8 af[MBW];
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
+        for (int mb = 0; mb < MBW; ++mb) {
           u32x4 raw = *(const u32x4*)(sa + a_addr(mb, 2 * q + h));
           if (tail) {
             uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
@@ -470,15 +473,15 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) 
           const u32x4 braw = u32x4{__builtin_bit_cast(u32x2, lo).x, __builtin_bit_cast(u32x2, lo).y,
                                    __builtin_bit_cast(u32x2, hi).x, __builtin_bit_cast(u32x2, hi).y};
 #pragma unroll
-          for (int mb = 0; mb < 2; ++mb)
+          for (int mb = 0; mb < MBW; ++mb)
             acc[mb][nb] = Mfma<T>::mma(__builtin_bit_cast(typename Mfma<T>::frag, braw),
                                        __builtin_bit_cast(typename Mfma<T>::frag, af[mb]), acc[mb][nb]);
         }
       } else {
         // k-group q: k = 8 q + 4 h + s, s = 0..3.
-        f32x4 af[2];
+        f32x4 af[MBW];
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
+        for (int mb = 0; mb < MBW; ++mb) {
           f32x4 v = *(const f32x4*)(sa + a_addr(mb, 2 * q + h));
           if (tail) {
 #pragma unroll
@@ -495,7 +498,7 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) 
             const int byte = (64 * wn + 32 * nb + lq) * 4;
             const float bv = *(const float*)(sb + row * BROW + (byte ^ (128 * ((row >> 2) & 1))));
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb)
+            for (int mb = 0; mb < MBW; ++mb)
               acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(bv, af[mb][s], acc[mb][nb], 0, 0, 0);
           }
         }
@@ -504,13 +507,13 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) 
   }
   wait_vmcnt<0>();
 
-  // lane (lq, h) holds row m = m_tile + 64 wm + 32 mb + lq and, for a = 0..3,
-  // columns n = n_tile + 64 wn + 32 nb + 8 a + 4 h + 0..3.
+  // lane (lq, h) holds row m = m_tile + 32 MBW wm + 32 mb + lq and, for
+  // a = 0..3, columns n = n_tile + 64 wn + 32 nb + 8 a + 4 h + 0..3.
   Bits* cbase = (Bits*)p.G.c[grp];
   const bool vec = (p.vec_store >> grp) & 1;
 #pragma unroll
-  for (int mb = 0; mb < 2; ++mb) {
-    const int m = m_tile + 64 * wm + 32 * mb + lq;
+  for (int mb = 0; mb < MBW; ++mb) {
+    const int m = m_tile + 32 * MBW * wm + 32 * mb + lq;
     if (m >= p.m) continue;
     Bits* crow = cbase + (int64_t)m * pldc;
 #pragma unroll
@@ -594,7 +597,7 @@ int launch_gemm(const void* a, const GemmGroups& G, int m, int k, int64_t lda, h
   // all of A and each B addressable with 32-bit offsets (stage reads run up
   // to one stage past the last row / k).
   bool aligned = lda % vec == 0 && ((uintptr_t)a % 16) == 0 &&
-                 ((int64_t)m + kGmTile + 1) * lda * esize < ((int64_t)1 << 32);
+                 ((int64_t)m + 2 * kGmTile + 1) * lda * esize < ((int64_t)1 << 32);
   int widest = 0;
   for (int g = 0; g < G.count; ++g) {
     aligned = aligned && G.ldb[g] % vec == 0 && G.n[g] % vec == 0 && ((uintptr_t)G.b[g] % 16) == 0 &&
@@ -602,7 +605,16 @@ int launch_gemm(const void* a, const GemmGroups& G, int m, int k, int64_t lda, h
     widest = G.n[g] > widest ? G.n[g] : widest;
   }
   if (aligned) {
-    p.tiles_m = (m + kGmTile - 1) / kGmTile;
+    // 16-bit: 256-row tiles (each B fragment feeds four MFMAs, 25% less
+    // operand traffic per product) when they still give every CU at least
+    // four; fewer, larger tiles leave CUs idle on the narrower products.
+    // Measured at a 2048-row Llama-3.2-3B prompt: gate/up 226 -> 219 us;
+    // q/k/v, o and down (320 or fewer such tiles) were slower with them.
+    int wide_tiles = 0;
+    for (int g = 0; g < G.count; ++g) wide_tiles += ((m + 2 * kGmTile - 1) / (2 * kGmTile)) * ((G.n[g] + kGmTile - 1) / kGmTile);
+    const bool wide = T::size == 2 && wide_tiles >= 4 * tl_device_cus();
+    const int tm = wide ? 2 * kGmTile : kGmTile;
+    p.tiles_m = (m + tm - 1) / tm;
     p.G.tile0[0] = 0;
     p.vec_store = 0;
     for (int g = 0; g < G.count; ++g) {
@@ -615,10 +627,14 @@ int launch_gemm(const void* a, const GemmGroups& G, int m, int k, int64_t lda, h
     // in three, 691 with 32 k in four, 507 with 64 k in three); fp32 is
     // within 1% across those and keeps 16 k in three stages.
     const dim3 grid((unsigned)(8 * p.per_xcd));
-    if constexpr (T::size == 2)
-      hipLaunchKernelGGL((gemm_mfma_kernel<T, 128, 2>), grid, dim3(kGmThreads), 0, st, p);
-    else
-      hipLaunchKernelGGL((gemm_mfma_kernel<T, 64, 3>), grid, dim3(kGmThreads), 0, st, p);
+    if constexpr (T::size == 2) {
+      if (wide)
+        hipLaunchKernelGGL((gemm_mfma_kernel<T, 64, 3, 4>), grid, dim3(kGmThreads), 0, st, p);
+      else
+        hipLaunchKernelGGL((gemm_mfma_kernel<T, 128, 2, 2>), grid, dim3(kGmThreads), 0, st, p);
+    } else {
+      hipLaunchKernelGGL((gemm_mfma_kernel<T, 64, 3, 2>), grid, dim3(kGmThreads), 0, st, p);
+    }
     return tl_launch_status();
   }
   dim3 grid((unsigned)((widest + 63) / 64), (unsigned)((m + 63) / 64), (unsigned)G.count);
