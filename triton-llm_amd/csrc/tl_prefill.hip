@@ -405,6 +405,7 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
   for (;;) {
     const int nrank = sched_rank(p, mach, r + 1);
     const bool has_next = nrank < p.q_tiles;
+    const Tile nxt = make_tile(has_next ? nrank : rank);  // wave-uniform (SGPRs)
     const int n_kt = cur.n_kt;
     const int q0 = cur.qt * K16_BM + 128 * group + 32 * wq;  // first row of this wave
     int wave_k_end = p.seq_k;
@@ -444,7 +445,6 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
         // K slot: K_{t+1}; at t = n_kt - 1 group 0's next Q rows (K_{n_kt}
         // is never used: G(n_kt) computes no S); at t = n_kt the next K_0.
         // V slot: V^T_t; at t = n_kt group 1's next Q rows.
-        const Tile nxt = make_tile(has_next ? nrank : rank);
         const i32x4 none = rsrc_of(cur.kg, 0u);
         if (t < n_kt - 1) {
           rk = k_rsrc(cur, t + 1);
@@ -658,7 +658,6 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
     //    waited for here.
     const float inv = kMfmaRowSum ? 1.f / l_acc[0] : 1.f / sum_xor32((l4[0] + l4[1]) + (l4[2] + l4[3]));
     const int ntb = (tb + n_kt + 1) & 1;  // where the next K_0 went
-    const Tile nxt = make_tile(has_next ? nrank : rank);
     // the next Q rows: group 0's in K buffer (tb + n_kt) & 1, group 1's in
     // V^T buffer (tb + n_kt) & 1; each group stages its output there too
     const int qbuf = (group == 0 ? 0 : 2 * TILEB) + ((tb + n_kt) & 1) * TILEB;
@@ -688,12 +687,28 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
           const int c = 4 * db + rq;
           *(u32x2*)(smem + wbase + lq * ROWB + ((c ^ lds_swz<D>(lq)) << 4) + 8 * h) = u32x2{pack2<T>(x0), pack2<T>(x1)};
         }
-      Bits* obase = (Bits*)p.o + cur.b * p.o_sb + cur.hq * p.o_sh;
+      // This wave's 32 output rows through one buffer resource that ends at
+      // row seq_q (stores past it are dropped: no per-row branch), 32-bit
+      // offsets (the shape check bounds 32 rows of o), all LDS reads first.
+      const uint64_t oa = (uint64_t)(uintptr_t)((Bits*)p.o + cur.b * p.o_sb + cur.hq * p.o_sh + (int64_t)q0 * p.o_ss);
+      const uint32_t o_ss2 = (uint32_t)p.o_ss * 2u;
+      // every field wave-uniform (read from the first lane), so the resource
+      // lives in SGPRs and the store needs no per-lane loop
+      char* obase = (char*)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(oa >> 32)) << 32) |
+                            (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)oa));
+      const int o_bytes = __builtin_amdgcn_readfirstlane((int)((uint32_t)min(max(p.seq_q - q0, 0), 32) * o_ss2));
+      const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(obase, (short)0, o_bytes, kBufRsrcWord3);
+      u32x4 val[32 / RPR];
 #pragma unroll
       for (int i = 0; i < 32 / RPR; ++i) {
         const int rr = i * RPR + ln / NSL, cc = ln % NSL;
-        const u32x4 val = *(const u32x4*)(smem + wbase + rr * ROWB + ((cc ^ lds_swz<D>(rr)) << 4));
-        if (q0 + rr < p.seq_q) *(u32x4*)(obase + (int64_t)(q0 + rr) * p.o_ss + 8 * cc) = val;
+        val[i] = *(const u32x4*)(smem + wbase + rr * ROWB + ((cc ^ lds_swz<D>(rr)) << 4));
+      }
+#pragma unroll
+      for (int i = 0; i < 32 / RPR; ++i) {
+        const int rr = i * RPR + ln / NSL, cc = ln % NSL;
+        const uint32_t voff = (uint32_t)rr * o_ss2 + (uint32_t)cc * 16u;
+        __builtin_amdgcn_raw_buffer_store_b128(val[i], ro, (int)voff, 0, 0);
       }
     }
     lds_barrier();  // the staging buffers are reused by the next tile's first loads
@@ -1090,11 +1105,13 @@ bool mfma_shape_ok(const FlashParams& p, int d_k, int dtype) {
   for (int64_t x : s)
     if (x < 0 || x % vec) return false;
   if (dtype != TL_DTYPE_F32) {
-    // The 16-bit kernel addresses a K or Q tile (128 rows) and a head's V^T
-    // copy with 32-bit byte offsets, and bounds a K or Q tile's reads by its
-    // row count times the row stride (rows must not overlap).
+    // The 16-bit kernel addresses a K or Q tile (128 rows), a wave's 32
+    // output rows and a head's V^T copy with 32-bit byte offsets, and bounds
+    // a K or Q tile's reads and an output block's stores by its row count
+    // times the row stride (rows must not overlap).
     const int64_t sk_pad = (p.seq_k + 127) / 128 * 128;
     if (p.k_ss < d_k || (128 * p.k_ss + d_k) * 2 >= ((int64_t)1 << 32) || p.q_ss < d_k ||
+        p.o_ss < d_k || (32 * p.o_ss + d_k) * 2 >= ((int64_t)1 << 32) ||
         (128 * p.q_ss + d_k) * 2 >= ((int64_t)1 << 32) || (int64_t)d_k * sk_pad * 2 >= ((int64_t)1 << 32))
       return false;
     // d_k 64 reads V tiles in place, bounded like K's
