@@ -203,16 +203,21 @@ int tl_rope_kv_append(void* q, const void* k_new, const void* v_new,
  * :360-363, :375).  k = 0 writes zeros; m = 0 or n = 0 does nothing.
  * m <= 8 (a decoded token) runs a hand-written HBM-streaming kernel whose
  * K-slice partial sums need tl_gemm_workspace_bytes(m, n, k, dtype) bytes of
- * workspace (0 otherwise); larger m runs a hand-written MFMA kernel
- * (128 x 128 tiles of C; rows of A and B must be 16-byte aligned, otherwise a
- * simple FMA kernel takes the product) and needs no workspace.
+ * workspace; larger m runs a hand-written MFMA kernel (128 x 128 tiles of
+ * C, or 256 x 128 for large 16-bit products; rows of A and B must be
+ * 16-byte aligned, otherwise a simple FMA kernel takes the product), which
+ * for fp32 products that leave CUs unevenly loaded splits K and keeps fp32
+ * partials in the workspace.  The query gives 0 when no workspace is used.
+ * Given less than the query asks for, the MFMA kernel runs whole-K instead
+ * of failing; the few-row kernel needs its workspace.
  * ------------------------------------------------------------------------- */
 size_t tl_gemm_workspace_bytes(int m, int n, int k, int dtype);
 int tl_gemm(const void* a, const void* b, void* c, int m, int n, int k, int64_t lda,
             int64_t ldb, int64_t ldc, void* workspace, size_t workspace_bytes, int dtype,
             void* stream);
 /* Up to four products that share A, C_g = A . B_g with B_g (k, n[g]),
- * in one launch (plus one split-K reduce launch for all of them when m <= 8):
+ * in one launch (plus one split-K reduce launch for all of them when K is
+ * split):
  * the q/k/v projections of a layer, or gate/up.  No reference counterpart as
  * one call: the reference's model calls gemm (gemm.py:53-108) once per
  * projection (smollm2_triton/model.py:285-287, :360-361).  Per group the

@@ -171,6 +171,55 @@ def test_gemm_prompt_wide_tiles(dtype, M, K, Ns):
         np.testing.assert_allclose(got, exp, rtol=8e-3, atol=1e-2)
 
 
+@pytest.mark.parametrize("dtype,M,K,Ns", [("float32", 2048, 3072, (3072,)), ("float32", 1900, 3000, (3000,)),
+                                          ("float32", 300, 3072, (3072, 1024, 1024)), ("float32", 2048, 8200, (3068,))])
+def test_gemm_prompt_split_k(dtype, M, K, Ns):
+    """fp32 products whose whole tiles would leave some CUs a tile more than
+    others run K in slices (fp32 partials, one reduce pass): ragged M and N,
+    a K tail in the last slice, the grouped form.  The workspace query
+    reports the partials, so these shapes do take the split path."""
+    print(f"[case] gemm split-k {dtype} {M}x{K} -> {Ns}", flush=True)
+    lib = gpu.runtime()
+    code = gpu.dtype_code(H.GPU_DTYPES[dtype])
+    n_arr = (ctypes.c_int * len(Ns))(*Ns)
+    assert lib.tl_gemm_grouped_workspace_bytes(M, K, len(Ns), n_arr, code) >= 2 * M * sum(Ns) * 4
+    rng = np.random.default_rng(M + K + sum(Ns))
+    a = on.to_storage(rng.standard_normal((M, K), dtype=np.float32), dtype)
+    bs = [on.to_storage(rng.standard_normal((K, n), dtype=np.float32) / np.sqrt(K), dtype) for n in Ns]
+    a_dev = H.upload(a, dtype)
+    if len(Ns) == 1:
+        outs = [gemm(a_dev, H.upload(bs[0], dtype))]
+    else:
+        outs = gemm_grouped(a_dev, [H.upload(b, dtype) for b in bs])
+    for b, o in zip(bs, outs):
+        got = on.from_storage(H.download(o), dtype)
+        exp = gemm_ref(on.from_storage(a, dtype), on.from_storage(b, dtype))
+        if dtype == "float32":
+            err = H.max_abs(got, exp)
+            H.report(f"split-k {dtype} {M}x{K}@{K}x{b.shape[1]}", err, 2e-3)
+            assert err <= 2e-3
+        else:
+            np.testing.assert_allclose(got, exp, rtol=8e-3, atol=1e-2)
+
+
+def test_gemm_prompt_split_k_without_workspace_runs_whole():
+    """The C ABI with no workspace for a shape its plan would split: the
+    product runs with whole-K tiles instead (no failure, same result)."""
+    lib = gpu.runtime()
+    M, K, N = 2048, 3072, 3072
+    code = gpu.dtype_code(np.float32)
+    assert lib.tl_gemm_workspace_bytes(M, N, K, code) > 0
+    rng = np.random.default_rng(5)
+    a = rng.standard_normal((M, K), dtype=np.float32)
+    b = (rng.standard_normal((K, N), dtype=np.float32) / np.sqrt(K)).astype(np.float32)
+    a_dev, b_dev = H.upload(a), H.upload(b)
+    c_dev = gpu.allocate((M, N), np.float32)
+    assert lib.tl_gemm(a_dev.ptr, b_dev.ptr, c_dev.ptr, M, N, K, K, N, N, None, 0, code, None) == 0
+    err = H.max_abs(H.download(c_dev), gemm_ref(a, b))
+    H.report("split-k shape, no workspace", err, 2e-3)
+    assert err <= 2e-3
+
+
 @pytest.mark.parametrize("dtype,K", [("bfloat16", 136), ("float16", 72), ("float32", 132), ("float32", 20)])
 def test_gemm_strided_operands_keep_padding_out(dtype, K):
     """Row strides past the logical sizes, with NaN in every padding element:

@@ -298,15 +298,25 @@ struct GemmParams {
   GemmGroups G;   // tile0 counts 128 x 128 tiles of C
   int tiles_m, per_xcd;
   int vec_store;  // bit g: C_g's rows and base allow 4-column vector stores
+  // Split K (ksplit > 1): item (slice s, tile t) covers stages
+  // [s kt_per, (s + 1) kt_per) and stores its fp32 partial tile at
+  // ws + ws_off[g] + (s m + row) n_g + col; split_reduce_kernel sums them.
+  int ksplit, kt_per;
+  float* ws;
+  int64_t ws_off[kMaxGroups];
 };
 
-// Tile of workgroup L: each XCD (workgroups are dealt to the 8 XCDs in turn)
-// takes a contiguous run of tiles, row tiles fastest, so the workgroups an
-// XCD runs at once share their B column tiles and A row tiles in its L2.
-__device__ __forceinline__ bool gemm_tile(const GemmParams& p, int& grp, int& tm, int& tn) {
+// Work item of workgroup L: each XCD (workgroups are dealt to the 8 XCDs in
+// turn) takes a contiguous run of items, row tiles fastest, so the
+// workgroups an XCD runs at once share their B column tiles and A row tiles
+// in its L2; items are slice-major (all tiles of K-slice 0, then slice 1).
+__device__ __forceinline__ bool gemm_tile(const GemmParams& p, int& grp, int& tm, int& tn, int& ks) {
   const int L = blockIdx.x;
-  const int t = (L % 8) * p.per_xcd + L / 8;
-  if (t >= p.G.tile0[p.G.count]) return false;
+  const int it = (L % 8) * p.per_xcd + L / 8;
+  const int tiles = p.G.tile0[p.G.count];
+  if (it >= tiles * p.ksplit) return false;
+  ks = it / tiles;
+  const int t = it - ks * tiles;
   grp = find_group(p.G.tile0, p.G.count, t);
   const int local = t - p.G.tile0[grp];
   tm = local % p.tiles_m;
@@ -338,8 +348,8 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) 
   auto a_swz = [](int row) __attribute__((always_inline)) {
     return ACH == 4 ? (row >> 2) & 3 : (row >> 1) & 7;
   };
-  int grp, tm, tn;
-  if (!gemm_tile(p, grp, tm, tn)) return;
+  int grp, tm, tn, ks;
+  if (!gemm_tile(p, grp, tm, tn, ks)) return;
   const int pn = p.G.n[grp];
   const int64_t pldb = p.G.ldb[grp], pldc = p.G.ldc[grp];
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
@@ -415,27 +425,29 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) 
   };
   const int n_kt = (p.k + BK - 1) / BK;
   const int k_rem = p.k - (n_kt - 1) * BK;  // valid k of the last stage
+  const int kt_lo = ks * p.kt_per;          // this item's stages
+  const int kt_hi = min(n_kt, kt_lo + p.kt_per);
 
 #pragma unroll
   for (int s = 0; s < kGmStages - 1; ++s)
-    if (s < n_kt) load_stage(s, s);
+    if (kt_lo + s < kt_hi) load_stage(kt_lo + s, (kt_lo + s) % kGmStages);
 
-  for (int kt = 0; kt < n_kt; ++kt) {
+  for (int kt = kt_lo; kt < kt_hi; ++kt) {
     // stage kt has landed (this wave's loads; the barrier covers the others'):
     // the stages issued after it, up to NST - 2 of them, may stay in flight
     constexpr int PER = A_REG + B_REG;
     if constexpr (NST >= 4) {
-      if (kt + 2 < n_kt) wait_vmcnt<2 * PER>();
-      else if (kt + 1 < n_kt) wait_vmcnt<PER>();
+      if (kt + 2 < kt_hi) wait_vmcnt<2 * PER>();
+      else if (kt + 1 < kt_hi) wait_vmcnt<PER>();
       else wait_vmcnt<0>();
     } else if constexpr (NST == 3) {
-      if (kt + 1 < n_kt) wait_vmcnt<PER>();
+      if (kt + 1 < kt_hi) wait_vmcnt<PER>();
       else wait_vmcnt<0>();
     } else {
       wait_vmcnt<0>();
     }
     lds_barrier();
-    if (kt + kGmStages - 1 < n_kt) load_stage(kt + kGmStages - 1, (kt + kGmStages - 1) % kGmStages);
+    if (kt + kGmStages - 1 < kt_hi) load_stage(kt + kGmStages - 1, (kt + kGmStages - 1) % kGmStages);
     const int buf = kt % kGmStages;
     const char* sa = smem + buf * kGmStageA;
     const char* sb = smem + kGmStages * kGmStageA + buf * kGmStageB;
@@ -509,6 +521,26 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) 
 
   // lane (lq, h) holds row m = m_tile + 32 MBW wm + 32 mb + lq and, for
   // a = 0..3, columns n = n_tile + 64 wn + 32 nb + 8 a + 4 h + 0..3.
+  if (p.ksplit > 1) {
+    // fp32 partial of this K-slice; n_g is a multiple of 4 on this path, so
+    // every 4-column run is whole and 16-byte aligned
+    float* wsb = p.ws + p.ws_off[grp] + (int64_t)ks * p.m * pn;
+#pragma unroll
+    for (int mb = 0; mb < MBW; ++mb) {
+      const int m = m_tile + 32 * MBW * wm + 32 * mb + lq;
+      if (m >= p.m) continue;
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+          const int n = n_tile + 64 * wn + 32 * nb + 8 * a + 4 * h;
+          if (n < pn)
+            *(f32x4*)(wsb + (int64_t)m * pn + n) =
+                f32x4{acc[mb][nb][4 * a], acc[mb][nb][4 * a + 1], acc[mb][nb][4 * a + 2], acc[mb][nb][4 * a + 3]};
+        }
+    }
+    return;
+  }
   Bits* cbase = (Bits*)p.G.c[grp];
   const bool vec = (p.vec_store >> grp) & 1;
 #pragma unroll
@@ -536,6 +568,46 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) 
             if (n + e < pn) crow[n + e] = from_f32<T>(v[e]);
         }
       }
+  }
+}
+
+// Split-K finish: C_g = sum over the K-slices of the fp32 partial tiles
+// (slice 0 first, so the result does not depend on timing), rounded to T.
+// One 4-column run per thread, grid-stride; blockIdx.y = group.
+template <typename T>
+__global__ __launch_bounds__(256) void split_reduce_kernel(GemmParams p) {
+  using Bits = typename T::bits;
+  const int g = blockIdx.y;
+  const int n = p.G.n[g];
+  const int q4 = n / 4;
+  const int runs = p.m * q4;
+  const float* w = p.ws + p.ws_off[g];
+  const int64_t slice = (int64_t)p.m * n;
+  Bits* c = (Bits*)p.G.c[g];
+  const int64_t ldc = p.G.ldc[g];
+  const bool vec = (p.vec_store >> g) & 1;
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < runs; i += gridDim.x * 256) {
+    const int r = i / q4;
+    const int col = (i - r * q4) * 4;
+    f32x4 sum = *(const f32x4*)(w + (int64_t)r * n + col);
+    for (int ks = 1; ks < p.ksplit; ++ks) sum += *(const f32x4*)(w + ks * slice + (int64_t)r * n + col);
+    Bits* dst = c + (int64_t)r * ldc + col;
+    if constexpr (T::size == 4) {
+      if (vec) {
+        *(f32x4*)dst = sum;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dst[e] = from_f32<T>(sum[e]);
+      }
+    } else {
+      const float x0[2] = {sum[0], sum[1]}, x1[2] = {sum[2], sum[3]};
+      if (vec) {
+        *(u32x2*)dst = u32x2{pack2<T>(x0), pack2<T>(x1)};
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dst[e] = from_f32<T>(sum[e]);
+      }
+    }
   }
 }
 
@@ -583,8 +655,68 @@ __global__ __launch_bounds__(256) void gemm_simple_kernel(GemmParams p) {
     }
 }
 
+// How a prompt-sized product runs on the MFMA kernel: tile height and K split.
+struct PromptPlan {
+  bool wide;      // 16-bit 256 x 128 tiles
+  int tiles_m, tiles;
+  int ksplit, kt_per;
+  size_t ws_bytes;  // fp32 partials when split
+};
+
+// 16-bit: 256-row tiles (each B fragment feeds four MFMAs, 25% less operand
+// traffic per product) when they still give every CU at least four; fewer,
+// larger tiles leave CUs idle on the narrower products.  Measured at a
+// 2048-row Llama-3.2-3B prompt: gate/up 226 -> 219 us; q/k/v, o and down
+// (320 or fewer such tiles) were slower with them.
+//
+// K split (fp32): a CU's time is set by the items it runs, and a whole tile
+// is the unit, so 384 tiles on 256 CUs cost two tiles' time where 1.5 would
+// do.  Splitting K in S slices makes the unit 1 / S of a tile at the price of
+// a reduce pass over S fp32 partials; S (1..4, at least 4 stages per slice)
+// is the one with the least modelled time, and a split must win by 3%.
+// Measured at a 2048-row Llama-3.2-3B prompt, fp32: q/k/v 583 -> 520, o
+// 403 -> 317, down 1061 -> 805 us (S = 2).  16-bit products are not split:
+// at their speed the partials' traffic cost more than the balance gained
+// (bf16 down 118 -> 127 us with S = 2).
+PromptPlan prompt_plan(int m, int k, const GemmGroups& G, int esize) {
+  PromptPlan P{};
+  const int cus = tl_device_cus();
+  int wide_tiles = 0;
+  int64_t ncols = 0;
+  for (int g = 0; g < G.count; ++g) {
+    wide_tiles += ((m + 2 * kGmTile - 1) / (2 * kGmTile)) * ((G.n[g] + kGmTile - 1) / kGmTile);
+    ncols += G.n[g];
+  }
+  P.wide = esize == 2 && wide_tiles >= 4 * cus;
+  const int tm = P.wide ? 2 * kGmTile : kGmTile;
+  P.tiles_m = (m + tm - 1) / tm;
+  P.tiles = 0;
+  for (int g = 0; g < G.count; ++g) P.tiles += P.tiles_m * ((G.n[g] + kGmTile - 1) / kGmTile);
+  const int bk = esize == 2 ? (P.wide ? 32 : 64) : 16;  // k per LDS stage of the kernel used
+  const int n_kt = (k + bk - 1) / bk;
+  // modelled seconds: the product at a sustained rate, scaled by the busiest
+  // CU's share of items; the reduce as HBM traffic plus a launch
+  const double rate = esize == 2 ? 9.0e14 : 1.3e14;
+  const double t1 = 2.0 * m * (double)k * (double)ncols / rate;
+  auto busiest = [&](int S) { return (double)((P.tiles * (int64_t)S + cus - 1) / cus) / S; };
+  double best = t1;
+  P.ksplit = 1;
+  for (int S = 2; S <= 4 && esize == 4; ++S) {
+    if (n_kt < 4 * S) break;
+    const double t = t1 * busiest(S) / busiest(1) + ((double)S * 4 + esize) * m * (double)ncols / 5.0e12 + 3e-6;
+    if (t < 0.97 * best) {
+      best = t;
+      P.ksplit = S;
+    }
+  }
+  P.kt_per = (n_kt + P.ksplit - 1) / P.ksplit;
+  P.ws_bytes = P.ksplit > 1 ? (size_t)P.ksplit * m * ncols * sizeof(float) : 0;
+  return P;
+}
+
 template <typename T>
-int launch_gemm(const void* a, const GemmGroups& G, int m, int k, int64_t lda, hipStream_t st) {
+int launch_gemm(const void* a, const GemmGroups& G, int m, int k, int64_t lda, void* workspace,
+                size_t workspace_bytes, hipStream_t st) {
   GemmParams p{};
   p.a = a;
   p.m = m;
@@ -605,36 +737,44 @@ int launch_gemm(const void* a, const GemmGroups& G, int m, int k, int64_t lda, h
     widest = G.n[g] > widest ? G.n[g] : widest;
   }
   if (aligned) {
-    // 16-bit: 256-row tiles (each B fragment feeds four MFMAs, 25% less
-    // operand traffic per product) when they still give every CU at least
-    // four; fewer, larger tiles leave CUs idle on the narrower products.
-    // Measured at a 2048-row Llama-3.2-3B prompt: gate/up 226 -> 219 us;
-    // q/k/v, o and down (320 or fewer such tiles) were slower with them.
-    int wide_tiles = 0;
-    for (int g = 0; g < G.count; ++g) wide_tiles += ((m + 2 * kGmTile - 1) / (2 * kGmTile)) * ((G.n[g] + kGmTile - 1) / kGmTile);
-    const bool wide = T::size == 2 && wide_tiles >= 4 * tl_device_cus();
-    const int tm = wide ? 2 * kGmTile : kGmTile;
-    p.tiles_m = (m + tm - 1) / tm;
+    const PromptPlan P = prompt_plan(m, k, G, (int)esize);
+    p.tiles_m = P.tiles_m;
     p.G.tile0[0] = 0;
     p.vec_store = 0;
     for (int g = 0; g < G.count; ++g) {
       p.G.tile0[g + 1] = p.G.tile0[g] + p.tiles_m * ((G.n[g] + kGmTile - 1) / kGmTile);
       if (G.ldc[g] % 4 == 0 && ((uintptr_t)G.c[g] % (4 * esize)) == 0) p.vec_store |= 1 << g;
     }
-    p.per_xcd = (p.G.tile0[G.count] + 7) / 8;
+    // the split needs its partials' workspace; without it the product runs whole
+    const bool split = P.ksplit > 1 && workspace && workspace_bytes >= P.ws_bytes && ((uintptr_t)workspace % 16) == 0;
+    p.ksplit = split ? P.ksplit : 1;
+    p.kt_per = split ? P.kt_per : (k + 15) / 16 + 1;  // whole: one slice covers every stage
+    p.ws = (float*)workspace;
+    int64_t off = 0;
+    for (int g = 0; g < G.count; ++g) {
+      p.ws_off[g] = off;
+      off += (int64_t)p.ksplit * m * G.n[g];
+    }
+    p.per_xcd = (p.G.tile0[G.count] * p.ksplit + 7) / 8;
     // Measured at the models' prompt shapes (2048 rows): 16-bit runs best
     // with 64 k per stage in two stages (729 against 645 TFLOP/s with 32 k
     // in three, 691 with 32 k in four, 507 with 64 k in three); fp32 is
     // within 1% across those and keeps 16 k in three stages.
     const dim3 grid((unsigned)(8 * p.per_xcd));
     if constexpr (T::size == 2) {
-      if (wide)
+      if (P.wide)
         hipLaunchKernelGGL((gemm_mfma_kernel<T, 64, 3, 4>), grid, dim3(kGmThreads), 0, st, p);
       else
         hipLaunchKernelGGL((gemm_mfma_kernel<T, 128, 2, 2>), grid, dim3(kGmThreads), 0, st, p);
     } else {
       hipLaunchKernelGGL((gemm_mfma_kernel<T, 64, 3, 2>), grid, dim3(kGmThreads), 0, st, p);
     }
+    int e = tl_launch_status();
+    if (e || p.ksplit == 1) return e;
+    int64_t runs = 0;
+    for (int g = 0; g < G.count; ++g) runs = (int64_t)m * (G.n[g] / 4) > runs ? (int64_t)m * (G.n[g] / 4) : runs;
+    const unsigned rb = (unsigned)((runs + 255) / 256 < 4096 ? (runs + 255) / 256 : 4096);
+    hipLaunchKernelGGL((split_reduce_kernel<T>), dim3(rb, G.count), dim3(256), 0, st, p);
     return tl_launch_status();
   }
   dim3 grid((unsigned)((widest + 63) / 64), (unsigned)((m + 63) / 64), (unsigned)G.count);
@@ -717,19 +857,24 @@ int gemm_groups(const void* a, const GemmGroups& G, int m, int k, int64_t lda, v
     }
   }
   switch (dtype) {
-    case TL_DTYPE_F32: return launch_gemm<F32>(a, live, m, k, lda, st);
-    case TL_DTYPE_F16: return launch_gemm<F16>(a, live, m, k, lda, st);
-    default: return launch_gemm<BF16>(a, live, m, k, lda, st);
+    case TL_DTYPE_F32: return launch_gemm<F32>(a, live, m, k, lda, workspace, workspace_bytes, st);
+    case TL_DTYPE_F16: return launch_gemm<F16>(a, live, m, k, lda, workspace, workspace_bytes, st);
+    default: return launch_gemm<BF16>(a, live, m, k, lda, workspace, workspace_bytes, st);
   }
 }
 
 size_t groups_workspace_bytes(int m, int k, const GemmGroups& G, int dtype) {
-  if (m <= 0 || k <= 0 || m > kSkinnyMaxM) return 0;
+  if (m <= 0 || k <= 0) return 0;
   GemmGroups live{};
   for (int g = 0; g < G.count; ++g)
     if (G.n[g] > 0) live.n[live.count++] = G.n[g];
   if (live.count == 0) return 0;
-  return skinny_workspace_bytes(m, live, k, dtype == TL_DTYPE_F32 ? 4 : 2);
+  const int esize = dtype == TL_DTYPE_F32 ? 4 : 2;
+  // few rows: the K-slice partials; more: the MFMA kernel's split-K partials
+  // (if its plan splits; a product that falls back to the simple kernel
+  // uses none of it)
+  if (m <= kSkinnyMaxM) return skinny_workspace_bytes(m, live, k, esize);
+  return prompt_plan(m, k, live, esize).ws_bytes;
 }
 
 }  // namespace

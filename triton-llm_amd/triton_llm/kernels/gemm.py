@@ -27,8 +27,9 @@ def _workspace(nbytes: int):
 def gemm(h_dev: "gpu.DeviceTensor", w_dev: "gpu.DeviceTensor",
          out_dev: "gpu.DeviceTensor | None" = None, workspace=None) -> "gpu.DeviceTensor":
     """GPU-resident GEMM. No sync, no host copies.  ``workspace``: optional
-    device buffer of at least ``tl_gemm_workspace_bytes`` for the few-row
-    (decoded token) path; a module-wide buffer is used when omitted."""
+    device buffer of at least ``tl_gemm_workspace_bytes`` (the few-row path's
+    K-slice partials, or a split-K fp32 prompt's partials); a module-wide
+    buffer is used when omitted."""
     M, K = h_dev.shape
     K2, N = w_dev.shape
     assert K == K2, f"gemm shape mismatch: ({M},{K}) x ({K2},{N})"
