@@ -97,6 +97,31 @@ def test_prefill_seq_q_ne_seq_k(sq, sk, d_k):
     compare(f"sq{sq} sk{sk}", np.nan_to_num(got), np.nan_to_num(exp), TOL[dt])
 
 
+@pytest.mark.parametrize("d_k", [64, 128])
+@pytest.mark.parametrize("B,Hq,Hkv,sq,sk,causal", [
+    (1, 12, 12, 128, 128, True),   # GPT-2 prompt: 12 query blocks (key-split kernel)
+    (2, 6, 2, 37, 300, True),      # key-split, bottom-right causal, GQA
+    (1, 4, 2, 300, 129, True),     # key-split, the first rows fully masked
+    (1, 3, 3, 70, 70, False),      # key-split, non-causal, ragged
+    (1, 16, 4, 600, 600, True),    # 80 blocks of 128 rows: the tiled kernel
+    (1, 16, 16, 520, 520, False),  # tiled, non-causal
+])
+def test_prefill_fp32_paths(B, Hq, Hkv, sq, sk, causal, d_k):
+    """fp32 runs the key-split kernel when fewer than 64 blocks of 128 query
+    rows would run, the tiled kernel otherwise; both against the oracle."""
+    dt = "float32"
+    print(f"[case] fp32 B={B} Hq={Hq} Hkv={Hkv} sq={sq} sk={sk} D={d_k} causal={causal}", flush=True)
+    rng = np.random.default_rng(sq * 1000 + sk + d_k + Hq)
+    q = rng.standard_normal((B, Hq, sq, d_k), dtype=np.float32)
+    k = rng.standard_normal((B, Hkv, sk, d_k), dtype=np.float32)
+    v = rng.standard_normal((B, Hkv, sk, d_k), dtype=np.float32)
+    o = flash_attention(H.upload(q, dt), H.upload(k, dt), H.upload(v, dt), causal=causal)
+    got = H.download(o)
+    exp = oa.attention_bhsd(q, k, v, causal=causal, dtype=dt)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(exp))
+    compare(f"fp32 sq{sq} sk{sk} d{d_k}", np.nan_to_num(got), np.nan_to_num(exp), TOL[dt])
+
+
 @pytest.mark.parametrize("d_k", [16, 32, 256])
 def test_prefill_generic_head_sizes(d_k):
     dt = "float32"

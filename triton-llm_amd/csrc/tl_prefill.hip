@@ -904,6 +904,182 @@ __global__ __launch_bounds__(kThreads, D == 128 ? 1 : 2) void flash_fwd_f32(Flas
 }
 
 // ---------------------------------------------------------------------------
+// fp32 kernel for small problems: the key range of a 32-row block split over
+// the waves of a workgroup.  With few query blocks (GPT-2's 128-token
+// prompt: 12 heads x 128 rows), flash_fwd_f32 runs a few dozen waves, each a
+// serial chain of fp32 MFMAs over every key (v_mfma_f32_32x32x2f32 is 64
+// cycles): latency, not throughput.  Here workgroup (b, hq, row block) runs
+// 4 waves; wave w takes the 32-key chunks w, w + 4, ... of the block's keys,
+// with K and V read from global memory straight into MFMA operand layout
+// (no LDS tiles), and keeps its own online softmax state; at the end the
+// four states are merged through LDS (m* = max m_w, O = sum 2^(m_w - m*)
+// O_w / sum 2^(m_w - m*) l_w) and the block's rows are stored.
+// ---------------------------------------------------------------------------
+constexpr int KS_ROWS = 32;  // query rows per workgroup
+constexpr int KS_KEYS = 32;  // keys per chunk
+#ifndef KS_SMALL_GRID
+#define KS_SMALL_GRID 64
+#endif
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(kThreads) void flash_fwd_f32_ks(FlashParams p) {
+  constexpr int NDB = D / 32;
+  constexpr int NC = D / 8;  // 16-byte chunks per lane half
+  __shared__ float s_ml[4][2][KS_ROWS];
+  __shared__ f32x16 s_o[3][NDB][64];  // waves 1..3's O^T accumulators
+
+  const int n_rb = (p.seq_q + KS_ROWS - 1) / KS_ROWS;
+  const int rb = n_rb - 1 - (int)(blockIdx.x % n_rb);  // longest blocks first
+  const int hq = (int)(blockIdx.x / n_rb) % p.n_head;
+  const int b = (int)(blockIdx.x / n_rb) / p.n_head;
+  const int hkv = hq / p.group;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lq = lane & 31;
+  const int h = lane >> 5;
+  const int off = p.seq_k - p.seq_q;
+  const int q0 = rb * KS_ROWS;
+  const int qi = q0 + lq;
+  int k_end = p.seq_k;
+  if (CAUSAL) k_end = max(0, min(p.seq_k, min(q0 + KS_ROWS - 1, p.seq_q - 1) + off + 1));
+  const int n_ch = (k_end + KS_KEYS - 1) / KS_KEYS;
+
+  f32x4 qf[NC];
+  {
+    const float* qrow = (const float*)p.q + b * p.q_sb + hq * p.q_sh + (int64_t)min(qi, p.seq_q - 1) * p.q_ss;
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc) {
+      const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+      qf[cc] = qi < p.seq_q ? *(const f32x4*)(qrow + h * (D / 2) + 4 * cc) : z;
+    }
+  }
+  f32x16 o_acc[NDB];
+#pragma unroll
+  for (int i = 0; i < NDB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o_acc[i][r] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  const float* kbase = (const float*)p.k + b * p.k_sb + hkv * p.k_sh;
+  const float* vbase = (const float*)p.v + b * p.v_sb + hkv * p.v_sh;
+  const float c = p.scale_log2;
+  for (int ch = wave; ch < n_ch; ch += 4) {
+    const int kb = ch * KS_KEYS;
+    // K^T operand: lane (lq, h) holds key kb + lq, d = h D/2 + 4 cc + i;
+    // V^T operand of step r: key kb + 8 (r / 4) + 4 h + r % 4, d = 32 db + lq.
+    f32x4 kf[NC];
+    float vf[16][NDB];
+    {
+      const int key = kb + lq;
+      const float* krow = kbase + (int64_t)min(key, p.seq_k - 1) * p.k_ss + h * (D / 2);
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) {
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+        kf[cc] = key < p.seq_k ? *(const f32x4*)(krow + 4 * cc) : z;
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kv = kb + 8 * (r >> 2) + 4 * h + (r & 3);
+        const float* vrow = vbase + (int64_t)min(kv, p.seq_k - 1) * p.v_ss + lq;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) vf[r][db] = kv < p.seq_k ? vrow[32 * db] : 0.f;
+      }
+    }
+    f32x16 s;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = 0.f;
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[cc][i], qf[cc][i], s, 0, 0, 0);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = kb + 8 * (r >> 2) + 4 * h + (r & 3);
+      const bool ok = key < p.seq_k && (!CAUSAL || key <= qi + off);
+      const float x = ok ? s[r] * c : -INFINITY;
+      s[r] = x;
+      mx = fmaxf(mx, x);
+    }
+    mx = fmaxf(mx, xor32(mx));
+    const float m_new = fmaxf(m_run, mx);
+    const float base = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = fast_exp2(m_run - base);
+    m_run = m_new;
+    l_run *= alpha;
+#pragma unroll
+    for (int i = 0; i < NDB; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o_acc[i][r] *= alpha;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float e = fast_exp2(s[r] - base);
+      s[r] = e;
+      l_run += e;
+    }
+    // O^T += V^T . P^T: step r uses key 8 (r / 4) + 4 h + r % 4 of the chunk
+    // in lane half h (MFMA k = h), so P^T is the lane's own S value.
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) o_acc[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[r][db], s[r], o_acc[db], 0, 0, 0);
+  }
+
+  // Merge the four waves' states (a wave with no chunk has m = -inf, l = 0).
+  const float l_row = l_run + xor32(l_run);  // both lane halves hold the row's max
+  if (h == 0) {
+    s_ml[wave][0][lq] = m_run;
+    s_ml[wave][1][lq] = l_row;
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) s_o[wave - 1][db][lane] = o_acc[db];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float mw[4];
+  float ms = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    mw[w] = s_ml[w][0][lq];
+    ms = fmaxf(ms, mw[w]);
+  }
+  const float mb = (ms == -INFINITY) ? 0.f : ms;
+  float wt[4], lsum = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    wt[w] = fast_exp2(mw[w] - mb);
+    lsum += wt[w] * s_ml[w][1][lq];
+  }
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+    f32x16 a = o_acc[db];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) a[r] *= wt[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) {
+      const f32x16 ow = s_o[w - 1][db][lane];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) a[r] += wt[w] * ow[r];
+    }
+    o_acc[db] = a;
+  }
+  const float inv = 1.f / lsum;
+  if (qi < p.seq_q) {
+    float* orow = (float*)p.o + b * p.o_sb + hq * p.o_sh + (int64_t)qi * p.o_ss;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d0 = 32 * db + 8 * rq + 4 * h;
+        const f32x4 v = {o_acc[db][4 * rq] * inv, o_acc[db][4 * rq + 1] * inv, o_acc[db][4 * rq + 2] * inv,
+                         o_acc[db][4 * rq + 3] * inv};
+        *(f32x4*)(orow + d0) = v;
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // V (b, kv, s, d) -> V^T (b, kv, d, s_pad), s_pad a multiple of 128, keys past
 // seq_k zero-filled.  Within each group of 16 keys the stored order is
 //     position 16 u + 8 h + j  <-  key 16 u + 8 (j / 4) + 4 h + (j % 4)
@@ -1082,7 +1258,17 @@ int launch_flash_16(FlashParams& p, void* ws, bool causal, hipStream_t st) {
 template <int D>
 int launch_flash_f32(FlashParams& p, bool causal, hipStream_t st) {
   p.n_qt = (p.seq_q + BM - 1) / BM;
-  dim3 grid((unsigned)(p.n_qt * p.n_head * p.batch));
+  const int64_t blocks = (int64_t)p.n_qt * p.n_head * p.batch;
+  if (blocks < KS_SMALL_GRID) {
+    // few 128-row blocks: split each 32-row block's keys over 4 waves
+    dim3 g((unsigned)((int64_t)((p.seq_q + KS_ROWS - 1) / KS_ROWS) * p.n_head * p.batch));
+    if (causal)
+      hipLaunchKernelGGL((flash_fwd_f32_ks<D, true>), g, dim3(kThreads), 0, st, p);
+    else
+      hipLaunchKernelGGL((flash_fwd_f32_ks<D, false>), g, dim3(kThreads), 0, st, p);
+    return tl_launch_status();
+  }
+  dim3 grid((unsigned)blocks);
   if (causal)
     hipLaunchKernelGGL((flash_fwd_f32<D, true>), grid, dim3(kThreads), 0, st, p);
   else
