@@ -436,6 +436,16 @@ def cpu_decode_baseline(cfg, data, oa, on, budget_s=10.0):
 # prefill
 # ---------------------------------------------------------------------------
 
+def prefill_kernel_name(cfg):
+    """The kernels tl_attention_fwd runs for a prefill config: fp32 takes the
+    key-split kernel when fewer than 64 blocks of 128 query rows would run;
+    16-bit d_k 128 reads V through the vt_pack copy."""
+    if cfg.dtype == "float32":
+        blocks = -(-cfg.seq // 128) * cfg.n_head * cfg.batch
+        return "flash_fwd_f32_ks" if blocks < 64 else "flash_fwd_f32"
+    return "flash_fwd_16 + vt_pack_kernel" if cfg.d_k == 128 else "flash_fwd_16"
+
+
 def bench_prefill(cfg, steps, warmup, replicas=1, cpu=True, cpu_budget_s=10.0, ramp_ms=0.0):
     from oracle import attention as oa
     from oracle import inputs as oi
@@ -489,8 +499,7 @@ def bench_prefill(cfg, steps, warmup, replicas=1, cpu=True, cpu_budget_s=10.0, r
         "clock_ramp": {"calls": ramp[0], "ms": round(ramp[1], 1)},
         "roofline": {
             "bound": "mfma",
-            "kernel": ("flash_fwd_f32 (tl_attention_fwd)" if dt == "float32"
-                       else "flash_fwd_16 + vt_pack_kernel (tl_attention_fwd)"),
+            "kernel": prefill_kernel_name(cfg) + " (tl_attention_fwd)",
             "achieved": tf,
             "peak": peak,
             "unit": "TFLOP/s",

@@ -925,7 +925,7 @@ __global__ __launch_bounds__(kThreads) void flash_fwd_f32_ks(FlashParams p) {
   constexpr int NDB = D / 32;
   constexpr int NC = D / 8;  // 16-byte chunks per lane half
   __shared__ float s_ml[4][2][KS_ROWS];
-  __shared__ f32x16 s_o[3][NDB][64];  // waves 1..3's O^T accumulators
+  __shared__ float s_o[3][NDB][16][64];  // waves 1..3's O^T accumulators, lane-minor (no bank conflicts)
 
   const int n_rb = (p.seq_q + KS_ROWS - 1) / KS_ROWS;
   const int rb = n_rb - 1 - (int)(blockIdx.x % n_rb);  // longest blocks first
@@ -1033,7 +1033,9 @@ __global__ __launch_bounds__(kThreads) void flash_fwd_f32_ks(FlashParams p) {
   }
   if (wave > 0) {
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) s_o[wave - 1][db][lane] = o_acc[db];
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s_o[wave - 1][db][r][lane] = o_acc[db][r];
   }
   __syncthreads();
   if (wave != 0) return;
@@ -1058,9 +1060,8 @@ __global__ __launch_bounds__(kThreads) void flash_fwd_f32_ks(FlashParams p) {
     for (int r = 0; r < 16; ++r) a[r] *= wt[0];
 #pragma unroll
     for (int w = 1; w < 4; ++w) {
-      const f32x16 ow = s_o[w - 1][db][lane];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) a[r] += wt[w] * ow[r];
+      for (int r = 0; r < 16; ++r) a[r] += wt[w] * s_o[w - 1][db][r][lane];
     }
     o_acc[db] = a;
   }
