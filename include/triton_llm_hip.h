@@ -140,7 +140,11 @@ int tl_attention_fwd(const void* q, const void* k, const void* v, void* o,
  * Launches the split pass, then a combine pass that merges the partials of
  * heads whose positions were shared by several workgroups and writes zeros
  * for empty sequences.  The workspace holds the partials and may be reused
- * by consecutive calls on one stream.
+ * by consecutive calls on one stream.  Small caches (max_ctx <= 2048 and at
+ * most 64 MiB of K and V) instead run one workgroup per (sequence, KV head)
+ * that finishes its heads itself: one launch, no partials, split_size and
+ * the workspace unused (the environment variable
+ * TRITON_LLM_HIP_DECODE_SHARES=1 forces the shares path).
  * ------------------------------------------------------------------------- */
 int tl_decode_split_size(int batch, int n_kv_head, int max_ctx);
 size_t tl_attention_decode_workspace_bytes(int batch, int n_head, int max_ctx,

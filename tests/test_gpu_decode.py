@@ -18,6 +18,20 @@ pytestmark = pytest.mark.gpu
 
 TOL = {"float32": 2e-3, "float16": 2e-2, "bfloat16": 2e-2}
 
+# Small caches (max_ctx <= 2048, <= 64 MiB of K/V) run one workgroup per
+# (sequence, KV head) that finishes its pair ("pair"); larger ones equal
+# shares of all positions plus a combine ("shares").  This variable forces
+# the shares path, so the edge cases below run on both.
+SHARES_ENV = "TRITON_LLM_HIP_DECODE_SHARES"
+MODES = ["pair", "shares"]
+
+
+def set_mode(monkeypatch, mode):
+    if mode == "shares":
+        monkeypatch.setenv(SHARES_ENV, "1")
+    else:
+        monkeypatch.delenv(SHARES_ENV, raising=False)
+
 
 def run_decode_step(cfg, data, batches=None, split=0):
     """GPU: append (+RoPE) then attend over len + 1.  Oracle on the same inputs.
@@ -81,9 +95,11 @@ def test_decode_config_5b_full_size_sampled():
     compare("config5b", got, exp, TOL[cfg.dtype], batches)
 
 
+@pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
 @pytest.mark.parametrize("group,d_k", [(1, 64), (3, 128), (4, 64), (8, 128), (12, 64)])
-def test_decode_shapes_and_dtypes(dtype, group, d_k):
+def test_decode_shapes_and_dtypes(monkeypatch, mode, dtype, group, d_k):
+    set_mode(monkeypatch, mode)
     Hkv = 2
     cfg = oi.Config("decode-edge", "decode", dtype, 5, Hkv * group, Hkv, d_k, 11, 0.3,
                     max_ctx=300, lo=0, hi=299, rope_theta=1e4)
@@ -91,10 +107,12 @@ def test_decode_shapes_and_dtypes(dtype, group, d_k):
     lens[:3] = [0, 299, 15]  # empty prefix, full cache, short
     data = oi.make_decode(cfg, fill="nan", lens=lens)
     got, exp, _, _ = run_decode_step(cfg, data, split=32)
-    compare(f"edge {dtype} g{group} d{d_k}", got, exp, TOL[dtype])
+    compare(f"edge {mode} {dtype} g{group} d{d_k}", got, exp, TOL[dtype])
 
 
-def test_decode_without_append_and_len_zero_gives_zeros():
+@pytest.mark.parametrize("mode", MODES)
+def test_decode_without_append_and_len_zero_gives_zeros(monkeypatch, mode):
+    set_mode(monkeypatch, mode)
     dt = "bfloat16"
     cfg = oi.Config("decode-noappend", "decode", dt, 4, 6, 2, 64, 5, 0.125, max_ctx=128, lo=1, hi=127)
     lens = oi.draw_lens(cfg)
@@ -110,7 +128,8 @@ def test_decode_without_append_and_len_zero_gives_zeros():
 
 
 @pytest.mark.parametrize("split", [16, 64, 256, 2048])
-def test_decode_split_sizes_agree(split):
+def test_decode_split_sizes_agree(monkeypatch, split):
+    monkeypatch.setenv(SHARES_ENV, "1")  # split sizes apply to the shares path
     cfg = oi.scaled(oi.CONFIGS["4"], batch=6, max_ctx=2048, lo=1, hi=2047)
     data = oi.make_decode(cfg, fill="nan")
     got, exp, _, _ = run_decode_step(cfg, data, split=split)
@@ -125,6 +144,7 @@ def test_decode_few_workgroups_span_many_sequences(monkeypatch, cus, batch):
     scan in several chunks.  Some sequences hold only the appended token, one
     fills the cache."""
     monkeypatch.setenv("TRITON_LLM_HIP_MAX_CUS", str(cus))
+    monkeypatch.setenv(SHARES_ENV, "1")
     cfg = oi.scaled(oi.CONFIGS["4"], batch=batch, max_ctx=640, lo=0, hi=639)
     lens = oi.draw_lens(cfg)
     lens[: min(4, batch)] = [0, 639, 1, 0][: min(4, batch)]
@@ -133,10 +153,13 @@ def test_decode_few_workgroups_span_many_sequences(monkeypatch, cus, batch):
     compare(f"cus{cus} b{batch}", got, exp, TOL[cfg.dtype])
 
 
-def test_decode_all_sequences_empty_over_64():
-    """Every length 0 (no append): the split kernel finds no positions and
-    exits; the combine writes zeros for all heads.  70 sequences take the
-    lengths scan in two chunks."""
+@pytest.mark.parametrize("mode", MODES)
+def test_decode_all_sequences_empty_over_64(monkeypatch, mode):
+    """Every length 0 (no append).  Shares: the split kernel finds no
+    positions and exits, the combine writes zeros for all heads, and 70
+    sequences take the lengths scan in two chunks.  Pair: each workgroup
+    finds an empty pair and writes its zeros."""
+    set_mode(monkeypatch, mode)
     dt = "bfloat16"
     cfg = oi.Config("decode-empty", "decode", dt, 70, 6, 2, 64, 5, 0.125, max_ctx=64, lo=0, hi=0)
     lens = np.zeros(70, np.int32)

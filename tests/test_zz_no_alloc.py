@@ -25,6 +25,13 @@ TOL = {"float32": 2e-3, "float16": 2e-2, "bfloat16": 2e-2}
 CODE = {"float32": _lib.DTYPE_F32, "float16": _lib.DTYPE_F16, "bfloat16": _lib.DTYPE_BF16}
 
 
+@pytest.fixture(autouse=True)
+def _shares_path(monkeypatch):
+    """Small caches would take the pair path, which writes no partials; the
+    equal-shares path is the one whose partials live in the static scratch."""
+    monkeypatch.setenv("TRITON_LLM_HIP_DECODE_SHARES", "1")
+
+
 def _run_both(cfg):
     dt = cfg.dtype
     B, Hq, Hkv, D, C = cfg.batch, cfg.n_head, cfg.n_kv_head, cfg.d_k, cfg.max_ctx

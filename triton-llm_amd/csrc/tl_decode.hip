@@ -19,6 +19,14 @@
 // reach 6.5 TB/s.)  A share may end inside one pair and continue into the
 // next; each piece is a segment with its own softmax state.
 //
+// Small caches (max_ctx <= 2048 and at most 64 MiB of K/V, e.g. GPT-2's
+// 1024-position cache) are latency-bound instead: a few MB spread over a
+// thousand shares cost a combine launch and dependent loads for little
+// streaming.  There one 16-wave workgroup (64 key streams, 8 keys each per
+// iteration) takes a whole (sequence, pair), finishes it and writes its
+// output (zeros for an empty sequence), and no combine runs (GPT-2 decode
+// 14.5 -> 9.8 us).
+//
 // The pass is HBM-bound (every K/V byte is read exactly once), so the design
 // goal is to keep the VALU work per byte well under the issue budget:
 //   * a key row (d_k elements) is read by 16 consecutive lanes with one
@@ -45,6 +53,7 @@
 #include "tl_common.h"
 
 #include <math.h>
+#include <stdlib.h>
 
 #include <mutex>
 
@@ -52,10 +61,15 @@
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kStreams = 16;  // lane-groups per workgroup
+constexpr int kThreads = 256;  // equal-share workgroups: 4 waves
+constexpr int kPairUnroll = 8;  // pair mode, small lane state: keys in flight per stream (4 and 16 measured slower)
+// pair-mode workgroups: 16 waves while a lane's state (G heads x D / 16
+// elements) fits the 128 VGPRs of a 1024-thread workgroup, else 8
+template <typename T, int D, int G>
+constexpr int pair_waves() { return D * G * T::size <= 512 ? 16 : 8; }
+constexpr int kPairMaxCtx = 2048;                  // pair mode: max_ctx at most
+constexpr int64_t kPairMaxBytes = 64ll << 20;      // pair mode: K/V cache bytes at most
 constexpr int kUnroll = 4;    // keys in flight per stream
-constexpr int kKeysPerIter = kStreams * kUnroll;
 constexpr float kRescaleLog2 = 8.f;
 constexpr int kAuxNontemporal = 2;  // buffer-load cache policy: nt
 
@@ -269,11 +283,20 @@ __device__ __forceinline__ void set_progress_priority(int64_t done, int64_t shar
   else __builtin_amdgcn_s_setprio(0);
 }
 
-// G: query heads of one (kv head, chunk) pair (<= group).
-template <typename T, int D, int G>
-__global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p) {
+// G: query heads of one (kv head, chunk) pair (<= group).  NW: waves per
+// workgroup (4 streams each).  PAIR: the pair-aligned mode for small caches
+// -- workgroup i streams all of pair i % n_pairs of sequence i / n_pairs and
+// finishes it (no partials, no combine launch); otherwise equal shares.
+template <typename T, int D, int G, int NW, bool PAIR>
+__global__ __launch_bounds__(64 * NW) void decode_split_kernel(DecodeParams p) {
   constexpr int EPL = D / 16;           // elements per lane per row
   constexpr int W = EPL * T::size / 4;  // 32-bit words per lane per row
+  constexpr int kThr = 64 * NW;
+  constexpr int kStr = 4 * NW;          // key streams (16-lane groups)
+  // keys in flight per stream: a pair workgroup streams its whole pair, so
+  // it takes more per iteration where a lane's state is small
+  constexpr int kU = PAIR && D * G * T::size <= 256 ? kPairUnroll : kUnroll;
+  constexpr int kKPI = kStr * kU;       // keys per iteration
   using Bits = typename T::bits;
 
   const int tid = threadIdx.x;
@@ -283,36 +306,19 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p) 
   const int stream = wave * 4 + (lane >> 4);
   const int n_chunks = p.n_pairs / p.n_kv;
 
-  const SeqScan scan = scan_first64(p, lane);
-  const bool in_regs = p.batch <= 64;
-  const int64_t total = in_regs ? uniform(__shfl(scan.incl, 63)) : total_rows(p, lane);
-  const int64_t rpb = uniform(rows_per_block(p, total));
-  const int64_t r0 = (int64_t)blockIdx.x * rpb;
-  if (r0 >= total) return;
-  const int64_t r1 = r0 + rpb < total ? r0 + rpb : total;
-
-  __shared__ float s_m[4][G], s_l[4][G];
-  __shared__ float s_acc[4][G][D];
+  __shared__ float s_m[NW][G], s_l[NW][G];
+  __shared__ float s_acc[NW][G][D];
   const uint32_t lane_bytes = sub * (EPL * T::size);
   const float c = p.scale_log2;
 
-  for (int64_t r = r0; r < r1;) {
-    // The segment [r, seg_end) of this workgroup's rows lies in one pair.
-    const SeqPos sp = in_regs ? locate_in(scan, r, p.n_pairs) : locate_row(p, r, lane);
-    const int b = sp.b;
-    const int pair = uniform((int)((r - sp.start) / sp.ctx));
-    const int64_t pair_row0 = sp.start + (int64_t)pair * sp.ctx;
-    const int start = (int)(r - pair_row0);
-    const int end = (int)((r1 - pair_row0) < sp.ctx ? (r1 - pair_row0) : sp.ctx);
-    r = pair_row0 + end;
+  // One segment: positions [start, end) of pair `pair` of sequence b (ctx
+  // positions).  whole: the pair lies in this workgroup alone, so its output
+  // is finished here; otherwise the partial goes to slot `slot`.
+  auto segment = [&](const int b, const int ctx, const int pair, const int start, const int end,
+                     const bool whole, const int slot, const int64_t seg_done0, const int64_t share) {
     const int hkv = pair / n_chunks;
     const int hq0 = hkv * p.group + (pair - hkv * n_chunks) * G;
     const int n_g = min(G, hkv * p.group + p.group - hq0);  // heads valid in this pair
-    // Workgroups covering this pair: the partial of this one goes to slot
-    // blockIdx.x - first; a pair inside one workgroup is finished here.
-    const int64_t first = uniform((int64_t)(pair_row0 / rpb));
-    const bool whole = uniform((int)((pair_row0 + sp.ctx - 1) / rpb - first)) == 0;
-    const int slot = (int)(blockIdx.x - first);
 
     // Query slices of the G heads, kept in storage format.
     Slice<W> qs[G];
@@ -336,14 +342,14 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p) 
     const __amdgpu_buffer_rsrc_t krs = make_rsrc((const Bits*)p.k + b * p.k_sb + hkv * p.k_sh, p.k_region_bytes);
     const __amdgpu_buffer_rsrc_t vrs = make_rsrc((const Bits*)p.v + b * p.v_sb + hkv * p.v_sh, p.v_region_bytes);
 
-    // One iteration: kUnroll keys per stream, 64 per workgroup.
+    // One iteration: kU keys per stream, kKPI per workgroup.
     auto iteration = [&](int key0, auto masked) {
       constexpr bool kMasked = decltype(masked)::value;
-      Slice<W> kr[kUnroll], vr[kUnroll];
-      bool valid[kUnroll];
+      Slice<W> kr[kU], vr[kU];
+      bool valid[kU];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int key = key0 + u * kStreams;
+      for (int u = 0; u < kU; ++u) {
+        const int key = key0 + u * kStr;
         if constexpr (kMasked) {
           // Out-of-range keys re-read this segment's first row (always
           // inside the sequence) and are masked out of the softmax below.
@@ -353,13 +359,13 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p) 
           load_slice(vr[u], vrs, row * p.v_row_bytes + lane_bytes, 0);
         } else {
           valid[u] = true;
-          load_slice(kr[u], krs, (uint32_t)key0 * p.k_row_bytes + lane_bytes, u * kStreams * p.k_row_bytes);
-          load_slice(vr[u], vrs, (uint32_t)key0 * p.v_row_bytes + lane_bytes, u * kStreams * p.v_row_bytes);
+          load_slice(kr[u], krs, (uint32_t)key0 * p.k_row_bytes + lane_bytes, u * kStr * p.k_row_bytes);
+          load_slice(vr[u], vrs, (uint32_t)key0 * p.v_row_bytes + lane_bytes, u * kStr * p.v_row_bytes);
         }
       }
-      float s[G][kUnroll];
+      float s[G][kU];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
+      for (int u = 0; u < kU; ++u) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
           const float d = row16_sum(dot_slice<T>(qs[g], kr[u])) * c;
@@ -374,7 +380,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p) 
       for (int g = 0; g < G; ++g) {
         mb[g] = s[g][0];
 #pragma unroll
-        for (int u = 1; u < kUnroll; ++u) mb[g] = fmaxf(mb[g], s[g][u]);
+        for (int u = 1; u < kU; ++u) mb[g] = fmaxf(mb[g], s[g][u]);
         grow |= mb[g] > m[g] + kRescaleLog2;
       }
       if (__any(grow)) {
@@ -388,18 +394,18 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p) 
           for (int e = 0; e < EPL; ++e) acc[g][e] *= alpha;
         }
       }
-      float pu[G][kUnroll];
+      float pu[G][kU];
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         const float base = (m[g] == -INFINITY) ? 0.f : m[g];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
+        for (int u = 0; u < kU; ++u) {
           pu[g][u] = fast_exp2(s[g][u] - base);
           l[g] += pu[g][u];
         }
       }
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
+      for (int u = 0; u < kU; ++u) {
         float vf[EPL];
         slice_to_float<T>(vr[u], vf);
 #pragma unroll
@@ -409,14 +415,15 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p) 
       }
     };
 
-    const int n_full = (end - start) / kKeysPerIter;
+    const int n_full = (end - start) / kKPI;
     int key0 = start + stream;
-    const int64_t seg_done0 = pair_row0 + start - r0;  // positions of the share already done
-    for (int it = 0; it < n_full; ++it, key0 += kKeysPerIter) {
-      if ((it & 3) == 0) set_progress_priority(seg_done0 + (int64_t)it * kKeysPerIter, r1 - r0);
+    for (int it = 0; it < n_full; ++it, key0 += kKPI) {
+      if constexpr (!PAIR) {
+        if ((it & 3) == 0) set_progress_priority(seg_done0 + (int64_t)it * kKPI, share);
+      }
       iteration(key0, std::false_type{});
     }
-    if (start + n_full * kKeysPerIter < end) iteration(key0, std::true_type{});
+    if (start + n_full * kKPI < end) iteration(key0, std::true_type{});
 
     // Merge the 4 streams of this wave (lane groups 16 apart).
 #pragma unroll
@@ -437,7 +444,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p) 
       }
     }
 
-    // Merge the 4 waves through LDS (the barrier in front protects the
+    // Merge the NW waves through LDS (the barrier in front protects the
     // previous segment's reads of the same arrays).
     __syncthreads();
     if (lane < 16) {
@@ -453,22 +460,23 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p) 
     }
     __syncthreads();
     const int64_t row_base = ((int64_t)b * p.n_head + hq0) * p.max_slots;
-    for (int idx = tid; idx < n_g * D; idx += kThreads) {
+    for (int idx = tid; idx < n_g * D; idx += kThr) {
       const int g = idx / D;
       const int d = idx - g * D;
       float mx = -INFINITY;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) mx = fmaxf(mx, s_m[w][g]);
+      for (int w = 0; w < NW; ++w) mx = fmaxf(mx, s_m[w][g]);
       const float base = (mx == -INFINITY) ? 0.f : mx;
       float a = 0.f, lsum = 0.f;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
+      for (int w = 0; w < NW; ++w) {
         const float wt = fast_exp2(s_m[w][g] - base);
         a += s_acc[w][g][d] * wt;
         lsum += s_l[w][g] * wt;
       }
       if (whole) {
-        store_out<T>(p.o, b * p.o_sb + (int64_t)(hq0 + g) * p.o_sh + d, a / lsum);
+        // (an empty sequence reads as zeros, the reference's empty-KV result)
+        store_out<T>(p.o, b * p.o_sb + (int64_t)(hq0 + g) * p.o_sh + d, ctx == 0 ? 0.f : a / lsum);
       } else {
         const int64_t row = row_base + (int64_t)g * p.max_slots + slot;
         p.ws_acc[row * D + d] = a;
@@ -477,6 +485,36 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p) 
           p.ws_ml[row * 2 + 1] = lsum;
         }
       }
+    }
+  };
+
+  if constexpr (PAIR) {
+    const int b = (int)blockIdx.x / p.n_pairs;
+    const int pair = (int)blockIdx.x - b * p.n_pairs;
+    const int ctx = uniform(ctx_len(p, b));
+    segment(b, ctx, pair, 0, ctx, true, 0, 0, 0);
+  } else {
+    const SeqScan scan = scan_first64(p, lane);
+    const bool in_regs = p.batch <= 64;
+    const int64_t total = in_regs ? uniform(__shfl(scan.incl, 63)) : total_rows(p, lane);
+    const int64_t rpb = uniform(rows_per_block(p, total));
+    const int64_t r0 = (int64_t)blockIdx.x * rpb;
+    if (r0 >= total) return;
+    const int64_t r1 = r0 + rpb < total ? r0 + rpb : total;
+    for (int64_t r = r0; r < r1;) {
+      // The segment [r, seg_end) of this workgroup's rows lies in one pair.
+      const SeqPos sp = in_regs ? locate_in(scan, r, p.n_pairs) : locate_row(p, r, lane);
+      const int pair = uniform((int)((r - sp.start) / sp.ctx));
+      const int64_t pair_row0 = sp.start + (int64_t)pair * sp.ctx;
+      const int start = (int)(r - pair_row0);
+      const int end = (int)((r1 - pair_row0) < sp.ctx ? (r1 - pair_row0) : sp.ctx);
+      r = pair_row0 + end;
+      // Workgroups covering this pair: the partial of this one goes to slot
+      // blockIdx.x - first; a pair inside one workgroup is finished here.
+      const int64_t first = uniform((int64_t)(pair_row0 / rpb));
+      const bool whole = uniform((int)((pair_row0 + sp.ctx - 1) / rpb - first)) == 0;
+      const int slot = (int)(blockIdx.x - first);
+      segment(sp.b, sp.ctx, pair, start, end, whole, slot, pair_row0 + start - r0, r1 - r0);
     }
   }
 }
@@ -574,12 +612,28 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
 
 template <typename T, int D, int G>
 int launch_decode_g(DecodeParams& p, hipStream_t st) {
+  // Small caches: one 16-wave workgroup per (sequence, pair), which finishes
+  // the pair itself -- no partials and no combine launch.  The cache bound
+  // is known on the host (max_ctx), the lengths are not: pair mode needs a
+  // short max_ctx (a workgroup streams its pair in a few iterations of 256
+  // keys) and a small whole cache (no equal-share spreading needed).
+  // (TRITON_LLM_HIP_DECODE_SHARES set to a nonzero value forces the shares,
+  // so tests can run both paths on the same small inputs.)
+  const int64_t cache_bytes = (int64_t)p.batch * p.n_pairs * p.max_ctx * 2 * D * T::size;
+  const char* force = getenv("TRITON_LLM_HIP_DECODE_SHARES");
+  const bool shares = force && atoi(force) != 0;
+  if (!shares && p.max_ctx <= kPairMaxCtx && cache_bytes <= kPairMaxBytes) {
+    p.n_blocks = p.batch * p.n_pairs;
+    constexpr int NW = pair_waves<T, D, G>();
+    hipLaunchKernelGGL((decode_split_kernel<T, D, G, NW, true>), dim3(p.n_blocks), dim3(64 * NW), 0, st, p);
+    return tl_launch_status();
+  }
   // One workgroup per resident slot (occupancy x compute units), never more
   // than the shares of min_share positions a full cache would hold.
   static int per_cu = 0;
   if (per_cu == 0) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_split_kernel<T, D, G>, kThreads, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_split_kernel<T, D, G, 4, false>, kThreads, 0) !=
             hipSuccess ||
         n <= 0)
       n = 1;
@@ -588,7 +642,7 @@ int launch_decode_g(DecodeParams& p, hipStream_t st) {
   const int64_t most = ((int64_t)p.batch * p.n_pairs * p.max_ctx + p.min_share - 1) / p.min_share;
   const int64_t slots = (int64_t)per_cu * tl_device_cus();
   p.n_blocks = (int)(most < slots ? most : slots);
-  hipLaunchKernelGGL((decode_split_kernel<T, D, G>), dim3(p.n_blocks), dim3(kThreads), 0, st, p);
+  hipLaunchKernelGGL((decode_split_kernel<T, D, G, 4, false>), dim3(p.n_blocks), dim3(kThreads), 0, st, p);
   int e = tl_launch_status();
   if (e) return e;
   hipLaunchKernelGGL((decode_combine_kernel<T, D>), dim3(p.n_head, p.batch), dim3(64), 0, st, p);
