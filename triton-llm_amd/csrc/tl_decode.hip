@@ -25,7 +25,7 @@
 // streaming.  There one 16-wave workgroup (64 key streams, 8 keys each per
 // iteration) takes a whole (sequence, pair), finishes it and writes its
 // output (zeros for an empty sequence), and no combine runs (GPT-2 decode
-// 14.5 -> 9.8 us).
+// 14.5 -> 9.7 us).
 //
 // The pass is HBM-bound (every K/V byte is read exactly once), so the design
 // goal is to keep the VALU work per byte well under the issue budget:
