@@ -202,22 +202,61 @@ def test_gemm_prompt_split_k(dtype, M, K, Ns):
             np.testing.assert_allclose(got, exp, rtol=8e-3, atol=1e-2)
 
 
-def test_gemm_prompt_split_k_without_workspace_runs_whole():
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
+@pytest.mark.parametrize("M,K,Ns", [(9, 3072, (3072,)), (33, 3072, (3072, 1024, 1024)), (64, 8192, (3072,)),
+                                    (130, 3072, (8192, 8192)), (17, 3000, (3000,))])
+def test_gemm_few_rows_split_k(dtype, M, K, Ns):
+    """A batch of decoded tokens (9 to a few hundred rows): the MFMA product
+    has only a few dozen tiles of C, so K is split until about two items per
+    CU run (fp32 partials in the workspace, one reduce pass rounding to the
+    output type); ragged M, a K tail, slices past K, the grouped form.  The
+    workspace query reports the partials, so these shapes take the split path."""
+    print(f"[case] gemm few-rows split-k {dtype} {M}x{K} -> {Ns}", flush=True)
+    lib = gpu.runtime()
+    code = gpu.dtype_code(H.GPU_DTYPES[dtype])
+    n_arr = (ctypes.c_int * len(Ns))(*Ns)
+    assert lib.tl_gemm_grouped_workspace_bytes(M, K, len(Ns), n_arr, code) >= 2 * M * sum(Ns) * 4
+    rng = np.random.default_rng(M + K + sum(Ns))
+    a = on.to_storage(rng.standard_normal((M, K), dtype=np.float32), dtype)
+    bs = [on.to_storage(rng.standard_normal((K, n), dtype=np.float32) / np.sqrt(K), dtype) for n in Ns]
+    a_dev = H.upload(a, dtype)
+    if len(Ns) == 1:
+        outs = [gemm(a_dev, H.upload(bs[0], dtype))]
+    else:
+        outs = gemm_grouped(a_dev, [H.upload(b, dtype) for b in bs])
+    for b, o in zip(bs, outs):
+        got = on.from_storage(H.download(o), dtype)
+        exp = gemm_ref(on.from_storage(a, dtype), on.from_storage(b, dtype))
+        if dtype == "float32":
+            err = H.max_abs(got, exp)
+            H.report(f"few-rows split-k {dtype} {M}x{K}@{K}x{b.shape[1]}", err, 2e-3)
+            assert err <= 2e-3
+        else:
+            np.testing.assert_allclose(got, exp, rtol=8e-3, atol=1e-2)
+
+
+@pytest.mark.parametrize("dtype,M", [("float32", 2048), ("float32", 40), ("bfloat16", 64)])
+def test_gemm_prompt_split_k_without_workspace_runs_whole(dtype, M):
     """The C ABI with no workspace for a shape its plan would split: the
     product runs with whole-K tiles instead (no failure, same result)."""
     lib = gpu.runtime()
-    M, K, N = 2048, 3072, 3072
-    code = gpu.dtype_code(np.float32)
+    K, N = 3072, 3072
+    code = gpu.dtype_code(H.GPU_DTYPES[dtype])
     assert lib.tl_gemm_workspace_bytes(M, N, K, code) > 0
-    rng = np.random.default_rng(5)
-    a = rng.standard_normal((M, K), dtype=np.float32)
-    b = (rng.standard_normal((K, N), dtype=np.float32) / np.sqrt(K)).astype(np.float32)
-    a_dev, b_dev = H.upload(a), H.upload(b)
-    c_dev = gpu.allocate((M, N), np.float32)
+    rng = np.random.default_rng(5 + M)
+    a = on.to_storage(rng.standard_normal((M, K), dtype=np.float32), dtype)
+    b = on.to_storage(rng.standard_normal((K, N), dtype=np.float32) / np.sqrt(K), dtype)
+    a_dev, b_dev = H.upload(a, dtype), H.upload(b, dtype)
+    c_dev = gpu.allocate((M, N), H.GPU_DTYPES[dtype])
     assert lib.tl_gemm(a_dev.ptr, b_dev.ptr, c_dev.ptr, M, N, K, K, N, N, None, 0, code, None) == 0
-    err = H.max_abs(H.download(c_dev), gemm_ref(a, b))
-    H.report("split-k shape, no workspace", err, 2e-3)
-    assert err <= 2e-3
+    got = on.from_storage(H.download(c_dev), dtype)
+    exp = gemm_ref(on.from_storage(a, dtype), on.from_storage(b, dtype))
+    if dtype == "float32":
+        err = H.max_abs(got, exp)
+        H.report(f"split-k shape {M} rows, no workspace", err, 2e-3)
+        assert err <= 2e-3
+    else:
+        np.testing.assert_allclose(got, exp, rtol=8e-3, atol=1e-2)
 
 
 @pytest.mark.parametrize("dtype,K", [("bfloat16", 136), ("float16", 72), ("float32", 132), ("float32", 20)])

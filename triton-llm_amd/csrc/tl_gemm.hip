@@ -21,6 +21,7 @@
 namespace {
 
 constexpr int kSkinnyMaxM = 8;     // rows of A handled by the skinny path
+constexpr int kMaxSmallSplit = 32; // K-slices at most for few-row MFMA products
 constexpr int kSkThreads = 256;    // 4 waves
 constexpr int kSkUnroll = 16;      // row loads in flight per lane
 constexpr int kSkMaxTk = 1024;     // rows per K-slice at most (A's slice is staged in LDS)
@@ -701,6 +702,24 @@ PromptPlan prompt_plan(int m, int k, const GemmGroups& G, int esize) {
   auto busiest = [&](int S) { return (double)((P.tiles * (int64_t)S + cus - 1) / cus) / S; };
   double best = t1;
   P.ksplit = 1;
+  // Few rows (a batch of decoded tokens): the product streams B, and a few
+  // dozen tiles of C, each walking all of K, leave most CUs idle (a
+  // workgroup streams only tens of GB/s).  Split K until about two items
+  // per CU run, while the fp32 partials stay under half of B's bytes (which
+  // rules out large m) and every slice keeps two stages.
+  if (P.tiles < 2 * cus) {
+    const int64_t by_traffic = (int64_t)k * esize / (2 * 4 * (int64_t)m);
+    int64_t S = (2 * cus + P.tiles - 1) / P.tiles;
+    S = S < by_traffic ? S : by_traffic;
+    S = S < n_kt / 2 ? S : n_kt / 2;
+    S = S < kMaxSmallSplit ? S : kMaxSmallSplit;
+    if (S >= 2) {
+      P.ksplit = (int)S;
+      P.kt_per = (n_kt + P.ksplit - 1) / P.ksplit;
+      P.ws_bytes = (size_t)P.ksplit * m * ncols * sizeof(float);
+      return P;
+    }
+  }
   for (int S = 2; S <= 4 && esize == 4; ++S) {
     if (n_kt < 4 * S) break;
     const double t = t1 * busiest(S) / busiest(1) + ((double)S * 4 + esize) * m * (double)ncols / 5.0e12 + 3e-6;
