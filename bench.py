@@ -269,16 +269,18 @@ GEMM_MODELS = {
 FP32_PEAK_TFLOPS = 157.3
 
 
-def bench_gemm(steps, warmup, cpu=True, models=("llama3.2-3b", "smollm2-360m"), prompt=2048):
+def bench_gemm(steps, warmup, cpu=True, models=("llama3.2-3b", "smollm2-360m"), prompt=2048, batch_rows=64):
     """Time the projections of one layer (q, k, v, o, gate, up, down) of each
-    model for one decoded token (M = 1, weight-bandwidth bound) and for a
-    prompt (M = prompt, MFMA bound), fp32 as the reference runs them and bf16,
+    model for one decoded token (M = 1, weight-bandwidth bound), for a batch
+    of decoded tokens (M = batch_rows, one per sequence of a batched decode
+    step: still weight-bandwidth bound) and for a prompt (M = prompt, MFMA
+    bound), fp32 as the reference runs them and bf16,
     two ways: seven gemm calls, and the grouped form a layer step uses
     (gemm_grouped for q/k/v and for gate/up, gemm for o and down: four
-    launches, plus a split-K reduce each for M = 1).  Each layer's launches
+    launches, plus a split-K reduce each for few rows).  Each layer's launches
     are recorded once and replayed back to back between two events.  For
-    M = 1 the weights rotate over copies totalling >= 1 GB so each layer
-    reads them from HBM, not MALL.  The CPU baseline is NumPy float32 matmul
+    M = 1 and batch_rows the weights rotate over copies totalling >= 1 GB so
+    each layer reads them from HBM, not MALL.  The CPU baseline is NumPy float32 matmul
     on the host (a bounded sample: one pass per shape, M = 1 and 128)."""
     from triton_llm import gpu
     from triton_llm.kernels import gemm, gemm_grouped
@@ -300,8 +302,8 @@ def bench_gemm(steps, warmup, cpu=True, models=("llama3.2-3b", "smollm2-360m"), 
 
             layer_w = sum(K * N for K, N in shapes.values()) * esz
             w0 = {name: gpu.to_device(host(shape), gdt) for name, shape in shapes.items()}
-            for M in (1, prompt):
-                reps = max(1, int(np.ceil(1e9 / layer_w))) if M == 1 else 1
+            for M in (1, batch_rows, prompt):
+                reps = max(1, int(np.ceil(1e9 / layer_w))) if M <= batch_rows else 1
                 W = [w0]
                 for _ in range(reps - 1):
                     copy = {}

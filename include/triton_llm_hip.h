@@ -210,10 +210,12 @@ int tl_rope_kv_append(void* q, const void* k_new, const void* v_new,
  * workspace; larger m runs a hand-written MFMA kernel (128 x 128 tiles of
  * C, or 256 x 128 for large 16-bit products; rows of A and B must be
  * 16-byte aligned, otherwise a simple FMA kernel takes the product), which
- * for fp32 products that leave CUs unevenly loaded splits K and keeps fp32
- * partials in the workspace.  The query gives 0 when no workspace is used.
+ * for fp32 products that leave CUs unevenly loaded, and for products of
+ * any dtype with fewer than two tiles per CU (a batch of decoded tokens:
+ * at most 64 rows take 64 x 128 tiles), splits K and keeps fp32 partials in
+ * the workspace.  The query gives 0 when no workspace is used.
  * Given less than the query asks for, the MFMA kernel runs whole-K instead
- * of failing; the few-row kernel needs its workspace.
+ * of failing; the skinny kernel needs its workspace.
  * ------------------------------------------------------------------------- */
 size_t tl_gemm_workspace_bytes(int m, int n, int k, int dtype);
 int tl_gemm(const void* a, const void* b, void* c, int m, int n, int k, int64_t lda,

@@ -8,7 +8,10 @@
 //   * a prompt (m > kSkinnyMaxM rows) is a compute-bound GEMM on the matrix
 //     cores: gemm_mfma_kernel (128 x 128 tiles, LDS-DMA staging, fp32
 //     accumulation); shapes whose rows are not 16-byte aligned take the
-//     simple fp32-FMA gemm_simple_kernel;
+//     simple fp32-FMA gemm_simple_kernel.  A batch of decoded tokens (a few
+//     dozen rows) has too few tiles to fill the device: K is split into
+//     slices with fp32 partials and a reduce pass, and up to 64 rows take
+//     64-row tiles;
 //   * a decoded token (m <= kSkinnyMaxM rows) reads every weight once for a
 //     handful of multiply-adds per element: an HBM-bound skinny product,
 //     where rocBLAS measured 0.4-0.7 TB/s.  skinny_partial_kernel cuts B
@@ -22,6 +25,13 @@ namespace {
 
 constexpr int kSkinnyMaxM = 8;     // rows of A handled by the skinny path
 constexpr int kMaxSmallSplit = 32; // K-slices at most for few-row MFMA products
+// 64-row tiles for at most 64 rows: half the padding MFMA work of 128-row
+// tiles (Llama-3.2-3B layer at 9-64 rows: fp32 286-300 -> 169-189 us, bf16
+// 84.5 -> 73.7 us at 9 rows); 16-bit keeps 64 k per stage in two stages
+// (32 k in four measured 3-5% slower).
+constexpr int kNarrowMaxM = 64;
+constexpr int kNarrowBkb16 = 128;
+constexpr int kNarrowNst16 = 2;
 constexpr int kSkThreads = 256;    // 4 waves
 constexpr int kSkUnroll = 16;      // row loads in flight per lane
 constexpr int kSkMaxTk = 1024;     // rows per K-slice at most (A's slice is staged in LDS)
@@ -326,8 +336,9 @@ __device__ __forceinline__ bool gemm_tile(const GemmParams& p, int& grp, int& tm
 }
 
 // BKB: bytes of k per A row per stage (64 or 128); NST: stages in LDS; MBW:
-// 32-row blocks per wave along m (2: 128 x 128 tiles, 4: 256 x 128 tiles,
-// where each B fragment a wave reads feeds four MFMAs instead of two).
+// 32-row blocks per wave along m (1: 64 x 128 tiles for few rows, 2: 128 x
+// 128 tiles, 4: 256 x 128 tiles, where each B fragment a wave reads feeds
+// four MFMAs instead of two).
 template <typename T, int BKB, int NST, int MBW>
 __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) {
   constexpr bool F32 = T::size == 4;
@@ -659,6 +670,7 @@ __global__ __launch_bounds__(256) void gemm_simple_kernel(GemmParams p) {
 // How a prompt-sized product runs on the MFMA kernel: tile height and K split.
 struct PromptPlan {
   bool wide;      // 16-bit 256 x 128 tiles
+  bool narrow;    // 64 x 128 tiles (few rows: half the padding of 128-row tiles)
   int tiles_m, tiles;
   int ksplit, kt_per;
   size_t ws_bytes;  // fp32 partials when split
@@ -689,11 +701,13 @@ PromptPlan prompt_plan(int m, int k, const GemmGroups& G, int esize) {
     ncols += G.n[g];
   }
   P.wide = esize == 2 && wide_tiles >= 4 * cus;
-  const int tm = P.wide ? 2 * kGmTile : kGmTile;
+  P.narrow = !P.wide && m <= kNarrowMaxM;
+  const int tm = P.wide ? 2 * kGmTile : (P.narrow ? kGmTile / 2 : kGmTile);
   P.tiles_m = (m + tm - 1) / tm;
   P.tiles = 0;
   for (int g = 0; g < G.count; ++g) P.tiles += P.tiles_m * ((G.n[g] + kGmTile - 1) / kGmTile);
-  const int bk = esize == 2 ? (P.wide ? 32 : 64) : 16;  // k per LDS stage of the kernel used
+  // k per LDS stage of the kernel used
+  const int bk = esize == 2 ? (P.wide ? 32 : (P.narrow ? kNarrowBkb16 / 2 : 64)) : 16;
   const int n_kt = (k + bk - 1) / bk;
   // modelled seconds: the product at a sustained rate, scaled by the busiest
   // CU's share of items; the reduce as HBM traffic plus a launch
@@ -783,10 +797,15 @@ int launch_gemm(const void* a, const GemmGroups& G, int m, int k, int64_t lda, v
     if constexpr (T::size == 2) {
       if (P.wide)
         hipLaunchKernelGGL((gemm_mfma_kernel<T, 64, 3, 4>), grid, dim3(kGmThreads), 0, st, p);
+      else if (P.narrow)
+        hipLaunchKernelGGL((gemm_mfma_kernel<T, kNarrowBkb16, kNarrowNst16, 1>), grid, dim3(kGmThreads), 0, st, p);
       else
         hipLaunchKernelGGL((gemm_mfma_kernel<T, 128, 2, 2>), grid, dim3(kGmThreads), 0, st, p);
     } else {
-      hipLaunchKernelGGL((gemm_mfma_kernel<T, 64, 3, 2>), grid, dim3(kGmThreads), 0, st, p);
+      if (P.narrow)
+        hipLaunchKernelGGL((gemm_mfma_kernel<T, 64, 3, 1>), grid, dim3(kGmThreads), 0, st, p);
+      else
+        hipLaunchKernelGGL((gemm_mfma_kernel<T, 64, 3, 2>), grid, dim3(kGmThreads), 0, st, p);
     }
     int e = tl_launch_status();
     if (e || p.ksplit == 1) return e;
