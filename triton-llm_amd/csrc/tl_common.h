@@ -122,6 +122,16 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 
+// Sum over each group of 8 lanes (half a DPP row); every lane of the group
+// receives the sum: quad sums by two quad permutations, then the mirrored
+// lane of the other quad (row_half_mirror maps lane i to 7 - i).
+__device__ __forceinline__ float row8_sum(float x) {
+  x += dpp_mov<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp_mov<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp_mov<0x141>(x);  // row_half_mirror
+  return x;
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Status returned by launch wrappers: the HIP error of the launch (0 = ok).

@@ -22,27 +22,28 @@
 // Small caches (max_ctx <= 2048 and at most 64 MiB of K/V, e.g. GPT-2's
 // 1024-position cache) are latency-bound instead: a few MB spread over a
 // thousand shares cost a combine launch and dependent loads for little
-// streaming.  There one 16-wave workgroup (64 key streams, 8 keys each per
-// iteration) takes a whole (sequence, pair), finishes it and writes its
-// output (zeros for an empty sequence), and no combine runs (GPT-2 decode
-// 14.5 -> 9.7 us).
+// streaming.  There one 16-wave workgroup (64 key streams -- 128 for
+// 128-byte rows -- 8 keys each per iteration) takes a whole (sequence,
+// pair), finishes it and writes its output (zeros for an empty sequence),
+// and no combine runs (GPT-2 decode 14.5 -> 9.7 us).
 //
 // The pass is HBM-bound (every K/V byte is read exactly once), so the design
 // goal is to keep the VALU work per byte well under the issue budget:
 //   * a key row (d_k elements) is read by 16 consecutive lanes with one
 //     16-byte (or 8/32-byte) nontemporal buffer load each, so one wave load
-//     covers 4 consecutive rows; the row offset lives in one 32-bit VGPR and
+//     covers 4 consecutive rows (128-byte rows: 8 lanes, 8 rows); the row offset lives in one 32-bit VGPR and
 //     the per-unroll step in an SGPR (no 64-bit address math per load);
 //   * q.k of 16-bit types uses packed dot2 (v_dot2c_f32_bf16 / _f16) straight
-//     on the stored words; the 16-lane row sum is 4 DPP-fused adds;
-//   * the 16 lane-groups of the workgroup are 16 independent key streams
-//     (stream s takes keys start + s, start + s + 16, ...), each keeping its
+//     on the stored words; the 16-lane row sum is 4 DPP-fused adds (8-lane:
+//     3);
+//   * the lane groups of the workgroup are independent key streams
+//     (stream s takes keys start + s, start + s + n_streams, ...), each keeping its
 //     own online-softmax state (max m, sum l, accumulator) in the log2 domain,
 //     rescaled lazily: only when a new score exceeds the running max by
 //     2^kRescaleLog2 (exact either way -- the max only bounds exponent range);
 //   * full 64-key iterations run without masks; one masked iteration takes
 //     the remainder.
-// At the end of a segment the 16 streams are merged (lane shuffles, then
+// At the end of a segment the streams are merged (lane shuffles, then
 // LDS).  A pair inside one share is normalised and written directly;
 // otherwise each share's segment stores (m, l, acc[d_k]) to the workspace and
 // a second, small kernel merges them and normalises (attention_gqa.py:143
@@ -67,6 +68,13 @@ constexpr int kPairUnroll = 8;  // pair mode, small lane state: keys in flight p
 // elements) fits the 128 VGPRs of a 1024-thread workgroup, else 8
 template <typename T, int D, int G>
 constexpr int pair_waves() { return D * G * T::size <= 512 ? 16 : 8; }
+// Lanes that read one key row.  In pair mode rows of 128 bytes (16-bit d_k
+// 64) are read by 8 lanes with 16-byte loads (8 keys per wave load), which
+// halves the lane-sum steps and loads per key (GPT-2 decode 12.5 -> 11.8
+// us); the equal shares measured the same either way (SmolLM2-360M 41.7
+// against 42.1 us) and keep 16 lanes, as do larger rows.
+template <typename T, int D, int G, bool PAIR>
+constexpr int lanes_per_row() { return PAIR && D * T::size == 128 && G <= 4 ? 8 : 16; }
 constexpr int kPairMaxCtx = 2048;                  // pair mode: max_ctx at most
 constexpr int64_t kPairMaxBytes = 64ll << 20;      // pair mode: K/V cache bytes at most
 constexpr int kUnroll = 4;    // keys in flight per stream
@@ -289,10 +297,11 @@ __device__ __forceinline__ void set_progress_priority(int64_t done, int64_t shar
 // finishes it (no partials, no combine launch); otherwise equal shares.
 template <typename T, int D, int G, int NW, bool PAIR>
 __global__ __launch_bounds__(64 * NW) void decode_split_kernel(DecodeParams p) {
-  constexpr int EPL = D / 16;           // elements per lane per row
+  constexpr int LPR = lanes_per_row<T, D, G, PAIR>();
+  constexpr int EPL = D / LPR;          // elements per lane per row
   constexpr int W = EPL * T::size / 4;  // 32-bit words per lane per row
   constexpr int kThr = 64 * NW;
-  constexpr int kStr = 4 * NW;          // key streams (16-lane groups)
+  constexpr int kStr = (64 / LPR) * NW;  // key streams (LPR-lane groups)
   // keys in flight per stream: a pair workgroup streams its whole pair, so
   // it takes more per iteration where a lane's state is small
   constexpr int kU = PAIR && D * G * T::size <= 256 ? kPairUnroll : kUnroll;
@@ -302,8 +311,8 @@ __global__ __launch_bounds__(64 * NW) void decode_split_kernel(DecodeParams p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int sub = lane & 15;
-  const int stream = wave * 4 + (lane >> 4);
+  const int sub = lane & (LPR - 1);
+  const int stream = wave * (64 / LPR) + lane / LPR;
   const int n_chunks = p.n_pairs / p.n_kv;
 
   __shared__ float s_m[NW][G], s_l[NW][G];
@@ -368,7 +377,8 @@ __global__ __launch_bounds__(64 * NW) void decode_split_kernel(DecodeParams p) {
       for (int u = 0; u < kU; ++u) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          const float d = row16_sum(dot_slice<T>(qs[g], kr[u])) * c;
+          const float dp = dot_slice<T>(qs[g], kr[u]);
+          const float d = (LPR == 8 ? row8_sum(dp) : row16_sum(dp)) * c;
           s[g][u] = (!kMasked || valid[u]) ? d : -INFINITY;
         }
       }
@@ -425,9 +435,9 @@ __global__ __launch_bounds__(64 * NW) void decode_split_kernel(DecodeParams p) {
     }
     if (start + n_full * kKPI < end) iteration(key0, std::true_type{});
 
-    // Merge the 4 streams of this wave (lane groups 16 apart).
+    // Merge the streams of this wave (lane groups LPR apart).
 #pragma unroll
-    for (int off = 16; off <= 32; off <<= 1) {
+    for (int off = LPR; off <= 32; off <<= 1) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         const float m2 = __shfl_xor(m[g], off);
@@ -447,7 +457,7 @@ __global__ __launch_bounds__(64 * NW) void decode_split_kernel(DecodeParams p) {
     // Merge the NW waves through LDS (the barrier in front protects the
     // previous segment's reads of the same arrays).
     __syncthreads();
-    if (lane < 16) {
+    if (lane < LPR) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         if (lane == 0) {
@@ -610,6 +620,16 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
   }
 }
 
+// Whether a call runs in pair mode (small caches; see launch_decode_g).
+// (TRITON_LLM_HIP_DECODE_SHARES set to a nonzero value forces the shares,
+// so tests can run both paths on the same small inputs.)
+bool pair_mode(const DecodeParams& p, int d_k, int esize) {
+  const int64_t cache_bytes = (int64_t)p.batch * p.n_pairs * p.max_ctx * 2 * d_k * esize;
+  const char* force = getenv("TRITON_LLM_HIP_DECODE_SHARES");
+  const bool shares = force && atoi(force) != 0;
+  return !shares && p.max_ctx <= kPairMaxCtx && cache_bytes <= kPairMaxBytes;
+}
+
 template <typename T, int D, int G>
 int launch_decode_g(DecodeParams& p, hipStream_t st) {
   // Small caches: one 16-wave workgroup per (sequence, pair), which finishes
@@ -617,12 +637,7 @@ int launch_decode_g(DecodeParams& p, hipStream_t st) {
   // is known on the host (max_ctx), the lengths are not: pair mode needs a
   // short max_ctx (a workgroup streams its pair in a few iterations of 256
   // keys) and a small whole cache (no equal-share spreading needed).
-  // (TRITON_LLM_HIP_DECODE_SHARES set to a nonzero value forces the shares,
-  // so tests can run both paths on the same small inputs.)
-  const int64_t cache_bytes = (int64_t)p.batch * p.n_pairs * p.max_ctx * 2 * D * T::size;
-  const char* force = getenv("TRITON_LLM_HIP_DECODE_SHARES");
-  const bool shares = force && atoi(force) != 0;
-  if (!shares && p.max_ctx <= kPairMaxCtx && cache_bytes <= kPairMaxBytes) {
+  if (pair_mode(p, D, T::size)) {
     p.n_blocks = p.batch * p.n_pairs;
     constexpr int NW = pair_waves<T, D, G>();
     hipLaunchKernelGGL((decode_split_kernel<T, D, G, NW, true>), dim3(p.n_blocks), dim3(64 * NW), 0, st, p);
@@ -836,11 +851,14 @@ int decode_entry(const void* q, const void* k_cache, const void* v_cache,
   p.o_sb = o_strides[0];
   p.o_sh = o_strides[1];
   p.scale_log2 = sm_scale * 1.4426950408889634f;
-  // Each lane loads d_k/16 contiguous elements with one vector load, so
-  // every row start must be aligned to that slice; positions are addressed
-  // with 32-bit byte offsets from the (b, head) base.
+  // Each lane loads d_k/16 contiguous elements (d_k/8 for 16-bit d_k 64
+  // with at most 4 heads per pair in pair mode: lanes_per_row) with one
+  // vector load, so every row start must be aligned to that slice;
+  // positions are addressed with 32-bit byte offsets from the (b, head)
+  // base.
   const int esize = dtype == TL_DTYPE_F32 ? 4 : 2;
-  const int64_t slice = d_k / 16;
+  const bool lanes8 = pair_mode(p, d_k, esize) && d_k * esize == 128 && p.heads_per_pair <= 4;
+  const int64_t slice = lanes8 ? d_k / 8 : d_k / 16;
   const uintptr_t align = (uintptr_t)(slice * esize);
   const int64_t st_all[] = {p.q_sb, p.q_sh, p.k_sb, p.k_sh, k_strides[2], p.v_sb, p.v_sh, v_strides[2]};
   for (int64_t s : st_all)
