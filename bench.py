@@ -570,7 +570,7 @@ def bench_gemm_case(model, dt, M, steps):
     """One GEMM layer case only, for rocprofv3: ``steps`` grouped one-layer
     projection passes (gemm_grouped q/k/v, gemm o, gemm_grouped gate/up, gemm
     down) of ``model`` in ``dt`` at M rows, weights rotated over >= 1 GB of
-    copies for M = 1 as in bench_gemm."""
+    copies for M <= 64 (decoded tokens) as in bench_gemm."""
     from triton_llm import gpu
     from triton_llm.kernels import gemm, gemm_grouped
 
@@ -585,7 +585,7 @@ def bench_gemm_case(model, dt, M, steps):
         return (x.view(np.uint32) >> 16).astype(np.uint16) if dt == "bfloat16" else x
 
     layer_w = sum(K * N for K, N in shapes.values()) * esz
-    reps = max(1, int(np.ceil(1e9 / layer_w))) if M == 1 else 1
+    reps = max(1, int(np.ceil(1e9 / layer_w))) if M <= 64 else 1
     W = [{name: gpu.to_device(host(shape), gdt) for name, shape in shapes.items()} for _ in range(reps)]
     x = {d: gpu.to_device(host((M, d)), gdt) for d in {e, q, inter}}
     out = {name: gpu.allocate((M, N), gdt) for name, (K, N) in shapes.items()}
