@@ -70,6 +70,24 @@ def test_argument_errors_return_invalid_without_launching():
                                  s3, s3, s3, s3, s3, _lib.DTYPE_F32, None) == 0
 
 
+def test_decode_pair_mode_needs_16_byte_row_slices(monkeypatch):
+    """A small 16-bit d_k 64 cache runs in pair mode, where 8 lanes read a
+    128-byte key row with 16-byte loads: a row stride that is a multiple of
+    4 elements but not of 8 is refused (TL_ERR_UNSUPPORTED) before any HIP
+    call, while an aligned-pointer check would otherwise pass."""
+    monkeypatch.delenv("TRITON_LLM_HIP_DECODE_SHARES", raising=False)
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x100000)
+    batch, n_head, n_kv, max_ctx, d_k = 2, 3, 1, 64, 64
+    ws = lib.tl_attention_decode_workspace_bytes(batch, n_head, max_ctx, d_k, 16)
+    q_st = _lib.strides(n_head * d_k, d_k, 1)
+    for row in (68, 76):
+        kv_st = _lib.strides(n_kv * max_ctx * row, max_ctx * row, row)
+        st = lib.tl_attention_decode(fake, fake, fake, None, 1, fake, fake, ws, batch, n_head, n_kv, max_ctx,
+                                     d_k, q_st, kv_st, kv_st, q_st, 0.125, 16, _lib.DTYPE_BF16, None)
+        assert st == 801, st
+
+
 def test_error_string():
     assert _lib.error_string(0) == "success"
     assert isinstance(_lib.error_string(1), str)
