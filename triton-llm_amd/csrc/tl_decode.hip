@@ -31,13 +31,14 @@
 // goal is to keep the VALU work per byte well under the issue budget:
 //   * a key row (d_k elements) is read by 16 consecutive lanes with one
 //     16-byte (or 8/32-byte) nontemporal buffer load each, so one wave load
-//     covers 4 consecutive rows (128-byte rows: 8 lanes, 8 rows); the row offset lives in one 32-bit VGPR and
+//     covers 4 consecutive rows (pair mode, 128-byte rows: 8 lanes with
+//     16-byte loads, 8 rows); the row offset lives in one 32-bit VGPR and
 //     the per-unroll step in an SGPR (no 64-bit address math per load);
 //   * q.k of 16-bit types uses packed dot2 (v_dot2c_f32_bf16 / _f16) straight
 //     on the stored words; the 16-lane row sum is 4 DPP-fused adds (8-lane:
 //     3);
-//   * the lane groups of the workgroup are independent key streams
-//     (stream s takes keys start + s, start + s + n_streams, ...), each keeping its
+//   * the lane groups of the workgroup are independent key streams (stream
+//     s takes keys start + s, start + s + n_streams, ...), each keeping its
 //     own online-softmax state (max m, sum l, accumulator) in the log2 domain,
 //     rescaled lazily: only when a new score exceeds the running max by
 //     2^kRescaleLog2 (exact either way -- the max only bounds exponent range);
