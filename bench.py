@@ -269,7 +269,38 @@ GEMM_MODELS = {
 FP32_PEAK_TFLOPS = 157.3
 
 
-def bench_gemm(steps, warmup, cpu=True, models=("llama3.2-3b", "smollm2-360m"), prompt=2048, batch_rows=64):
+def rocblas_calls(lib, shapes, x, w, out, M, dt):
+    """Zero-argument launchers of rocblas_gemm_ex for each projection
+    C (M, N) = X (M, K) . W (K, N), row-major, run as the column-major
+    C^T = W^T X^T on the library stream, fp32 accumulation.  A measurement
+    reference point only (bench.py --gemm --gemm-rocblas)."""
+    import ctypes
+
+    rb = ctypes.CDLL("librocblas.so")
+    lib.tl_default_stream.restype = ctypes.c_void_p
+    handle = ctypes.c_void_p()
+    if rb.rocblas_create_handle(ctypes.byref(handle)) != 0:
+        raise RuntimeError("rocblas_create_handle failed")
+    if rb.rocblas_set_stream(handle, ctypes.c_void_p(lib.tl_default_stream())) != 0:
+        raise RuntimeError("rocblas_set_stream failed")
+    code = 151 if dt == "float32" else 168  # rocblas_datatype_f32_r / _bf16_r
+    one, zero = ctypes.c_float(1.0), ctypes.c_float(0.0)
+    calls = []
+    for name, (K, N) in shapes.items():
+        a, b, c = x[K].ptr.value, w[name].ptr.value, out[name].ptr.value
+
+        def call(a=a, b=b, c=c, K=K, N=N):
+            st = rb.rocblas_gemm_ex(handle, 111, 111, N, M, K, ctypes.byref(one), ctypes.c_void_p(b), code, N,
+                                    ctypes.c_void_p(a), code, K, ctypes.byref(zero), ctypes.c_void_p(c), code, N,
+                                    ctypes.c_void_p(c), code, N, 151, 0, 0, 0)
+            if st != 0:
+                raise RuntimeError(f"rocblas_gemm_ex failed: {st}")
+        calls.append(call)
+    return calls
+
+
+def bench_gemm(steps, warmup, cpu=True, models=("llama3.2-3b", "smollm2-360m"), prompt=2048, batch_rows=64,
+               vs_rocblas=False):
     """Time the projections of one layer (q, k, v, o, gate, up, down) of each
     model for one decoded token (M = 1, weight-bandwidth bound), for a batch
     of decoded tokens (M = batch_rows, one per sequence of a batched decode
@@ -339,6 +370,17 @@ def bench_gemm(steps, warmup, cpu=True, models=("llama3.2-3b", "smollm2-360m"), 
                     })
                     log(f"gemm {model} {dt} M={M} {form}: {ms * 1e3:.1f} us/layer, {rows[-1]['tflops']:.1f} TFLOP/s, "
                         f"{rows[-1]['gbs']:.0f} GB/s")
+                if vs_rocblas and M == prompt:
+                    rcalls = rocblas_calls(lib, shapes, x, W[0], out, M, dt)
+                    ms, _, _ = time_calls(lib, [lambda: [c() for c in rcalls]], steps, warmup, 0.0)
+                    rows.append({
+                        "model": model, "dtype": dt, "M": M, "form": "rocBLAS, seven calls (reference point)",
+                        "ms_per_layer": ms, "tflops": flops / (ms * 1e-3) / 1e12,
+                        "frac_mfma": flops / (ms * 1e-3) / 1e12 / peak,
+                        "gbs": nbytes / (ms * 1e-3) / 1e9, "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                    })
+                    log(f"gemm {model} {dt} M={M} rocBLAS reference: {ms * 1e3:.1f} us/layer, "
+                        f"{rows[-1]['tflops']:.1f} TFLOP/s")
                 del W
     res = {"metric": "projection GEMMs per layer (tl_gemm)", "rows": rows}
     res["layers"] = bench_layers(steps, warmup)
@@ -697,6 +739,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gemm", action="store_true",
                     help="time the model's projection GEMMs (tl_gemm) instead of attention")
+    ap.add_argument("--gemm-rocblas", action="store_true",
+                    help="with --gemm: also time rocBLAS (rocblas_gemm_ex through its C API, the "
+                         "seven calls back to back on the library stream) at the prompt size, as a "
+                         "reference point; the library itself never calls rocBLAS")
     ap.add_argument("--sample", action="store_true",
                     help="time next-token sampling (tl_sample) instead of attention")
     ap.add_argument("--sample-case", default="",
@@ -737,7 +783,8 @@ def main():
         print(json.dumps(bench_sample(min(args.steps, 50), min(args.warmup, 5), cpu=cpu)))
         return
     if args.gemm:
-        print(json.dumps(bench_gemm(min(args.steps, 20), min(args.warmup, 5), cpu=cpu)))
+        print(json.dumps(bench_gemm(min(args.steps, 20), min(args.warmup, 5), cpu=cpu,
+                                    vs_rocblas=args.gemm_rocblas)))
         return
     sel = {"5": ["5a", "5b"], "all": ["1", "2", "3", "4", "5a", "5b"]}.get(args.config, [args.config])
     results = {}
