@@ -127,6 +127,29 @@ def test_decode_without_append_and_len_zero_gives_zeros(monkeypatch, mode):
     compare("no-append", got, exp, TOL[dt])
 
 
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16", "float32"])
+@pytest.mark.parametrize("n_head,n_kv,d_k", [(2, 2, 64), (6, 2, 64), (3, 1, 128)])
+def test_decode_iteration_boundary_lengths(monkeypatch, mode, dtype, n_head, n_kv, d_k):
+    """Lengths at and around the kernels' iteration sizes: a pair-mode
+    workgroup takes 512 or 1024 keys per full iteration (8- or 16-lane rows),
+    an equal-share workgroup 64; positions past each length hold NaN, and a
+    zero length gives zeros."""
+    set_mode(monkeypatch, mode)
+    lens = np.array([0, 1, 63, 64, 65, 127, 128, 511, 512, 513, 1023, 1024, 1025, 2047, 2048], np.int32)
+    print(f"[case] decode boundary lengths {mode} {dtype} Hq{n_head} Hkv{n_kv} d{d_k}", flush=True)
+    cfg = oi.Config("decode-bounds", "decode", dtype, len(lens), n_head, n_kv, d_k, 41, 1 / np.sqrt(d_k),
+                    max_ctx=2048, lo=1, hi=2047)
+    data = oi.make_decode(cfg, fill="nan", lens=lens)
+    out = attention_decode(H.upload(data["q"], dtype), H.upload(data["k_cache"], dtype),
+                           H.upload(data["v_cache"], dtype), gpu.to_device(data["lens"]), n_head, n_kv,
+                           sm_scale=cfg.scale, len_add=0)
+    got = on.from_storage(H.download(out), dtype)
+    exp = oa.decode_ref(data["q"], data["k_cache"], data["v_cache"], data["lens"], sm_scale=cfg.scale, dtype=dtype)
+    assert np.all(got[0] == 0)
+    compare(f"boundary-lens {mode} {dtype}", got[1:], exp[1:], TOL[dtype])
+
+
 @pytest.mark.parametrize("split", [16, 64, 256, 2048])
 def test_decode_split_sizes_agree(monkeypatch, split):
     monkeypatch.setenv(SHARES_ENV, "1")  # split sizes apply to the shares path
