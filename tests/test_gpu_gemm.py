@@ -235,6 +235,31 @@ def test_gemm_few_rows_split_k(dtype, M, K, Ns):
             np.testing.assert_allclose(got, exp, rtol=8e-3, atol=1e-2)
 
 
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
+@pytest.mark.parametrize("M", [9, 63, 64, 65])
+def test_gemm_row_tile_boundaries(dtype, M):
+    """Around the switch from 64-row to 128-row tiles (64 / 65 rows), with a K
+    tail in every dtype (1000 = 15 stages of 64 k + 40, or 62 of 16 + 8) and
+    column counts that are not whole tiles, grouped and single."""
+    print(f"[case] gemm row-tile boundary {dtype} M={M}", flush=True)
+    K, Ns = 1000, (1000, 200)
+    rng = np.random.default_rng(M)
+    a = on.to_storage(rng.standard_normal((M, K), dtype=np.float32), dtype)
+    bs = [on.to_storage(rng.standard_normal((K, n), dtype=np.float32) / np.sqrt(K), dtype) for n in Ns]
+    a_dev = H.upload(a, dtype)
+    outs = gemm_grouped(a_dev, [H.upload(b, dtype) for b in bs]) + [gemm(a_dev, H.upload(bs[1], dtype))]
+    for b, o in zip(bs + [bs[1]], outs):
+        got = on.from_storage(H.download(o), dtype)
+        exp = gemm_ref(on.from_storage(a, dtype), on.from_storage(b, dtype))
+        if dtype == "float32":
+            err = H.max_abs(got, exp)
+            H.report(f"row-tile boundary {dtype} {M}x{K}@{K}x{b.shape[1]}", err, 2e-3)
+            assert err <= 2e-3
+        else:
+            assert np.all(np.isfinite(got))
+            np.testing.assert_allclose(got, exp, rtol=8e-3, atol=1e-2)
+
+
 @pytest.mark.parametrize("dtype,M", [("float32", 2048), ("float32", 40), ("bfloat16", 64)])
 def test_gemm_prompt_split_k_without_workspace_runs_whole(dtype, M):
     """The C ABI with no workspace for a shape its plan would split: the
