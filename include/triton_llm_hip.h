@@ -145,6 +145,12 @@ int tl_attention_fwd(const void* q, const void* k, const void* v, void* o,
  * that finishes its heads itself: one launch, no partials, split_size and
  * the workspace unused (the environment variable
  * TRITON_LLM_HIP_DECODE_SHARES=1 forces the shares path).
+ * d_k is 64 or 128.  Each lane reads a slice of d_k / 16 elements of a
+ * row (d_k / 8 for 16-bit d_k 64 in the small-cache mode with at most 4
+ * query heads per KV head), so q, k_cache, v_cache and every q / k / v
+ * stride must be multiples of that slice; otherwise, or when one (sequence,
+ * head) region of a cache exceeds 2 GiB, the call returns
+ * TL_ERR_UNSUPPORTED.
  * ------------------------------------------------------------------------- */
 int tl_decode_split_size(int batch, int n_kv_head, int max_ctx);
 size_t tl_attention_decode_workspace_bytes(int batch, int n_head, int max_ctx,
