@@ -214,7 +214,7 @@ int tl_rope_kv_append(void* q, const void* k_new, const void* v_new,
  * m <= 8 (a decoded token) runs a hand-written HBM-streaming kernel whose
  * K-slice partial sums need tl_gemm_workspace_bytes(m, n, k, dtype) bytes of
  * workspace; larger m runs a hand-written MFMA kernel (128 x 128 tiles of
- * C, or 256 x 128 for large 16-bit products; rows of A and B must be
+ * C, or 256 x 128 / 256 x 256 for large 16-bit products; rows of A and B must be
  * 16-byte aligned, otherwise a simple FMA kernel takes the product), which
  * for fp32 products that leave CUs unevenly loaded, and for products of
  * any dtype with fewer than two tiles per CU (a batch of decoded tokens:

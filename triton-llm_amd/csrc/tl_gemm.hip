@@ -338,19 +338,23 @@ __device__ __forceinline__ bool gemm_tile(const GemmParams& p, int& grp, int& tm
 // BKB: bytes of k per A row per stage (64 or 128); NST: stages in LDS; MBW:
 // 32-row blocks per wave along m (1: 64 x 128 tiles for few rows, 2: 128 x
 // 128 tiles, 4: 256 x 128 tiles, where each B fragment a wave reads feeds
-// four MFMAs instead of two).
-template <typename T, int BKB, int NST, int MBW>
-__global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) {
+// four MFMAs instead of two); NWV: waves (4, or 8 for 16-bit 256 x 256 tiles:
+// two along m by four along n, B staged as 512-byte rows, one workgroup per
+// CU, half the operand bytes staged per MFMA of two 256 x 128 workgroups).
+template <typename T, int BKB, int NST, int MBW, int NWV = 4>
+__global__ __launch_bounds__(64 * NWV, NWV == 8 ? 1 : 2) void gemm_mfma_kernel(GemmParams p) {
   constexpr bool F32 = T::size == 4;
   constexpr int TM = 64 * MBW;                // rows of C per tile
   constexpr int BK = BKB / T::size;           // k per stage
   constexpr int ACH = BKB / 16;               // 16-byte chunks per A row (4 or 8)
-  constexpr int BROW = kGmTile * T::size;     // bytes per B row in LDS
+  constexpr int TN = 32 * NWV;               // columns of C per tile (128 or 256)
+  constexpr int BROW = TN * T::size;          // bytes per B row in LDS
   constexpr int NQ = F32 ? BK / 8 : BK / 16;  // fp32 k-groups / 16-bit k-steps per stage
   constexpr int kGmStages = NST;
   constexpr int kGmStageA = TM * BKB;         // bytes of one A stage
   constexpr int kGmStageB = BK * BROW;        // bytes of one B stage
-  static_assert(kGmStageA % 4096 == 0 && kGmStageB % 4096 == 0, "every wave loads whole 1 KiB regions");
+  static_assert(kGmStageA % (1024 * NWV) == 0 && kGmStageB % (1024 * NWV) == 0, "every wave loads whole 1 KiB regions");
+  static_assert(NWV == 4 || !F32, "eight waves: 16-bit only");
   using Bits = typename T::bits;
   __shared__ __attribute__((aligned(1024))) char smem[kGmStages * (kGmStageA + kGmStageB)];
 
@@ -367,7 +371,7 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) 
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int wm = wave & 1, wn = wave >> 1;  // this wave's (32 MBW) x 64 block
-  const int m_tile = tm * TM, n_tile = tn * kGmTile;
+  const int m_tile = tm * TM, n_tile = tn * TN;
   __attribute__((address_space(3))) char* const lds_base = (__attribute__((address_space(3))) char*)smem;
   const uint32_t lds0 = (uint32_t)(size_t)lds_base;
   const uint32_t lds_a = lds0, lds_b = lds0 + kGmStages * kGmStageA;
@@ -395,29 +399,33 @@ __global__ __launch_bounds__(kGmThreads, 2) void gemm_mfma_kernel(GemmParams p) 
   constexpr int A_RPR = 1024 / BKB;
   const int a_row0 = A_RPR * wave + lane / ACH;
   const uint32_t a_off = (uint32_t)(m_tile + a_row0) * lda2 + (uint32_t)(((lane % ACH) ^ a_swz(a_row0)) * 16);
+  static_assert(NWV == 4 || BKB == 64, "eight waves: 64-byte A rows (the swizzle bits survive a 128-row step)");
   // B, 16-bit: regions of 4 rows of 256 bytes, lane i -> row 4 R + i / 16,
   // slot i % 16 (swizzle 4 (row % 4) = 4 (i / 16)).  fp32: regions of 2 rows
   // of 512 bytes, lane i -> row 2 R + i / 32, slot i % 32 (swizzle
   // 8 ((row >> 2) & 1) = 8 ((R >> 1) & 1), and R = wave + 4 j keeps that bit).
   uint32_t b_off;
-  if constexpr (!F32)
+  if constexpr (!F32 && NWV == 8)  // 512-byte rows: regions of 2 rows, lane i -> row 2 R + i / 32
+    b_off = (uint32_t)(2 * wave + lane / 32) * ldb2 + (uint32_t)(n_tile * 2) +
+            (uint32_t)(((lane % 32) ^ (4 * ((2 * wave + lane / 32) & 3))) * 16);
+  else if constexpr (!F32)
     b_off = (uint32_t)(4 * wave + lane / 16) * ldb2 + (uint32_t)(n_tile * 2) +
             (uint32_t)(((lane % 16) ^ (4 * (lane / 16))) * 16);
   else
     b_off = (uint32_t)(2 * wave + lane / 32) * ldb2 + (uint32_t)(n_tile * 4) +
             (uint32_t)(((lane % 32) ^ (8 * ((wave >> 1) & 1))) * 16);
-  constexpr int A_REG = kGmStageA / 1024 / 4;  // regions per wave per stage
-  constexpr int B_REG = kGmStageB / 1024 / 4;
+  constexpr int A_REG = kGmStageA / 1024 / NWV;  // regions per wave per stage
+  constexpr int B_REG = kGmStageB / 1024 / NWV;
   constexpr int B_RPR = 1024 / BROW;           // B rows per region
   auto load_stage = [&](int kt, int buf) __attribute__((always_inline)) {
     const uint32_t ka = (uint32_t)(kt * BK * T::size);  // A: column bytes of the stage
     const uint32_t kb = (uint32_t)(kt * BK) * ldb2;     // B: row offset of the stage
 #pragma unroll
     for (int j = 0; j < A_REG; ++j)
-      dma(ra, a_off + ka + (uint32_t)(4 * A_RPR * j) * lda2, lds_a + buf * kGmStageA + (wave + 4 * j) * 1024);
+      dma(ra, a_off + ka + (uint32_t)(NWV * A_RPR * j) * lda2, lds_a + buf * kGmStageA + (wave + NWV * j) * 1024);
 #pragma unroll
     for (int j = 0; j < B_REG; ++j)
-      dma(rb, b_off + kb + (uint32_t)(4 * B_RPR * j) * ldb2, lds_b + buf * kGmStageB + (wave + 4 * j) * 1024);
+      dma(rb, b_off + kb + (uint32_t)(NWV * B_RPR * j) * ldb2, lds_b + buf * kGmStageB + (wave + NWV * j) * 1024);
   };
 
   f32x16 acc[MBW][2];  // [m block][n block], C^T layout
@@ -669,6 +677,7 @@ __global__ __launch_bounds__(256) void gemm_simple_kernel(GemmParams p) {
 
 // How a prompt-sized product runs on the MFMA kernel: tile height and K split.
 struct PromptPlan {
+  bool huge;      // 16-bit 256 x 256 tiles (eight waves)
   bool wide;      // 16-bit 256 x 128 tiles
   bool narrow;    // 64 x 128 tiles (few rows: half the padding of 128-row tiles)
   int tiles_m, tiles;
@@ -680,7 +689,9 @@ struct PromptPlan {
 // traffic per product) when they still give every CU at least four; fewer,
 // larger tiles leave CUs idle on the narrower products.  Measured at a
 // 2048-row Llama-3.2-3B prompt: gate/up 226 -> 219 us; q/k/v, o and down
-// (320 or fewer such tiles) were slower with them.
+// (320 or fewer such tiles) were slower with them.  Where 256 x 256 tiles
+// (eight waves, one workgroup per CU) still give every CU two, they run
+// instead: gate/up 206-209 -> 191 us, the layer 456-462 -> 442 us.
 //
 // K split (fp32): a CU's time is set by the items it runs, and a whole tile
 // is the unit, so 384 tiles on 256 CUs cost two tiles' time where 1.5 would
@@ -700,14 +711,19 @@ PromptPlan prompt_plan(int m, int k, const GemmGroups& G, int esize) {
     wide_tiles += ((m + 2 * kGmTile - 1) / (2 * kGmTile)) * ((G.n[g] + kGmTile - 1) / kGmTile);
     ncols += G.n[g];
   }
+  int huge_tiles = 0;
+  for (int g = 0; g < G.count; ++g)
+    huge_tiles += ((m + 2 * kGmTile - 1) / (2 * kGmTile)) * ((G.n[g] + 2 * kGmTile - 1) / (2 * kGmTile));
+  P.huge = esize == 2 && huge_tiles >= 2 * cus;
   P.wide = esize == 2 && wide_tiles >= 4 * cus;
-  P.narrow = !P.wide && m <= kNarrowMaxM;
-  const int tm = P.wide ? 2 * kGmTile : (P.narrow ? kGmTile / 2 : kGmTile);
+  P.narrow = !P.wide && !P.huge && m <= kNarrowMaxM;
+  const int tm = (P.wide || P.huge) ? 2 * kGmTile : (P.narrow ? kGmTile / 2 : kGmTile);
   P.tiles_m = (m + tm - 1) / tm;
   P.tiles = 0;
-  for (int g = 0; g < G.count; ++g) P.tiles += P.tiles_m * ((G.n[g] + kGmTile - 1) / kGmTile);
+  const int tn = P.huge ? 2 * kGmTile : kGmTile;
+  for (int g = 0; g < G.count; ++g) P.tiles += P.tiles_m * ((G.n[g] + tn - 1) / tn);
   // k per LDS stage of the kernel used
-  const int bk = esize == 2 ? (P.wide ? 32 : (P.narrow ? kNarrowBkb16 / 2 : 64)) : 16;
+  const int bk = esize == 2 ? ((P.wide || P.huge) ? 32 : (P.narrow ? kNarrowBkb16 / 2 : 64)) : 16;
   const int n_kt = (k + bk - 1) / bk;
   // modelled seconds: the product at a sustained rate, scaled by the busiest
   // CU's share of items; the reduce as HBM traffic plus a launch
@@ -779,7 +795,8 @@ int launch_gemm(const void* a, const GemmGroups& G, int m, int k, int64_t lda, v
     p.G.tile0[0] = 0;
     p.vec_store = 0;
     for (int g = 0; g < G.count; ++g) {
-      p.G.tile0[g + 1] = p.G.tile0[g] + p.tiles_m * ((G.n[g] + kGmTile - 1) / kGmTile);
+      const int tn = P.huge ? 2 * kGmTile : kGmTile;
+      p.G.tile0[g + 1] = p.G.tile0[g] + p.tiles_m * ((G.n[g] + tn - 1) / tn);
       if (G.ldc[g] % 4 == 0 && ((uintptr_t)G.c[g] % (4 * esize)) == 0) p.vec_store |= 1 << g;
     }
     // the split needs its partials' workspace; without it the product runs whole
@@ -799,7 +816,9 @@ int launch_gemm(const void* a, const GemmGroups& G, int m, int k, int64_t lda, v
     // within 1% across those and keeps 16 k in three stages.
     const dim3 grid((unsigned)(8 * p.per_xcd));
     if constexpr (T::size == 2) {
-      if (P.wide)
+      if (P.huge)
+        hipLaunchKernelGGL((gemm_mfma_kernel<T, 64, 3, 4, 8>), grid, dim3(512), 0, st, p);
+      else if (P.wide)
         hipLaunchKernelGGL((gemm_mfma_kernel<T, 64, 3, 4>), grid, dim3(kGmThreads), 0, st, p);
       else if (P.narrow)
         hipLaunchKernelGGL((gemm_mfma_kernel<T, kNarrowBkb16, kNarrowNst16, 1>), grid, dim3(kGmThreads), 0, st, p);
