@@ -108,7 +108,12 @@ int tl_rope_inplace(void* x, const float* cos_table, const float* sin_table,
  * attention_gqa.py:97; equal to attention.py's top-left mask when
  * seq_q == seq_k).  Scores are (q . k) * sm_scale.
  * Requires seq_q >= 1, seq_k >= 1 (the Python layer returns the reference's
- * empty/zero results itself).  Workspace: tl_attention_fwd_workspace_bytes
+ * empty/zero results itself).  d_k 64 and 128 with 16-byte-aligned rows run
+ * the MFMA kernels; any other d_k up to 4096 (the reference accepts any
+ * power of two) runs a generic fp32 kernel; larger d_k returns
+ * TL_ERR_UNSUPPORTED.  fp16 with |sm_scale| * log2(e) > 1 scales the scores
+ * in fp32 instead of pre-scaling Q, whose fp16 copy could overflow.
+ * Workspace: tl_attention_fwd_workspace_bytes
  * (the 16-bit MFMA path at d_k 128 stages a key-major copy of V there; 0
  * for d_k 64 and fp32, which read V in place; NULL is accepted when 0).
  * ------------------------------------------------------------------------- */
@@ -142,9 +147,12 @@ int tl_attention_fwd(const void* q, const void* k, const void* v, void* o,
  * for empty sequences.  The workspace holds the partials and may be reused
  * by consecutive calls on one stream.  Small caches (max_ctx <= 2048 and at
  * most 64 MiB of K and V) instead run one workgroup per (sequence, KV head)
- * that finishes its heads itself: one launch, no partials, split_size and
- * the workspace unused (the environment variable
- * TRITON_LLM_HIP_DECODE_SHARES=1 forces the shares path).
+ * that finishes its heads itself: one launch, no partials, and the kernels
+ * read neither split_size nor the workspace.  The workspace arguments are
+ * checked in every mode all the same (non-NULL, 16-byte aligned, at least
+ * tl_attention_decode_workspace_bytes), so a caller never depends on which
+ * mode a shape takes.  (TRITON_LLM_HIP_DECODE_SHARES=1 in the environment
+ * when tl_init runs forces the shares path; tests use it.)
  * d_k is 64 or 128.  Each lane reads a slice of d_k / 16 elements of a
  * row (d_k / 8 for 16-bit d_k 64 in the small-cache mode with at most 4
  * query heads per KV head), so q, k_cache, v_cache and every q / k / v
@@ -175,6 +183,9 @@ int tl_attention_decode(const void* q, const void* k_cache, const void* v_cache,
  * array and race: issue them on one stream.  Results are identical to
  * tl_attention_decode's for the same arguments. */
 #define TL_DECODE_NOALLOC_SCRATCH_BYTES (32u << 20)
+/* The same limit as a data symbol of the loaded library, so a binding reads
+ * it from the library it calls instead of repeating the number. */
+extern const size_t tl_decode_noalloc_scratch_bytes;
 int tl_attention_decode_noalloc(const void* q, const void* k_cache, const void* v_cache,
                                 const int32_t* cache_lens, int len_add, void* o, int batch,
                                 int n_head, int n_kv_head, int max_ctx, int d_k,
@@ -214,7 +225,7 @@ int tl_rope_kv_append(void* q, const void* k_new, const void* v_new,
  * m <= 8 (a decoded token) runs a hand-written HBM-streaming kernel whose
  * K-slice partial sums need tl_gemm_workspace_bytes(m, n, k, dtype) bytes of
  * workspace; larger m runs a hand-written MFMA kernel (128 x 128 tiles of
- * C, or 256 x 128 / 256 x 256 for large 16-bit products; rows of A and B must be
+ * C, or 256 x 256 for large 16-bit products; rows of A and B must be
  * 16-byte aligned, otherwise a simple FMA kernel takes the product), which
  * for fp32 products that leave CUs unevenly loaded, and for products of
  * any dtype with fewer than two tiles per CU (a batch of decoded tokens:

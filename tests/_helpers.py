@@ -47,6 +47,18 @@ def attention_gqa_cpu(q, k, v, n_head, n_kv_head, causal=True, dtype="float32", 
     return download(o)
 
 
+def set_override(monkeypatch, name: str, value) -> None:
+    """Set (or, for None, clear) one of the library's test-only environment
+    overrides and have the library re-read them now (it reads them in
+    tl_init, not per launch).  monkeypatch restores the variable after the
+    test, and the autouse fixture in conftest re-reads it then."""
+    if value is None:
+        monkeypatch.delenv(name, raising=False)
+    else:
+        monkeypatch.setenv(name, str(value))
+    gpu.reload_overrides()
+
+
 def max_abs(a, b) -> float:
     """Largest |a - b| over the broadcast arrays, NaN-strict.
 

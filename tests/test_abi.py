@@ -70,12 +70,11 @@ def test_argument_errors_return_invalid_without_launching():
                                  s3, s3, s3, s3, s3, _lib.DTYPE_F32, None) == 0
 
 
-def test_decode_pair_mode_needs_16_byte_row_slices(monkeypatch):
+def test_decode_pair_mode_needs_16_byte_row_slices():
     """A small 16-bit d_k 64 cache runs in pair mode, where 8 lanes read a
     128-byte key row with 16-byte loads: a row stride that is a multiple of
     4 elements but not of 8 is refused (TL_ERR_UNSUPPORTED) before any HIP
     call, while an aligned-pointer check would otherwise pass."""
-    monkeypatch.delenv("TRITON_LLM_HIP_DECODE_SHARES", raising=False)
     lib = _lib.load()
     fake = ctypes.c_void_p(0x100000)
     batch, n_head, n_kv, max_ctx, d_k = 2, 3, 1, 64, 64

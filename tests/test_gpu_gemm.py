@@ -152,11 +152,11 @@ def test_gemm_prompt_shapes_mfma(dtype, M, K, N):
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
 @pytest.mark.parametrize("M,K,Ns", [(1900, 136, (16456,)), (2048, 264, (16384,)), (2000, 72, (8192, 8200))])
-def test_gemm_prompt_wide_tiles(dtype, M, K, Ns):
-    """Products with at least four 256-row tiles per CU take the 256 x 128
-    tile kernel (16-bit): ragged M and N, K tails inside a 32-k stage, and
-    the grouped form."""
-    print(f"[case] gemm wide {dtype} {M}x{K} -> {Ns}", flush=True)
+def test_gemm_prompt_huge_tiles(dtype, M, K, Ns):
+    """16-bit products with at least two 256 x 256 tiles per CU (520, 512 and
+    520 such tiles here) take the eight-wave 256 x 256 tile kernel: ragged M
+    and N, K tails inside a 32-k stage, and the grouped form."""
+    print(f"[case] gemm huge {dtype} {M}x{K} -> {Ns}", flush=True)
     rng = np.random.default_rng(M + K + sum(Ns))
     a = on.to_storage(rng.standard_normal((M, K), dtype=np.float32), dtype)
     bs = [on.to_storage(rng.standard_normal((K, n), dtype=np.float32) / np.sqrt(K), dtype) for n in Ns]

@@ -13,7 +13,8 @@ from oracle import inputs as oi
 from oracle import numerics as on
 from tests import _helpers as H
 from triton_llm import gpu
-from triton_llm.kernels import apply_rope, flash_attention, flash_attention_strided, precompute_cos_sin
+from triton_llm.kernels import (apply_rope, attention_gqa, flash_attention, flash_attention_strided,
+                                precompute_cos_sin)
 
 pytestmark = pytest.mark.gpu
 
@@ -122,14 +123,58 @@ def test_prefill_fp32_paths(B, Hq, Hkv, sq, sk, causal, d_k):
     compare(f"fp32 sq{sq} sk{sk} d{d_k}", np.nan_to_num(got), np.nan_to_num(exp), TOL[dt])
 
 
-@pytest.mark.parametrize("d_k", [16, 32, 256])
-def test_prefill_generic_head_sizes(d_k):
-    dt = "float32"
-    cfg = oi.Config("generic", "prefill", dt, 1, 4, 2, d_k, 5, 1 / np.sqrt(d_k), seq=70)
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+@pytest.mark.parametrize("d_k", [16, 32, 256, 512, 1024])
+def test_prefill_generic_head_sizes(dtype, d_k):
+    """Head sizes the MFMA kernels do not take run the generic kernel; the
+    reference accepts any power-of-two d_k (attention_gqa.py:230-233), and
+    this build computes up to 4096."""
+    cfg = oi.Config("generic", "prefill", dtype, 1, 4, 2, d_k, 5, 1 / np.sqrt(d_k), seq=70)
     raw = oi.make_prefill_raw(cfg)
     got = gpu_prefill(cfg, raw)
-    exp = oa.attention_bhsd(raw["q"], raw["k"], raw["v"], causal=True, sm_scale=cfg.scale)
-    compare(f"generic d{d_k}", got, exp, TOL[dt])
+    exp = oa.attention_bhsd(raw["q"], raw["k"], raw["v"], causal=True, sm_scale=cfg.scale, dtype=dtype)
+    compare(f"generic {dtype} d{d_k}", got, exp, TOL[dtype])
+
+
+def test_attention_gqa_head_size_512_and_beyond_the_limit():
+    """The drop-in entry point computes d_k 512 (the reference's power-of-two
+    rule) and refuses d_k above 4096 with the ValueError it documents."""
+    rng = np.random.default_rng(512)
+    q = rng.standard_normal((2 * 9, 512), dtype=np.float32)
+    k = rng.standard_normal((1 * 9, 512), dtype=np.float32)
+    v = rng.standard_normal((1 * 9, 512), dtype=np.float32)
+    got = H.attention_gqa_cpu(q, k, v, 2, 1, causal=True)
+    exp = oa.attention_gqa_ref(q, k, v, 2, 1, causal=True)
+    compare("attention_gqa d512", got, exp, TOL["float32"])
+    big = gpu.allocate((2, 8192), np.float32)
+    with pytest.raises(ValueError, match="not supported"):
+        attention_gqa(big, big, big, 1, 1)
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("d_k", [64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_scale_past_fp16_range(dtype, d_k, causal):
+    """sm_scale 4 (4 log2 e = 5.8 in the log2 domain) with q[..., 0] = 60000
+    and k[..., 0] = 0: q * sm_scale * log2 e exceeds the fp16 range (65504)
+    while every score is moderate.  fp16 then scales the scores in fp32
+    instead of pre-scaling Q (which would give inf * 0 = NaN); bf16 keeps
+    fp32's range and pre-scales.  Both must match the oracle."""
+    rng = np.random.default_rng(4000 + d_k + causal)
+    B, Hq, Hkv, S = 1, 6, 2, 300
+    q = 0.1 * rng.standard_normal((B, Hq, S, d_k), dtype=np.float32)
+    k = 0.25 * rng.standard_normal((B, Hkv, S, d_k), dtype=np.float32)
+    v = rng.standard_normal((B, Hkv, S, d_k), dtype=np.float32)
+    q[..., 0] = 60000.0
+    k[..., 0] = 0.0
+    q, k, v = (on.to_storage(x, dtype) for x in (q, k, v))
+    print(f"[case] scale past fp16 range {dtype} d{d_k} causal={causal}", flush=True)
+    o = flash_attention(H.upload(q, dtype), H.upload(k, dtype), H.upload(v, dtype), causal=causal,
+                        sm_scale=4.0)
+    got = on.from_storage(H.download(o), dtype)
+    exp = oa.attention_bhsd(q, k, v, causal=causal, sm_scale=4.0, dtype=dtype)
+    assert np.all(np.isfinite(got))
+    compare(f"scale 4 {dtype} d{d_k} causal={causal}", got, exp, TOL[dtype])
 
 
 @pytest.mark.parametrize("d_k", [64, 128])
@@ -174,7 +219,7 @@ def test_prefill_persistent_schedules(monkeypatch, cus, seq_q, seq_k, n_head, n_
     """The persistent kernel walks several query tiles per workgroup (forced by capping the CU
     count), switching tiles with prefetched Q / K and, after a tile with no visible key, cold;
     d_k 64 and 128 (different LDS tile sizes and load slots)."""
-    monkeypatch.setenv("TRITON_LLM_HIP_MAX_CUS", str(cus))
+    H.set_override(monkeypatch, "TRITON_LLM_HIP_MAX_CUS", cus)
     dtype = "bfloat16"
     cfg = oi.Config("sched", "prefill", dtype, 1, n_head, n_kv, d_k, 77, 1 / np.sqrt(d_k), seq=seq_q)
     print(f"[case] persistent cus={cus} sq={seq_q} sk={seq_k} Hq={n_head} Hkv={n_kv} causal={causal} "

@@ -25,11 +25,11 @@ TOL = {"float32": 2e-3, "float16": 2e-2, "bfloat16": 2e-2}
 CODE = {"float32": _lib.DTYPE_F32, "float16": _lib.DTYPE_F16, "bfloat16": _lib.DTYPE_BF16}
 
 
-@pytest.fixture(autouse=True)
-def _shares_path(monkeypatch):
+@pytest.fixture
+def shares_path(monkeypatch):
     """Small caches would take the pair path, which writes no partials; the
     equal-shares path is the one whose partials live in the static scratch."""
-    monkeypatch.setenv("TRITON_LLM_HIP_DECODE_SHARES", "1")
+    H.set_override(monkeypatch, "TRITON_LLM_HIP_DECODE_SHARES", 1)
 
 
 def _run_both(cfg):
@@ -64,10 +64,14 @@ def _run_both(cfg):
 
 
 def _lib_max_bytes():
-    return 32 << 20  # TL_DECODE_NOALLOC_SCRATCH_BYTES in include/triton_llm_hip.h
+    return _lib.noalloc_scratch_bytes()
 
 
-def test_noalloc_matches_decode_on_two_calls_second_smaller():
+def test_noalloc_scratch_size_is_the_header_limit():
+    assert _lib_max_bytes() == 32 << 20  # TL_DECODE_NOALLOC_SCRATCH_BYTES
+
+
+def test_noalloc_matches_decode_on_two_calls_second_smaller(shares_path):
     big = oi.scaled(oi.CONFIGS["4"], batch=16, max_ctx=4096, lo=1, hi=4095, seed=31)
     small = oi.scaled(oi.CONFIGS["2"], batch=3, max_ctx=300, lo=0, hi=299, seed=32)
     _run_both(big)
@@ -75,10 +79,20 @@ def test_noalloc_matches_decode_on_two_calls_second_smaller():
 
 
 @pytest.mark.parametrize("dtype,d_k", [("float32", 64), ("bfloat16", 128)])
-def test_noalloc_dtypes(dtype, d_k):
+def test_noalloc_dtypes(shares_path, dtype, d_k):
     cfg = oi.Config("noalloc-dt", "decode", dtype, 5, 8, 2, d_k, 33, 1 / np.sqrt(d_k),
                     max_ctx=700, lo=0, hi=699)
     _run_both(cfg)
+
+
+def test_noalloc_pair_mode_default_path():
+    """No override: a small 16-bit d_k 64 cache takes pair mode (one
+    workgroup per (sequence, KV head) that writes the finished output, no
+    partials), twice in a row, the second call smaller."""
+    _run_both(oi.Config("noalloc-pair", "decode", "bfloat16", 6, 12, 4, 64, 34, 0.125,
+                        max_ctx=1024, lo=0, hi=1023))
+    _run_both(oi.Config("noalloc-pair2", "decode", "float16", 2, 6, 2, 64, 35, 0.125,
+                        max_ctx=256, lo=0, hi=255))
 
 
 def test_noalloc_refuses_problems_past_the_scratch():

@@ -144,9 +144,22 @@ hipStream_t tl_resolve_stream(void* stream);
 // HIP graph as a kernel node).
 int tl_fill_bytes(void* dst, unsigned char value, size_t nbytes, hipStream_t st);
 
-// Compute units of the current device (cached per device), capped by the
-// environment variable TRITON_LLM_HIP_MAX_CUS when set (tests use it to force
-// multi-round schedules on small problems).
+// Test-only overrides.  tl_init reads them from the environment on every
+// call (so a test re-reads them by calling tl_init again); launches read only
+// these fields, never the environment.
+//   max_cus        TRITON_LLM_HIP_MAX_CUS: caps the compute units the
+//                  persistent and equal-share schedules plan for (0: none),
+//                  so small problems take multi-round schedules;
+//   decode_shares  TRITON_LLM_HIP_DECODE_SHARES nonzero: small-cache decode
+//                  takes the equal-share path instead of pair mode.
+struct TlOverrides {
+  int max_cus;
+  int decode_shares;
+};
+extern TlOverrides tl_overrides;
+
+// Compute units of the current device (cached per device), capped by
+// tl_overrides.max_cus when set.
 int tl_device_cus();
 
 // ---- matrix-core and LDS helpers shared by the MFMA kernels -------------
@@ -196,6 +209,40 @@ template <>
 __device__ __forceinline__ uint32_t pack2<F16>(const float (&x)[2]) {
   const f16x2 v = {(_Float16)x[0], (_Float16)x[1]};
   return __builtin_bit_cast(uint32_t, v);
+}
+
+// Buffer resource over `bytes` bytes at `base` (raw, no stride) as the four
+// SGPR words an LDS-DMA takes: reads past the end return zeros with no
+// memory access.  Every word is taken from the first lane (callers pass
+// wave-uniform values), so the resource lives in SGPRs.
+__device__ __forceinline__ i32x4 uniform_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+               __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu)),
+               __builtin_amdgcn_readfirstlane((int)bytes), kBufRsrcWord3};
+}
+
+// Global -> LDS copy (buffer_load_dwordx4 ... lds, "LDS-DMA"): lane i's 16
+// bytes at byte offset voff of the resource land at LDS byte address
+// lds_addr + 16 i, with no register round trip.  lds_addr is wave-uniform
+// (an SGPR); the instruction takes it from m0.
+//
+// Inline assembly, not __builtin_amdgcn_raw_ptr_buffer_load_lds: with the
+// builtin the compiler waits for every outstanding LDS-DMA (vmcnt(0))
+// before each later LDS read it cannot prove disjoint from the DMA target,
+// which here includes every ds_read_b64_tr_b16.  That serialises the
+// prefetch of the next key tile behind the current tile's operand reads
+// (measured: the d_k 64 prefill, config 3, fell from 543 to 342 TFLOP/s).
+// So the kernels order the DMAs themselves: each issuing wave waits with
+// wait_vmcnt<0>() before the barrier that publishes the tile.  The compiler
+// does not count these loads, which only makes its own vmcnt waits wait
+// longer (loads return in order), never shorter.  m0 is written here and
+// cannot be declared clobbered (it is a reserved register); the library
+// build (triton_llm/_build.py) therefore rejects any kernel that issues
+// these DMAs and in which compiler-generated code reads or writes m0.
+__device__ __forceinline__ void lds_dma16(const i32x4& rsrc, uint32_t voff, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds_addr), "v"(voff), "s"(rsrc)
+               : "memory");
 }
 
 // s_waitcnt vmcnt(N) (gfx9 encoding; expcnt and lgkmcnt left unconstrained).

@@ -622,13 +622,11 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
 }
 
 // Whether a call runs in pair mode (small caches; see launch_decode_g).
-// (TRITON_LLM_HIP_DECODE_SHARES set to a nonzero value forces the shares,
-// so tests can run both paths on the same small inputs.)
+// (tl_overrides.decode_shares forces the shares, so tests can run both
+// paths on the same small inputs.)
 bool pair_mode(const DecodeParams& p, int d_k, int esize) {
   const int64_t cache_bytes = (int64_t)p.batch * p.n_pairs * p.max_ctx * 2 * d_k * esize;
-  const char* force = getenv("TRITON_LLM_HIP_DECODE_SHARES");
-  const bool shares = force && atoi(force) != 0;
-  return !shares && p.max_ctx <= kPairMaxCtx && cache_bytes <= kPairMaxBytes;
+  return !tl_overrides.decode_shares && p.max_ctx <= kPairMaxCtx && cache_bytes <= kPairMaxBytes;
 }
 
 template <typename T, int D, int G>
@@ -710,6 +708,7 @@ int decode_entry(const void* q, const void* k_cache, const void* v_cache,
 // slots its own split pass wrote), so nothing is cleared; calls that
 // overlap in time on one GPU share the array and race.
 static __device__ __align__(256) unsigned char scratch[TL_DECODE_NOALLOC_SCRATCH_BYTES];
+extern "C" const size_t tl_decode_noalloc_scratch_bytes = sizeof(scratch);
 
 namespace {
 

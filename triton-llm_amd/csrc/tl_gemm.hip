@@ -378,18 +378,11 @@ __global__ __launch_bounds__(64 * NWV, NWV == 8 ? 1 : 2) void gemm_mfma_kernel(G
 
   // Buffer resources over all of A (rows < m) and B (rows < k): rows past
   // them read as zeros with no memory access.
-  auto rsrc = [](const void* base, uint64_t bytes) __attribute__((always_inline)) {
-    const uint64_t a = (uint64_t)(uintptr_t)base;
-    return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
-                 __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu)),
-                 __builtin_amdgcn_readfirstlane((int)(uint32_t)bytes), kBufRsrcWord3};
-  };
   const uint32_t lda2 = (uint32_t)(p.lda * T::size), ldb2 = (uint32_t)(pldb * T::size);
-  const i32x4 ra = rsrc(p.a, (uint64_t)p.m * lda2);
-  const i32x4 rb = rsrc(p.G.b[grp], (uint64_t)p.k * ldb2);
+  const i32x4 ra = uniform_rsrc(p.a, (uint32_t)((uint64_t)p.m * lda2));
+  const i32x4 rb = uniform_rsrc(p.G.b[grp], (uint32_t)((uint64_t)p.k * ldb2));
   auto dma = [&](const i32x4& rs, uint32_t voff, uint32_t la) __attribute__((always_inline)) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(la), "v"(voff), "s"(rs)
-                 : "memory");
+    lds_dma16(rs, voff, la);
   };
   // DMA lane offsets (bytes, stage k0 = 0).  A: region R (1 KiB: 1024 / BKB
   // rows) is filled by wave R % 4; lane i -> row R * (1024 / BKB) + i / ACH,
@@ -678,20 +671,20 @@ __global__ __launch_bounds__(256) void gemm_simple_kernel(GemmParams p) {
 // How a prompt-sized product runs on the MFMA kernel: tile height and K split.
 struct PromptPlan {
   bool huge;      // 16-bit 256 x 256 tiles (eight waves)
-  bool wide;      // 16-bit 256 x 128 tiles
   bool narrow;    // 64 x 128 tiles (few rows: half the padding of 128-row tiles)
   int tiles_m, tiles;
   int ksplit, kt_per;
   size_t ws_bytes;  // fp32 partials when split
 };
 
-// 16-bit: 256-row tiles (each B fragment feeds four MFMAs, 25% less operand
-// traffic per product) when they still give every CU at least four; fewer,
-// larger tiles leave CUs idle on the narrower products.  Measured at a
-// 2048-row Llama-3.2-3B prompt: gate/up 226 -> 219 us; q/k/v, o and down
-// (320 or fewer such tiles) were slower with them.  Where 256 x 256 tiles
-// (eight waves, one workgroup per CU) still give every CU two, they run
-// instead: gate/up 206-209 -> 191 us, the layer 456-462 -> 442 us.
+// 16-bit: 256 x 256 tiles (eight waves, one workgroup per CU; each B
+// fragment feeds four MFMAs) where they still give every CU two: at a
+// 2048-row Llama-3.2-3B prompt gate/up 206-209 -> 191 us, the layer
+// 456-462 -> 442 us.  Fewer, larger tiles leave CUs idle on the narrower
+// products (q/k/v, o and down keep 128 x 128).  (A 256 x 128 tile, taken
+// at four or more per CU, measured gate/up 226 -> 219 us; every shape with
+// four such tiles per CU has at least two 256 x 256 ones, so it was never
+// reached once those existed, and it was removed.)
 //
 // K split (fp32): a CU's time is set by the items it runs, and a whole tile
 // is the unit, so 384 tiles on 256 CUs cost two tiles' time where 1.5 would
@@ -705,25 +698,20 @@ struct PromptPlan {
 PromptPlan prompt_plan(int m, int k, const GemmGroups& G, int esize) {
   PromptPlan P{};
   const int cus = tl_device_cus();
-  int wide_tiles = 0;
   int64_t ncols = 0;
-  for (int g = 0; g < G.count; ++g) {
-    wide_tiles += ((m + 2 * kGmTile - 1) / (2 * kGmTile)) * ((G.n[g] + kGmTile - 1) / kGmTile);
-    ncols += G.n[g];
-  }
+  for (int g = 0; g < G.count; ++g) ncols += G.n[g];
   int huge_tiles = 0;
   for (int g = 0; g < G.count; ++g)
     huge_tiles += ((m + 2 * kGmTile - 1) / (2 * kGmTile)) * ((G.n[g] + 2 * kGmTile - 1) / (2 * kGmTile));
   P.huge = esize == 2 && huge_tiles >= 2 * cus;
-  P.wide = esize == 2 && wide_tiles >= 4 * cus;
-  P.narrow = !P.wide && !P.huge && m <= kNarrowMaxM;
-  const int tm = (P.wide || P.huge) ? 2 * kGmTile : (P.narrow ? kGmTile / 2 : kGmTile);
+  P.narrow = !P.huge && m <= kNarrowMaxM;
+  const int tm = P.huge ? 2 * kGmTile : (P.narrow ? kGmTile / 2 : kGmTile);
   P.tiles_m = (m + tm - 1) / tm;
   P.tiles = 0;
   const int tn = P.huge ? 2 * kGmTile : kGmTile;
   for (int g = 0; g < G.count; ++g) P.tiles += P.tiles_m * ((G.n[g] + tn - 1) / tn);
   // k per LDS stage of the kernel used
-  const int bk = esize == 2 ? ((P.wide || P.huge) ? 32 : (P.narrow ? kNarrowBkb16 / 2 : 64)) : 16;
+  const int bk = esize == 2 ? (P.huge ? 32 : (P.narrow ? kNarrowBkb16 / 2 : 64)) : 16;
   const int n_kt = (k + bk - 1) / bk;
   // modelled seconds: the product at a sustained rate, scaled by the busiest
   // CU's share of items; the reduce as HBM traffic plus a launch
@@ -818,8 +806,6 @@ int launch_gemm(const void* a, const GemmGroups& G, int m, int k, int64_t lda, v
     if constexpr (T::size == 2) {
       if (P.huge)
         hipLaunchKernelGGL((gemm_mfma_kernel<T, 64, 3, 4, 8>), grid, dim3(512), 0, st, p);
-      else if (P.wide)
-        hipLaunchKernelGGL((gemm_mfma_kernel<T, 64, 3, 4>), grid, dim3(kGmThreads), 0, st, p);
       else if (P.narrow)
         hipLaunchKernelGGL((gemm_mfma_kernel<T, kNarrowBkb16, kNarrowNst16, 1>), grid, dim3(kGmThreads), 0, st, p);
       else

@@ -205,7 +205,12 @@ __device__ __forceinline__ int sched_rank(const FlashParams& p, int j, int r) {
   return r * m + ((rr & 1) ? m - 1 - j : j);
 }
 
-template <typename T, int D, bool CAUSAL>
+// SCALE_S: Q is used as stored and each score is scaled in fp32 in the
+// softmax (one FMA per score: s * scale_log2 - m_run) instead of Q being
+// pre-scaled and rounded back to 16 bits.  Taken for fp16 when
+// |sm_scale * log2 e| > 1, where the pre-scaled Q could exceed the fp16
+// range (bf16 has fp32's range; the reference scales q in fp32).
+template <typename T, int D, bool CAUSAL, bool SCALE_S = false>
 __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
   using M = Mfma<T>;
   using frag = typename M::frag;
@@ -304,16 +309,12 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
     return tl;
   };
 
-  auto dma = [&](const i32x4& rsrc, uint32_t voff, uint32_t la) __attribute__((always_inline)) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(la), "v"(voff), "s"(rsrc)
-                 : "memory");
+  using rsrc_t = i32x4;
+  auto dma = [&](const rsrc_t& rsrc, uint32_t voff, uint32_t la) __attribute__((always_inline)) {
+    lds_dma16(rsrc, voff, la);
   };
   auto rsrc_of = [&](const char* base, uint32_t bytes) __attribute__((always_inline)) {
-    const uint64_t a = (uint64_t)(uintptr_t)base;
-    // every word wave-uniform, so the resource stays in SGPRs
-    return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
-                 __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu)),
-                 __builtin_amdgcn_readfirstlane((int)bytes), kBufRsrcWord3};
+    return uniform_rsrc(base, bytes);
   };
   // K tile tk of a tile: rows past its k_rows read as zeros, no traffic.
   auto k_rsrc = [&](const Tile& tl, int tk) __attribute__((always_inline)) {
@@ -354,6 +355,7 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
   u32x4 pw[BN / 16];  // P_t packed 16-bit
 
   auto scale_q = [&]() __attribute__((always_inline)) {
+    if constexpr (SCALE_S) return;
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
       const u32x4 raw = __builtin_bit_cast(u32x4, qf[ks]);
@@ -373,7 +375,7 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
   auto cold_start = [&](const Tile& tl, int kb) __attribute__((always_inline)) {
     const int ln = fresh_lane();
     const int h = ln >> 5;
-    const i32x4 rk = k_rsrc(tl, 0);
+    const rsrc_t rk = k_rsrc(tl, 0);
     const uint32_t kvo = kq_off(ln, p.k_ss);
 #pragma unroll
     for (int i = group; i < RPW; i += 2) dma(rk, kvo + (uint32_t)i * k_step, lds_k0 + kb * TILEB + i * 4096 + wave_lds);
@@ -439,13 +441,13 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
       constexpr bool DO_PV = decltype(pv_tag)::value;
       constexpr bool DO_S = decltype(s_tag)::value;
       const int ln = fresh_lane();
-      i32x4 rk = {0, 0, 0, 0}, rv = {0, 0, 0, 0};
+      rsrc_t rk = {0, 0, 0, 0}, rv = {0, 0, 0, 0};
       uint32_t kvo = 0, vvo = 0, kstep = k_step, vstep = v_step;
       if constexpr (DO_DMA) {
         // K slot: K_{t+1}; at t = n_kt - 1 group 0's next Q rows (K_{n_kt}
         // is never used: G(n_kt) computes no S); at t = n_kt the next K_0.
         // V slot: V^T_t; at t = n_kt group 1's next Q rows.
-        const i32x4 none = rsrc_of(cur.kg, 0u);
+        const rsrc_t none = rsrc_of(cur.kg, 0u);
         if (t < n_kt - 1) {
           rk = k_rsrc(cur, t + 1);
           kvo = kq_off(ln, p.k_ss);
@@ -546,6 +548,13 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
         __builtin_amdgcn_sched_barrier(0);
         return;
       }
+      if constexpr (SCALE_S) {
+        // raw scores -> log2 domain relative to m_run (s_init stays 0)
+#pragma unroll
+        for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+          for (int rr = 0; rr < 16; ++rr) s[mb][rr] = fmaf(s[mb][rr], p.scale_log2, -m_run);
+      }
       const bool need_mask = (kb + BN > p.seq_k) || (CAUSAL && kb + BN - 1 > q0 + off);
       if (need_mask) {
         const int ln = fresh_lane();
@@ -593,8 +602,10 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
         for (int mb = 0; mb < NMB; ++mb)
 #pragma unroll
           for (int rr = 0; rr < 16; ++rr) s[mb][rr] -= delta;
+        if constexpr (!SCALE_S) {
 #pragma unroll
-        for (int rr = 0; rr < 16; ++rr) s_init[rr] = -m_run;
+          for (int rr = 0; rr < 16; ++rr) s_init[rr] = -m_run;
+        }
       }
       // P chunk tt (keys 16 tt..) = s[tt / 2][8 (tt % 2) + 0..7]; fp32 row sums
       // (v_dot2 does not co-execute with the partner's MFMAs).
@@ -1152,14 +1163,22 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(const uint16_t* __restrict
 }
 
 // ---------------------------------------------------------------------------
-// Generic fallback for head sizes the MFMA kernels do not cover (any d_k up
-// to 256): one wave per (query row, head), keys in tiles of 64 with the
-// reference's online softmax.
+// Generic kernel for what the MFMA kernels do not cover: any power-of-two d_k
+// up to kGenericMaxD (the reference accepts any power of two), strides that
+// are not 16-byte multiples, and fp16 with a scale that would overflow a
+// pre-scaled Q.  One wave per (query row, head), keys in tiles of 64 with
+// the reference's online softmax, all in fp32.  The scaled query row and the
+// output accumulator live in LDS (2 * d_k floats, dynamic), lane l owning
+// accumulator entries l, l + 64, ...
 // ---------------------------------------------------------------------------
+constexpr int kGenericMaxD = 4096;
+
 template <typename T>
 __global__ __launch_bounds__(64) void attn_generic_kernel(FlashParams p, int D, int causal) {
   using Bits = typename T::bits;
-  __shared__ float qs[256];
+  extern __shared__ float gsm[];
+  float* qs = gsm;       // [D]
+  float* acc = gsm + D;  // [D]
   __shared__ float ps[64];
   const int qi = blockIdx.x;
   const int hq = blockIdx.y;
@@ -1167,12 +1186,14 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(FlashParams p, int D, 
   const int hkv = hq / p.group;
   const int lane = threadIdx.x;
   const Bits* qrow = (const Bits*)p.q + b * p.q_sb + hq * p.q_sh + (int64_t)qi * p.q_ss;
-  for (int d = lane; d < D; d += 64) qs[d] = to_f32<T>(qrow[d]);
+  for (int d = lane; d < D; d += 64) {
+    qs[d] = to_f32<T>(qrow[d]);
+    acc[d] = 0.f;
+  }
   __syncthreads();
   const Bits* kb = (const Bits*)p.k + b * p.k_sb + hkv * p.k_sh;
   const Bits* vb = (const Bits*)p.v + b * p.v_sb + hkv * p.v_sh;
   const int limit = causal ? min(p.seq_k, qi + (p.seq_k - p.seq_q) + 1) : p.seq_k;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
   const float c = p.scale_log2;
   for (int k0 = 0; k0 < p.seq_k; k0 += 64) {
@@ -1198,26 +1219,18 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(FlashParams p, int D, 
     ps[lane] = pk;
     __syncthreads();
     const int n = min(64, p.seq_k - k0);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int d = lane + 64 * j;
-      if (d < D) {
-        float a = acc[j] * alpha;
-        for (int kk = 0; kk < n; ++kk) {
-          const float pw = ps[kk];
-          if (pw != 0.f) a = fmaf(pw, to_f32<T>(vb[(int64_t)(k0 + kk) * p.v_ss + d]), a);
-        }
-        acc[j] = a;
+    for (int d = lane; d < D; d += 64) {
+      float a = acc[d] * alpha;
+      for (int kk = 0; kk < n; ++kk) {
+        const float pw = ps[kk];
+        if (pw != 0.f) a = fmaf(pw, to_f32<T>(vb[(int64_t)(k0 + kk) * p.v_ss + d]), a);
       }
+      acc[d] = a;
     }
   }
   Bits* orow = (Bits*)p.o + b * p.o_sb + hq * p.o_sh + (int64_t)qi * p.o_ss;
   const float inv = 1.f / l_run;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int d = lane + 64 * j;
-    if (d < D) orow[d] = from_f32<T>(acc[j] * inv);
-  }
+  for (int d = lane; d < D; d += 64) orow[d] = from_f32<T>(acc[d] * inv);
 }
 
 inline bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
@@ -1230,6 +1243,8 @@ size_t vt_bytes(int batch, int n_kv, int seq_k, int d_k) {
 
 template <typename T, int D>
 int launch_flash_16(FlashParams& p, void* ws, bool causal, hipStream_t st) {
+  // fp16 Q pre-scaled by |sm_scale log2 e| > 1 could overflow: scale scores instead
+  const bool scale_s = std::is_same<T, F16>::value && fabsf(p.scale_log2) > 1.f;
   p.vt = ws;
   p.n_qt = (p.seq_q + K16_BM - 1) / K16_BM;
   // Tile lists: one per XCD when the (batch, kv head) units split evenly.
@@ -1249,6 +1264,15 @@ int launch_flash_16(FlashParams& p, void* ws, bool causal, hipStream_t st) {
     if (e) return e;
   }
   dim3 grid((unsigned)(p.q_machines * p.n_queues));
+  if constexpr (std::is_same<T, F16>::value) {
+    if (scale_s) {
+      if (causal)
+        hipLaunchKernelGGL((flash_fwd_16<T, D, true, true>), grid, dim3(K16_THREADS), 0, st, p);
+      else
+        hipLaunchKernelGGL((flash_fwd_16<T, D, false, true>), grid, dim3(K16_THREADS), 0, st, p);
+      return tl_launch_status();
+    }
+  }
   if (causal)
     hipLaunchKernelGGL((flash_fwd_16<T, D, true>), grid, dim3(K16_THREADS), 0, st, p);
   else
@@ -1280,7 +1304,7 @@ int launch_flash_f32(FlashParams& p, bool causal, hipStream_t st) {
 template <typename T>
 int launch_generic(FlashParams& p, int d_k, bool causal, hipStream_t st) {
   dim3 grid(p.seq_q, p.n_head, p.batch);
-  hipLaunchKernelGGL(attn_generic_kernel<T>, grid, dim3(64), 0, st, p, d_k, causal ? 1 : 0);
+  hipLaunchKernelGGL(attn_generic_kernel<T>, grid, dim3(64), 2 * d_k * sizeof(float), st, p, d_k, causal ? 1 : 0);
   return tl_launch_status();
 }
 
@@ -1328,9 +1352,10 @@ int tl_attention_fwd(const void* q, const void* k, const void* v, void* o, void*
                      void* stream) {
   if (batch == 0 || n_head == 0 || seq_q == 0) return 0;
   if (!q || !k || !v || !o || batch < 0 || n_head < 0 || n_kv_head < 1 ||
-      n_head % n_kv_head != 0 || seq_q < 0 || seq_k < 1 || d_k < 1 || d_k > 256 ||
+      n_head % n_kv_head != 0 || seq_q < 0 || seq_k < 1 || d_k < 1 ||
       !q_strides || !k_strides || !v_strides || !o_strides)
     return TL_ERR_INVALID;
+  if (d_k > kGenericMaxD) return TL_ERR_UNSUPPORTED;
   FlashParams p{};
   p.q = q;
   p.k = k;

@@ -54,12 +54,19 @@ int tl_device_cus() {
     }
     n = cus[dev];
   }
-  if (const char* cap = getenv("TRITON_LLM_HIP_MAX_CUS")) {
-    const int c = atoi(cap);
-    if (c > 0 && c < n) n = c;
-  }
+  const int c = tl_overrides.max_cus;
+  if (c > 0 && c < n) n = c;
   return n;
 }
+
+TlOverrides tl_overrides = {0, 0};
+
+namespace {
+int env_int(const char* name) {
+  const char* v = getenv(name);
+  return v ? atoi(v) : 0;
+}
+}  // namespace
 
 extern "C" {
 
@@ -72,6 +79,8 @@ int tl_device_count(int* count) {
 }
 
 int tl_init(int device) {
+  tl_overrides.max_cus = env_int("TRITON_LLM_HIP_MAX_CUS");
+  tl_overrides.decode_shares = env_int("TRITON_LLM_HIP_DECODE_SHARES") != 0;
   if (g_stream && g_device == device) return 0;
   hipError_t e = hipSetDevice(device);
   if (e != hipSuccess) return (int)e;

@@ -12,6 +12,7 @@ from __future__ import annotations
 
 import concurrent.futures
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -57,15 +58,69 @@ def sources() -> list[str]:
     )
 
 
+# Instructions that read or write m0 without naming it.
+_M0_IMPLICIT = re.compile(r"\b(s_movrel|v_movrel|s_sendmsg|ds_gws|ds_read_addtid|ds_write_addtid|v_interp|"
+                          r"s_ttracedata)")
+_M0_NAMED = re.compile(r"\bm0\b")
+
+
+def check_m0(asm_text: str, source: str) -> int:
+    """Reject a kernel that issues the inline-asm LDS-DMA (csrc/tl_common.h
+    lds_dma16, which writes m0) and in which compiler-generated code reads
+    or writes m0 too.  m0 is a reserved register, so the asm cannot declare
+    it clobbered; this check, run on every build, is what makes that asm
+    safe: no value of the compiler's lives in m0 around it.  Returns the
+    number of kernels that issue the DMA."""
+    funcs: dict[str, list] = {}  # name -> [issues the asm DMA, compiler m0 uses]
+    name, in_asm = None, False
+    for line in asm_text.splitlines():
+        m = re.match(r"\s*\.type\s+([^,\s]+)\s*,\s*@function", line)
+        if m:
+            name, in_asm = m.group(1), False
+            funcs[name] = [False, []]
+            continue
+        if name is None:
+            continue
+        if ";;#ASMSTART" in line:
+            in_asm = True
+            continue
+        if ";;#ASMEND" in line:
+            in_asm = False
+            continue
+        code = line.split(";", 1)[0]
+        if in_asm:
+            funcs[name][0] = funcs[name][0] or code.rstrip().endswith(" lds")
+        elif _M0_NAMED.search(code) or _M0_IMPLICIT.search(code) or code.rstrip().endswith(" lds"):
+            funcs[name][1].append(code.strip())
+    bad = [f"{n}: {uses[:3]}" for n, (dma, uses) in funcs.items() if dma and uses]
+    if bad:
+        raise RuntimeError(f"{os.path.basename(source)}: compiler-generated code uses m0 in kernels that issue "
+                           f"the inline-asm LDS-DMA (which writes m0):\n  " + "\n  ".join(bad))
+    return sum(1 for dma, _ in funcs.values() if dma)
+
+
 def _compile_one(src: str, obj: str) -> None:
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-c", src, "-o", obj]
-    res = subprocess.run(cmd, capture_output=True, text=True)
+    # -save-temps=obj leaves the device assembly next to the object (in the
+    # build's temporary directory) for check_m0.
+    cmd = [_hipcc(), *HIPCC_FLAGS, "-save-temps=obj", "-c", src, "-o", obj]
+    res = subprocess.run(cmd, capture_output=True, text=True, cwd=os.path.dirname(obj))
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {os.path.basename(src)}:\n{err}")
     if err.strip():
         print(err, file=sys.stderr)
+    stem = os.path.splitext(os.path.basename(src))[0]
+    asm = os.path.join(os.path.dirname(obj), f"{stem}-hip-amdgcn-amd-amdhsa-{OFFLOAD_ARCH}.s")
+    if not os.path.exists(asm):
+        raise RuntimeError(f"device assembly {asm} missing: cannot check m0 use")
+    with open(asm) as f:
+        n_dma = check_m0(f.read(), src)
+    with open(src) as f:
+        calls_dma = "lds_dma16(" in f.read()
+    if calls_dma and n_dma == 0:
+        raise RuntimeError(f"{os.path.basename(src)} calls lds_dma16 but check_m0 found no kernel issuing it: "
+                           "the guard no longer recognises the DMA")
 
 
 def build(verbose: bool = True, jobs: int | None = None) -> str:

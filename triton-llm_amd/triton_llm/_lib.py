@@ -131,6 +131,13 @@ def load() -> ctypes.CDLL:
     return lib
 
 
+def noalloc_scratch_bytes() -> int:
+    """Size of tl_attention_decode_noalloc's static scratch, read from the
+    loaded library's data symbol (the header's
+    TL_DECODE_NOALLOC_SCRATCH_BYTES)."""
+    return int(ctypes.c_size_t.in_dll(load(), "tl_decode_noalloc_scratch_bytes").value)
+
+
 def strides(*vals: int) -> ctypes.Array:
     """Pack element strides into the int64[] the C ABI takes."""
     arr = (ctypes.c_int64 * len(vals))(*[int(v) for v in vals])

@@ -103,6 +103,14 @@ def _initialize():
     _initialized = True
 
 
+def reload_overrides():
+    """Make the library re-read its test-only environment overrides
+    (TRITON_LLM_HIP_MAX_CUS, TRITON_LLM_HIP_DECODE_SHARES), which it reads
+    in tl_init, never per launch.  Does nothing before the first GPU use."""
+    if _initialized:
+        check_error(_rt.tl_init(int(os.environ.get("TRITON_LLM_DEVICE", "0"))))
+
+
 def runtime():
     """The loaded HIP library (initialising on first use)."""
     _initialize()

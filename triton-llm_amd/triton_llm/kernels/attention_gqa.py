@@ -27,6 +27,10 @@ from ._common import launch, check_status, default_scale, same_dtype, shared_wor
 from triton_llm import _lib
 
 DECODE_D = (64, 128)
+# Largest head size the library computes (its generic kernel keeps a query
+# row and an accumulator row of d_k floats in LDS).  The reference accepts
+# any power of two; above this one this build raises.
+MAX_D = 4096
 
 
 def attention_gqa(
@@ -86,8 +90,8 @@ def attention_gqa(
         raise ValueError(
             f"d_k ({d_k}) must be a positive power of 2"
         )
-    if d_k > 256:
-        raise ValueError(f"d_k ({d_k}) > 256 is not supported by the HIP kernels")
+    if d_k > MAX_D:
+        raise ValueError(f"d_k ({d_k}) > {MAX_D} is not supported by the HIP kernels")
 
     if sm_scale is None:
         sm_scale = default_scale(d_k)

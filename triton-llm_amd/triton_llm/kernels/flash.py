@@ -21,6 +21,7 @@ import numpy as np
 from triton_llm import gpu
 from triton_llm import _lib
 from ._common import launch, check_status, contiguous_strides, default_scale, same_dtype, scratch, vp
+from .attention_gqa import MAX_D
 
 
 def flash_workspace_bytes(batch: int, n_kv_head: int, seq_k: int, d_k: int, dtype) -> int:
@@ -34,8 +35,8 @@ def flash_attention_strided(q, k, v, out, *, batch, n_head, n_kv_head, seq_q, se
     """Launch the flash kernel on raw layouts given by element strides."""
     if n_head <= 0 or n_kv_head <= 0 or n_head % n_kv_head:
         raise ValueError(f"n_head ({n_head}) must be a positive multiple of n_kv_head ({n_kv_head})")
-    if not (d_k > 0 and (d_k & (d_k - 1)) == 0 and d_k <= 256):
-        raise ValueError(f"d_k ({d_k}) must be a power of 2 <= 256")
+    if not (d_k > 0 and (d_k & (d_k - 1)) == 0 and d_k <= MAX_D):
+        raise ValueError(f"d_k ({d_k}) must be a power of 2 <= {MAX_D}")
     code = same_dtype(q, k, v, out)
     if batch == 0 or seq_q == 0:
         return out
