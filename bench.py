@@ -15,7 +15,13 @@ decode-step HBM throughput (GB/s), the headline; 5a is repeated in the
 ``cpu_baseline`` (the NumPy oracle of the same attention, a bounded number of
 passes on this host's cores).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config all|5|1|2|3|4|5a|5b]
+``append-5a`` and ``append-3`` time the fused RoPE + KV append at those
+prefill configs' full prompts (what the GPU-resident cache runs before
+prefill attention), HBM-bound, with the oracle's NumPy append as the CPU
+baseline.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+                       [--config all|5|append|1|2|3|4|5a|5b|append-5a|append-3]
 """
 
 from __future__ import annotations
@@ -589,6 +595,112 @@ def cpu_prefill_baseline(cfg, raw, oa, on, oi, budget_s=10.0):
     }
 
 
+# ---------------------------------------------------------------------------
+# prompt-size RoPE + KV append (what the GPU-resident cache runs before prefill)
+# ---------------------------------------------------------------------------
+
+APPEND_CASES = {
+    # name: (prefill config whose prompt it appends, workload name)
+    "append-5a": ("5a", "llama3.2-3b-prompt-rope-append-bf16"),
+    "append-3": ("3", "smollm2-135m-prompt-rope-append-bf16"),
+}
+
+
+def append_bytes(cfg):
+    """Algorithmic HBM bytes of one S-token append into an empty cache: q read
+    and written (rotated in place), k_new read and written to the cache
+    (rotated), v_new read and written to the cache, and the cos / sin table
+    rows of the S positions read once (2 x d_k / 2 fp32 each)."""
+    e = 4 if cfg.dtype == "float32" else 2
+    B, S, Hq, Hkv, D = cfg.batch, cfg.seq, cfg.n_head, cfg.n_kv_head, cfg.d_k
+    return 2 * B * S * (Hq + 2 * Hkv) * D * e + S * D * 4
+
+
+def bench_append(name, steps, warmup, cpu=True, cpu_budget_s=4.0, ramp_ms=0.0):
+    """tl_rope_kv_append at a prefill config's full prompt, as
+    GpuKVCache.attention runs it (rows (B, S, H, D), an empty cache of
+    capacity S, RoPE tables of S rows).  Input replicas rotate so that >= 1
+    GB of other data passes between two uses of one set."""
+    from oracle import inputs as oi
+    from oracle import numerics as on
+    from oracle import rope as orope
+    from triton_llm import gpu
+    from triton_llm.kernels import precompute_cos_sin, rope_kv_append
+    from triton_llm.kernels._common import record
+
+    base, workload = APPEND_CASES[name]
+    cfg = oi.CONFIGS[base]
+    dt = cfg.dtype
+    gdt = {"bfloat16": gpu.bfloat16, "float16": np.float16, "float32": np.float32}[dt]
+    B, S, Hq, Hkv, D = cfg.batch, cfg.seq, cfg.n_head, cfg.n_kv_head, cfg.d_k
+    rng = np.random.default_rng(cfg.seed)
+    q = on.to_storage(rng.standard_normal((B, S, Hq, D), dtype=np.float32), dt)
+    kn = on.to_storage(rng.standard_normal((B, S, Hkv, D), dtype=np.float32), dt)
+    vn = on.to_storage(rng.standard_normal((B, S, Hkv, D), dtype=np.float32), dt)
+    cos, sin = precompute_cos_sin(S, D, cfg.rope_theta)
+    cd, sd = gpu.to_device(cos), gpu.to_device(sin)
+    lens = gpu.to_device(np.zeros(B, np.int32))
+    nbytes = append_bytes(cfg)
+    replicas = max(1, int(np.ceil(1024e6 / nbytes)))
+    sets = []
+    for _ in range(replicas):
+        sets.append((gpu.to_device(q, gdt), gpu.to_device(kn, gdt), gpu.to_device(vn, gdt),
+                     gpu.zeros((B, Hkv, S, D), gdt), gpu.zeros((B, Hkv, S, D), gdt)))
+    lib = gpu.runtime()
+
+    def step(i):
+        qd, kd, vd, kc, vc = sets[i % replicas]
+        rope_kv_append(qd, kd, vd, kc, vc, lens, cd, sd)
+
+    calls = [record(lambda i=i: step(i)) for i in range(replicas)]
+    ms, ramp, wall_ms = time_calls(lib, calls, steps, warmup, ramp_ms)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    res = {
+        "value": gbs,
+        "unit": "GB/s",
+        "ms_per_step": ms,
+        "wall_ms_per_step": wall_ms,
+        "timing": f"{steps} calls enqueued back to back between two events (C-ABI launch recorded from "
+                  f"the wrapper), cycling over {replicas} input replica(s)",
+        "clock_ramp": {"calls": ramp[0], "ms": round(ramp[1], 1)},
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "rope_kv_append_vec_kernel (tl_rope_kv_append)",
+            "achieved": gbs,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": gbs / HBM_PEAK_GBS,
+            "traffic": profile_traffic(f"rope_kv_append_{workload}.md"),
+            "algorithmic_bytes": nbytes,
+            "kernel_ms": ms,
+        },
+    }
+    if cpu:
+        # The oracle's restatement of the same append on host storage: q and
+        # k rotated in fp32 and rounded to the storage type, k and v written
+        # into an empty cache; whole workload, repeated for cpu_budget_s.
+        kc_h = np.zeros((B, Hkv, S, D), kn.dtype)
+        vc_h = np.zeros((B, Hkv, S, D), vn.dtype)
+        pos = np.arange(S)[:, None]
+        passes, t_total = [], 0.0
+        while t_total < cpu_budget_s or len(passes) < 3:
+            t0 = time.perf_counter()
+            for b in range(B):
+                orope.apply_rope_storage(q[b], cos, sin, pos, dt)
+                kc_h[b] = np.swapaxes(orope.apply_rope_storage(kn[b], cos, sin, pos, dt), 0, 1)
+                vc_h[b] = np.swapaxes(vn[b], 0, 1)
+            passes.append(time.perf_counter() - t0)
+            t_total += passes[-1]
+        t = float(np.median(passes))
+        res["cpu_baseline"] = {
+            "value": nbytes / t / 1e9, "unit": "GB/s", "cores": 1, "host": cpu_host(), "kind": "port",
+            "sample": f"the whole workload ({B} x {S} tokens), the oracle's NumPy RoPE + cache write "
+                      f"(oracle/rope.py apply_rope_storage; elementwise NumPy, one thread), median of "
+                      f"{len(passes)} passes ({t_total:.1f}s); bytes counted as the GPU's",
+        }
+    return res
+
+
 def copy_probe(mib):
     """Five plain device-to-device copies of ``mib`` MiB each (one blit kernel
     per copy): a dispatch of known HBM traffic -- mib MiB read, mib MiB
@@ -728,8 +840,9 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="all",
-                    help="all (default: every BASELINE config, headline 5b), 5 (5a + 5b), or one of "
-                         "1 2 3 4 5a 5b")
+                    help="all (default: every BASELINE config, headline 5b, plus the prompt-size RoPE + "
+                         "KV append of 5a and 3), 5 (5a + 5b), append (both appends), or one of "
+                         "1 2 3 4 5a 5b append-5a append-3")
     # The GPU's shader clock climbs over the first tens of milliseconds of
     # sustained load: each config first runs its own step untimed for this long
     # (measured: 5 warm-up steps alone left 5a ~10% slow).
@@ -786,9 +899,19 @@ def main():
         print(json.dumps(bench_gemm(min(args.steps, 20), min(args.warmup, 5), cpu=cpu,
                                     vs_rocblas=args.gemm_rocblas)))
         return
-    sel = {"5": ["5a", "5b"], "all": ["1", "2", "3", "4", "5a", "5b"]}.get(args.config, [args.config])
+    sel = {"5": ["5a", "5b"], "all": ["1", "2", "3", "4", "5a", "5b", "append-5a", "append-3"],
+           "append": ["append-5a", "append-3"]}.get(args.config, [args.config])
     results = {}
     for name in sel:
+        if name in APPEND_CASES:
+            log(f"config {name}: {APPEND_CASES[name][1]}")
+            results[name] = bench_append(name, args.steps, args.warmup, cpu=cpu,
+                                         cpu_budget_s=args.cpu_budget_s, ramp_ms=args.clock_ramp_ms)
+            results[name]["workload"] = APPEND_CASES[name][1]
+            gpu.empty_cache()
+            log(f"config {name}: {results[name]['value']:.1f} GB/s "
+                f"({results[name]['roofline']['frac'] * 100:.1f}% of roofline)")
+            continue
         cfg = oi.CONFIGS[name]
         log(f"config {name}: {cfg.name}")
         kw = dict(cpu=cpu, cpu_budget_s=args.cpu_budget_s, ramp_ms=args.clock_ramp_ms)
@@ -810,7 +933,7 @@ def main():
 
     head = "5b" if "5b" in results else sel[0]
     r = results[head]
-    cfg = oi.CONFIGS[head]
+    cfg = oi.CONFIGS[APPEND_CASES[head][0] if head in APPEND_CASES else head]
     line = {
         "metric": METRIC,
         "value": r["value"],
@@ -825,7 +948,8 @@ def main():
         "dtype": DT_SHORT[cfg.dtype],
         "data": "synthetic (seeded N(0,1) q/k/v per BASELINE config; decode lengths drawn U[lo, hi])",
         "config": {
-            "workload": f"{cfg.name} (config {head})" + (" + llama3.2-3b-prefill-bf16 (config 5a)" if "5a" in results and head == "5b" else ""),
+            "workload": (r["workload"] if head in APPEND_CASES else f"{cfg.name} (config {head})")
+                        + (" + llama3.2-3b-prefill-bf16 (config 5a)" if "5a" in results and head == "5b" else ""),
             "batch": cfg.batch, "n_head": cfg.n_head, "n_kv_head": cfg.n_kv_head, "d_k": cfg.d_k,
             "max_ctx": cfg.max_ctx or None, "seq": cfg.seq or None,
         },
