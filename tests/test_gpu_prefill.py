@@ -21,6 +21,21 @@ pytestmark = pytest.mark.gpu
 TOL = {"float32": 2e-3, "float16": 2e-2, "bfloat16": 2e-2}
 
 
+@pytest.fixture(params=["w32", "w64"])
+def d128_kernel(request, monkeypatch):
+    """16-bit d_k 128 prefill has two kernels: 32 query rows per wave (the
+    default) and 64 rows per wave (TRITON_LLM_HIP_PREFILL_W64); tests that
+    take this fixture run on both.  Other d_k / dtypes have one kernel, so
+    their second run is skipped."""
+    H.set_override(monkeypatch, "TRITON_LLM_HIP_PREFILL_W64", 1 if request.param == "w64" else None)
+    return request.param
+
+
+def skip_w64_repeat(kernel, d_k, dtype="bfloat16"):
+    if kernel == "w64" and (d_k != 128 or dtype == "float32"):
+        pytest.skip("one prefill kernel for this d_k / dtype")
+
+
 def gpu_prefill(cfg, raw, causal=True):
     dt = cfg.dtype
     B, Hq, Hkv, S, D = cfg.batch, cfg.n_head, cfg.n_kv_head, cfg.seq, cfg.d_k
@@ -71,8 +86,9 @@ def test_prefill_config_5a_full_size_sampled_rows():
 @pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
 @pytest.mark.parametrize("d_k", [64, 128])
 @pytest.mark.parametrize("causal", [True, False])
-def test_prefill_ragged_shapes(dtype, d_k, causal):
+def test_prefill_ragged_shapes(d128_kernel, dtype, d_k, causal):
     # seq not a multiple of either tile size; GQA group 3; batch 2.
+    skip_w64_repeat(d128_kernel, d_k, dtype)
     cfg = oi.Config("ragged", "prefill", dtype, 2, 6, 2, d_k, 21, 1 / np.sqrt(d_k), seq=200)
     raw = oi.make_prefill_raw(cfg)
     got = gpu_prefill(cfg, raw, causal=causal)
@@ -82,9 +98,10 @@ def test_prefill_ragged_shapes(dtype, d_k, causal):
 
 @pytest.mark.parametrize("d_k", [64, 128])
 @pytest.mark.parametrize("sq,sk", [(1, 1), (1, 300), (37, 300), (130, 129), (64, 64), (5, 3), (300, 700)])
-def test_prefill_seq_q_ne_seq_k(sq, sk, d_k):
+def test_prefill_seq_q_ne_seq_k(d128_kernel, sq, sk, d_k):
     """Bottom-right causal alignment; sq > sk leaves the first rows fully masked (NaN).
     d_k 64 reads V in place, d_k 128 through its V^T copy."""
+    skip_w64_repeat(d128_kernel, d_k)
     dt = "bfloat16"
     rng = np.random.default_rng(sq * 1000 + sk + d_k)
     B, Hq, Hkv, D = 1, 4, 2, d_k
@@ -215,10 +232,11 @@ def test_prefill_reads_cache_layout_and_seq_major_rows():
     (8, 768, 768, 6, 2, True),       # 2 (batch, kv) units: one list, 3 workgroups
 ])
 @pytest.mark.parametrize("d_k", [64, 128])
-def test_prefill_persistent_schedules(monkeypatch, cus, seq_q, seq_k, n_head, n_kv, causal, d_k):
+def test_prefill_persistent_schedules(monkeypatch, d128_kernel, cus, seq_q, seq_k, n_head, n_kv, causal, d_k):
     """The persistent kernel walks several query tiles per workgroup (forced by capping the CU
     count), switching tiles with prefetched Q / K and, after a tile with no visible key, cold;
     d_k 64 and 128 (different LDS tile sizes and load slots)."""
+    skip_w64_repeat(d128_kernel, d_k)
     H.set_override(monkeypatch, "TRITON_LLM_HIP_MAX_CUS", cus)
     dtype = "bfloat16"
     cfg = oi.Config("sched", "prefill", dtype, 1, n_head, n_kv, d_k, 77, 1 / np.sqrt(d_k), seq=seq_q)
@@ -234,3 +252,70 @@ def test_prefill_persistent_schedules(monkeypatch, cus, seq_q, seq_k, n_head, n_
     exp = oa.attention_bhsd(q, k, v, causal=causal, sm_scale=cfg.scale, dtype=dtype)
     np.testing.assert_array_equal(np.isnan(got), np.isnan(exp))
     compare(f"persistent cus={cus} sq={seq_q} sk={seq_k}", np.nan_to_num(got), np.nan_to_num(exp), TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("sq,sk,causal", [
+    (64, 64, True),      # one key tile (the stream pads to two; the second reads zeros)
+    (65, 65, True),      # a wave with one row; keys past seq_k in the first 64-key tile
+    (200, 40, False),    # seq_k < 64, non-causal
+    (130, 100, True),    # bottom-right causal with sq > sk: the first rows see no key (NaN)
+    (257, 257, True),    # two query tiles, the second with one row (three waves without rows)
+    (520, 2000, True),   # sq < sk: every row sees the first 1481 keys
+    (1000, 1000, False),
+])
+def test_prefill_w64_edges(monkeypatch, dtype, sq, sk, causal):
+    """The d_k 128 kernel with 64 rows per wave: 64-key tiles padded to two
+    per query tile, waves whose rows end early or do not exist, keys past
+    seq_k inside a tile, fully masked rows."""
+    H.set_override(monkeypatch, "TRITON_LLM_HIP_PREFILL_W64", 1)
+    rng = np.random.default_rng(7 * sq + sk + causal)
+    B, Hq, Hkv, D = 2, 6, 2, 128
+    print(f"[case] w64 edge {dtype} sq={sq} sk={sk} causal={causal}", flush=True)
+    q = on.to_storage(rng.standard_normal((B, Hq, sq, D), dtype=np.float32), dtype)
+    k = on.to_storage(rng.standard_normal((B, Hkv, sk, D), dtype=np.float32), dtype)
+    v = on.to_storage(rng.standard_normal((B, Hkv, sk, D), dtype=np.float32), dtype)
+    o = flash_attention(H.upload(q, dtype), H.upload(k, dtype), H.upload(v, dtype), causal=causal)
+    got = on.from_storage(H.download(o), dtype)
+    exp = oa.attention_bhsd(q, k, v, causal=causal, dtype=dtype)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(exp))
+    compare(f"w64 edge {dtype} sq{sq} sk{sk}", np.nan_to_num(got), np.nan_to_num(exp), TOL[dtype])
+
+
+@pytest.mark.parametrize("kernel", ["w64", "w32"])
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_growing_scores_rescale(monkeypatch, kernel, causal):
+    """Scores that rise along the keys: q[..., 0] = 1 and k[j, 0] = 2.35 j
+    add about 0.3 (log2 units) per key on top of moderate noise, so each
+    row's running maximum passes the lazy-rescale threshold (8) about every
+    27 keys and the accumulated output is rescaled some 25 times per row,
+    while the softmax stays well conditioned (weights spread over the last
+    few keys)."""
+    H.set_override(monkeypatch, "TRITON_LLM_HIP_PREFILL_W64", 1 if kernel == "w64" else None)
+    dtype = "bfloat16"
+    rng = np.random.default_rng(99 + causal)
+    B, Hq, Hkv, S, D = 1, 4, 2, 700, 128
+    q = 0.5 * rng.standard_normal((B, Hq, S, D), dtype=np.float32)
+    k = rng.standard_normal((B, Hkv, S, D), dtype=np.float32)
+    v = rng.standard_normal((B, Hkv, S, D), dtype=np.float32)
+    q[..., 0] = 1.0
+    k[..., 0] = 2.35 * np.arange(S, dtype=np.float32)
+    q, k, v = (on.to_storage(x, dtype) for x in (q, k, v))
+    print(f"[case] growing scores {kernel} causal={causal}", flush=True)
+    o = flash_attention(H.upload(q, dtype), H.upload(k, dtype), H.upload(v, dtype), causal=causal)
+    got = on.from_storage(H.download(o), dtype)
+    exp = oa.attention_bhsd(q, k, v, causal=causal, dtype=dtype)
+    compare(f"growing scores {kernel} causal={causal}", got, exp, TOL[dtype])
+
+
+def test_prefill_w64_and_w32_agree_on_5a_rows(monkeypatch):
+    """Config 5a's prompt through both d_k 128 kernels: the same rows within
+    the bf16 tolerance of each other (and of the oracle, which the full-size
+    5a test checks for the default kernel)."""
+    cfg = oi.CONFIGS["5a"]
+    raw = oi.make_prefill_raw(cfg)
+    outs = {}
+    for kernel in ("w64", "w32"):
+        H.set_override(monkeypatch, "TRITON_LLM_HIP_PREFILL_W64", 1 if kernel == "w64" else None)
+        outs[kernel] = gpu_prefill(cfg, raw)
+    compare("5a w64 vs w32", outs["w64"], outs["w32"], TOL[cfg.dtype])

@@ -151,10 +151,15 @@ int tl_fill_bytes(void* dst, unsigned char value, size_t nbytes, hipStream_t st)
 //                  persistent and equal-share schedules plan for (0: none),
 //                  so small problems take multi-round schedules;
 //   decode_shares  TRITON_LLM_HIP_DECODE_SHARES nonzero: small-cache decode
-//                  takes the equal-share path instead of pair mode.
+//                  takes the equal-share path instead of pair mode;
+//   prefill_w64    TRITON_LLM_HIP_PREFILL_W64 nonzero: 16-bit d_k 128
+//                  prefill runs flash_fwd_w64 (64 query rows per wave)
+//                  instead of flash_fwd_16, so tests and A/B timing can
+//                  run both.
 struct TlOverrides {
   int max_cus;
   int decode_shares;
+  int prefill_w64;
 };
 extern TlOverrides tl_overrides;
 
@@ -241,7 +246,8 @@ __device__ __forceinline__ i32x4 uniform_rsrc(const void* base, uint32_t bytes) 
 // build (triton_llm/_build.py) therefore rejects any kernel that issues
 // these DMAs and in which compiler-generated code reads or writes m0.
 __device__ __forceinline__ void lds_dma16(const i32x4& rsrc, uint32_t voff, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds_addr), "v"(voff), "s"(rsrc)
+  const uint32_t la = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_addr);  // wave-uniform by contract
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(la), "v"(voff), "s"(rsrc)
                : "memory");
 }
 

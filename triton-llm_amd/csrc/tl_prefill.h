@@ -1,0 +1,98 @@
+// Internal header of the prefill kernels (tl_prefill.hip, tl_prefill_w64.hip):
+// the launch parameters, the persistent tile schedule and the LDS swizzles
+// they share.  Not part of the C ABI.
+#pragma once
+
+#include "tl_common.h"
+
+namespace tlp {
+
+struct FlashParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* vt;  // key-major V^T copy (16-bit path), see vt_pack_kernel
+  void* o;
+  int batch, n_head, n_kv, group, seq_q, seq_k, n_qt, sk_pad;
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_sh, o_ss;
+  float scale_log2;
+  // Static tile schedule of the persistent 16-bit kernel (see flash_fwd_16).
+  int n_queues;    // 8 (one tile list per XCD) or 1
+  int q_units;     // (batch, kv head) units per list
+  int q_tiles;     // tiles per list: q_units * n_qt * group
+  int q_machines;  // workgroups per list
+  int q_triple;    // first three rounds use the balanced-triple order
+};
+
+// 16-bit kernels: query rows per tile (both flash_fwd_16 and flash_fwd_w64)
+// and the lazy-rescale threshold of the online softmax.
+constexpr int K16_BM = 256;       // query rows per tile
+constexpr int K16_BN = 128;       // keys per K / V^T tile
+constexpr int K16_THREADS = 512;  // 8 waves
+constexpr float kRescaleLog2 = 8.0f;
+
+// Slot swizzle of LDS rows of D 16-bit elements: 16 consecutive rows read
+// the same 16-byte chunk of their row in one operand load, so the chunk is
+// XORed with bits of the row index that spread those rows over all banks.
+template <int D>
+__device__ __forceinline__ int lds_swz(int r) {
+  if constexpr (D == 128) return 4 * (r & 3) + ((r >> 2) & 3);
+  else return 4 * ((r >> 1) & 1) + ((r >> 2) & 3);
+}
+
+__device__ __forceinline__ float max_xor32(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float sum_xor32(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// The lane index, read afresh at each use (an opaque read that cannot be
+// hoisted), so that lane-derived offsets are recomputed where they are used
+// instead of occupying registers across the tile loop.
+__device__ __forceinline__ int fresh_lane() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
+// Tile i of list `queue` of the persistent schedule: lists hold the (batch,
+// kv head) units' query tiles ordered by qt descending (causal cost), the
+// group's query heads of one qt adjacent.
+__device__ __forceinline__ void decode_tile(const FlashParams& p, int queue, int i, int& b, int& hq, int& qt) {
+  const int per_qt = p.q_units * p.group;  // tiles per qt step in a list
+  const int qt_rev = i / per_qt;
+  const int rem = i - qt_rev * per_qt;
+  const int u = queue * p.q_units + rem / p.group;  // (batch, kv head) unit
+  const int hkv = u % p.n_kv;
+  b = u / p.n_kv;
+  qt = p.n_qt - 1 - qt_rev;
+  hq = hkv * p.group + rem % p.group;
+}
+
+// Rank (position in its list) of workgroup j's r-th tile; >= q_tiles: none.
+__device__ __forceinline__ int sched_rank(const FlashParams& p, int j, int r) {
+  const int m = p.q_machines;
+  if (p.q_triple && r < 3) {
+    const int hm = m / 2;
+    if (r == 0) return j;
+    if (r == 1) return m + (j < hm ? m - 1 - 2 * j : 2 * m - 2 - 2 * j);
+    return 2 * m + (j < hm ? hm + j : j - hm);
+  }
+  const int rr = p.q_triple ? r - 3 : r;
+  return r * m + ((rr & 1) ? m - 1 - j : j);
+}
+
+// d_k 128 16-bit prefill with 64 query rows per wave (tl_prefill_w64.hip);
+// expects p.vt to hold the vt_pack copy of V and the schedule fields set.
+int launch_flash_w64(FlashParams& p, int dtype, bool causal, hipStream_t st);
+
+}  // namespace tlp

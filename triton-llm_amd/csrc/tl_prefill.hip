@@ -31,7 +31,7 @@
 //
 // Kernels: vt_pack_kernel + flash_fwd_16 (f16 / bf16, d_k 64 / 128), flash_fwd_f32
 // (fp32, d_k 64 / 128), attn_generic_kernel (any d_k <= 256).
-#include "tl_common.h"
+#include "tl_prefill.h"
 
 #include <math.h>
 #include <stdlib.h>
@@ -40,29 +40,12 @@
 
 namespace {
 
+using namespace tlp;
+
 constexpr int BM = 128;  // query rows per workgroup
 constexpr int BN = 64;   // keys per tile
 constexpr int kThreads = 256;
 
-struct FlashParams {
-  const void* q;
-  const void* k;
-  const void* v;
-  const void* vt;  // key-major V^T copy (16-bit path), see vt_pack_kernel
-  void* o;
-  int batch, n_head, n_kv, group, seq_q, seq_k, n_qt, sk_pad;
-  int64_t q_sb, q_sh, q_ss;
-  int64_t k_sb, k_sh, k_ss;
-  int64_t v_sb, v_sh, v_ss;
-  int64_t o_sb, o_sh, o_ss;
-  float scale_log2;
-  // Static tile schedule of the persistent 16-bit kernel (see flash_fwd_16).
-  int n_queues;    // 8 (one tile list per XCD) or 1
-  int q_units;     // (batch, kv head) units per list
-  int q_tiles;     // tiles per list: q_units * n_qt * group
-  int q_machines;  // workgroups per list
-  int q_triple;    // first three rounds use the balanced-triple order
-};
 
 
 __device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32); }
@@ -123,32 +106,9 @@ __device__ __forceinline__ void decode_block(const FlashParams& p, int& b, int& 
 // c ^ lds_swz(r) (lds_swz<D> for K and Q rows, lds_swz<128> for the 256-byte
 // V^T rows), which makes every operand read conflict-free.
 // ---------------------------------------------------------------------------
-constexpr int K16_BM = 256;       // query rows per tile
-constexpr int K16_BN = 128;       // keys per K / V^T tile
-constexpr int K16_THREADS = 512;  // 8 waves
-constexpr float kRescaleLog2 = 8.0f;
-
-// Slot swizzle of LDS rows of D 16-bit elements: 16 consecutive rows read
-// the same 16-byte chunk of their row in one operand load, so the chunk is
-// XORed with bits of the row index that spread those rows over all banks.
-template <int D>
-__device__ __forceinline__ int lds_swz(int r) {
-  if constexpr (D == 128) return 4 * (r & 3) + ((r >> 2) & 3);
-  else return 4 * ((r >> 1) & 1) + ((r >> 2) & 3);
-}
 
 
-__device__ __forceinline__ float max_xor32(float x) {
-  const uint32_t u = __float_as_uint(x);
-  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
 
-__device__ __forceinline__ float sum_xor32(float x) {
-  const uint32_t u = __float_as_uint(x);
-  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
 
 
 // ---------------------------------------------------------------------------
@@ -172,38 +132,6 @@ __device__ __forceinline__ float sum_xor32(float x) {
 // reads).  At the switch each wave copies its next Q from LDS, then stages
 // its output in the same buffer; the output stores drain in the background.
 // ---------------------------------------------------------------------------
-// The lane index, read afresh at each use (an opaque read that cannot be
-// hoisted), so that lane-derived offsets are recomputed where they are used
-// instead of occupying registers across the tile loop.
-__device__ __forceinline__ int fresh_lane() {
-  int l;
-  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
-  return l;
-}
-
-__device__ __forceinline__ void decode_tile(const FlashParams& p, int queue, int i, int& b, int& hq, int& qt) {
-  const int per_qt = p.q_units * p.group;  // tiles per qt step in a list
-  const int qt_rev = i / per_qt;
-  const int rem = i - qt_rev * per_qt;
-  const int u = queue * p.q_units + rem / p.group;  // (batch, kv head) unit
-  const int hkv = u % p.n_kv;
-  b = u / p.n_kv;
-  qt = p.n_qt - 1 - qt_rev;
-  hq = hkv * p.group + rem % p.group;
-}
-
-// Rank (position in its list) of workgroup j's r-th tile; >= q_tiles: none.
-__device__ __forceinline__ int sched_rank(const FlashParams& p, int j, int r) {
-  const int m = p.q_machines;
-  if (p.q_triple && r < 3) {
-    const int hm = m / 2;
-    if (r == 0) return j;
-    if (r == 1) return m + (j < hm ? m - 1 - 2 * j : 2 * m - 2 - 2 * j);
-    return 2 * m + (j < hm ? hm + j : j - hm);
-  }
-  const int rr = p.q_triple ? r - 3 : r;
-  return r * m + ((rr & 1) ? m - 1 - j : j);
-}
 
 // SCALE_S: Q is used as stored and each score is scaled in fp32 in the
 // softmax (one FMA per score: s * scale_log2 - m_run) instead of Q being
@@ -1235,10 +1163,12 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(FlashParams p, int D, 
 
 inline bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
-// Bytes of the key-major V^T copy: keys padded to a multiple of 128.
+// Keys per V^T row: seq_k rounded up to a multiple of 128.
+inline int64_t vt_row_keys(int64_t seq_k) { return (seq_k + 127) / 128 * 128; }
+
+// Bytes of the key-major V^T copy.
 size_t vt_bytes(int batch, int n_kv, int seq_k, int d_k) {
-  const size_t sk_pad = (size_t)((seq_k + 127) / 128) * 128;
-  return (size_t)batch * n_kv * d_k * sk_pad * 2;
+  return (size_t)batch * n_kv * d_k * (size_t)vt_row_keys(seq_k) * 2;
 }
 
 template <typename T, int D>
@@ -1262,6 +1192,14 @@ int launch_flash_16(FlashParams& p, void* ws, bool causal, hipStream_t st) {
                        p.seq_k, p.sk_pad, p.n_kv, vt_tiles, p.v_sb, p.v_sh, p.v_ss);
     const int e = tl_launch_status();
     if (e) return e;
+  }
+  // d_k 128 with 64 query rows per wave (tl_prefill_w64.hip): on request
+  // only (TRITON_LLM_HIP_PREFILL_W64); it measures about 8% slower than this
+  // kernel on config 5a.  Not when the scores must be scaled in fp32 (fp16,
+  // large scale); it addresses a wave's 64 output rows with 32-bit offsets.
+  if constexpr (D == 128) {
+    const bool w64_ok = (64 * p.o_ss + D) * 2 < ((int64_t)1 << 32);
+    if (!scale_s && tl_overrides.prefill_w64 && w64_ok) return launch_flash_w64(p, T::code, causal, st);
   }
   dim3 grid((unsigned)(p.q_machines * p.n_queues));
   if constexpr (std::is_same<T, F16>::value) {
@@ -1320,7 +1258,7 @@ bool mfma_shape_ok(const FlashParams& p, int d_k, int dtype) {
     // output rows and a head's V^T copy with 32-bit byte offsets, and bounds
     // a K or Q tile's reads and an output block's stores by its row count
     // times the row stride (rows must not overlap).
-    const int64_t sk_pad = (p.seq_k + 127) / 128 * 128;
+    const int64_t sk_pad = vt_row_keys(p.seq_k);
     if (p.k_ss < d_k || (128 * p.k_ss + d_k) * 2 >= ((int64_t)1 << 32) || p.q_ss < d_k ||
         p.o_ss < d_k || (32 * p.o_ss + d_k) * 2 >= ((int64_t)1 << 32) ||
         (128 * p.q_ss + d_k) * 2 >= ((int64_t)1 << 32) || (int64_t)d_k * sk_pad * 2 >= ((int64_t)1 << 32))
@@ -1368,7 +1306,7 @@ int tl_attention_fwd(const void* q, const void* k, const void* v, void* o, void*
   p.seq_q = seq_q;
   p.seq_k = seq_k;
   p.n_qt = (seq_q + BM - 1) / BM;
-  p.sk_pad = (seq_k + 127) / 128 * 128;
+  p.sk_pad = (int)vt_row_keys(seq_k);
   p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.q_ss = q_strides[2];
   p.k_sb = k_strides[0]; p.k_sh = k_strides[1]; p.k_ss = k_strides[2];
   p.v_sb = v_strides[0]; p.v_sh = v_strides[1]; p.v_ss = v_strides[2];

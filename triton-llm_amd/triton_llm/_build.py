@@ -41,6 +41,14 @@ HIPCC_FLAGS = [
 ]
 
 
+# Extra flags per source.  tl_prefill_w64.hip builds its MFMA builtins in VGPR
+# form: its S products are read by VALU code, while its O accumulators live in
+# AGPRs through inline assembly (at one wave per SIMD the compiler would
+# otherwise give every MFMA AGPR operands and copy S out for the softmax).
+FILE_FLAGS: dict[str, list[str]] = {
+    "tl_prefill_w64.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
 # Only the HIP runtime is linked (hipcc adds it); every kernel is this library's own.
 LINK_LIBS: list[str] = []
 
@@ -102,7 +110,8 @@ def check_m0(asm_text: str, source: str) -> int:
 def _compile_one(src: str, obj: str) -> None:
     # -save-temps=obj leaves the device assembly next to the object (in the
     # build's temporary directory) for check_m0.
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-save-temps=obj", "-c", src, "-o", obj]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-save-temps=obj", "-c", src,
+           "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True, cwd=os.path.dirname(obj))
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
