@@ -693,7 +693,7 @@ int decode_entry(const void* q, const void* k_cache, const void* v_cache,
                  size_t workspace_bytes, int batch, int n_head, int n_kv_head, int max_ctx,
                  int d_k, const int64_t* q_strides, const int64_t* k_strides,
                  const int64_t* v_strides, const int64_t* o_strides, float sm_scale,
-                 int split_size, int dtype, void* stream);
+                 int split_size, int dtype, void* stream, bool check_only = false);
 
 }  // namespace
 
@@ -790,8 +790,16 @@ int tl_attention_decode_noalloc(const void* q, const void* k_cache, const void* 
   if (tl_attention_decode_workspace_bytes(batch, n_head, max_ctx, d_k, split_size) >
       (size_t)TL_DECODE_NOALLOC_SCRATCH_BYTES)
     return TL_ERR_INVALID;
+  // every other argument check first, against a stand-in workspace address
+  // (only its null-ness and alignment are checked), so an invalid call
+  // returns before any HIP call
+  int st = decode_entry(q, k_cache, v_cache, cache_lens, len_add, o, (void*)(uintptr_t)256,
+                        (size_t)TL_DECODE_NOALLOC_SCRATCH_BYTES, batch, n_head, n_kv_head, max_ctx, d_k,
+                        q_strides, k_strides, v_strides, o_strides, sm_scale, split_size, dtype, stream,
+                        /*check_only=*/true);
+  if (st != 0) return st;
   void* ws = nullptr;
-  const int st = noalloc_scratch(&ws);
+  st = noalloc_scratch(&ws);
   if (st != 0) return st;
   return decode_entry(q, k_cache, v_cache, cache_lens, len_add, o, ws,
                       (size_t)TL_DECODE_NOALLOC_SCRATCH_BYTES, batch, n_head, n_kv_head, max_ctx,
@@ -808,7 +816,7 @@ int decode_entry(const void* q, const void* k_cache, const void* v_cache,
                  size_t workspace_bytes, int batch, int n_head, int n_kv_head, int max_ctx,
                  int d_k, const int64_t* q_strides, const int64_t* k_strides,
                  const int64_t* v_strides, const int64_t* o_strides, float sm_scale,
-                 int split_size, int dtype, void* stream) {
+                 int split_size, int dtype, void* stream, bool check_only) {
   if (batch == 0 || n_head == 0) return 0;
   if (!q || !k_cache || !v_cache || !o || !workspace || batch < 0 ||
       n_head < 0 || n_kv_head < 1 || n_head % n_kv_head != 0 || max_ctx < 1 ||
@@ -872,6 +880,7 @@ int decode_entry(const void* q, const void* k_cache, const void* v_cache,
   p.v_row_bytes = (uint32_t)(v_strides[2] * esize);
   p.k_region_bytes = (uint32_t)k_region;
   p.v_region_bytes = (uint32_t)v_region;
+  if (check_only) return 0;  // every argument check passed; nothing launched
   hipStream_t st = tl_resolve_stream(stream);
   switch (dtype) {
     case TL_DTYPE_F32: return launch_decode_t<F32>(p, d_k, st);

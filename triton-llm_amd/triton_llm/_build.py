@@ -157,5 +157,50 @@ def build(verbose: bool = True, jobs: int | None = None) -> str:
     return LIB_PATH
 
 
+def build_host_asan(out_dir: str, jobs: int | None = None) -> str:
+    """A CPU-only AddressSanitizer build of the library's host code, for
+    tests that drive the entry points' argument checks and workspace sizing
+    (which return before any HIP call).  Host-only compile (no device code:
+    the device binary embedded is empty, so no kernel can be launched from
+    this build); the sanitizer applies to the host pass only.  Returns the
+    library path.  Needs the ASan runtime preloaded into the process that
+    loads it (see asan_runtime())."""
+    os.makedirs(out_dir, exist_ok=True)
+    empty_fb = os.path.join(out_dir, "empty.hipfb")
+    open(empty_fb, "wb").close()
+    host_flags = ["--offload-host-only", "-O1", "-g", "-std=c++17", "-fPIC",
+                  "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer",
+                  "-Xclang", "-fcuda-include-gpubinary", "-Xclang", empty_fb]
+    srcs = sources()
+    objs = [os.path.join(out_dir, os.path.basename(s) + ".o") for s in srcs]
+
+    def one(src, obj):
+        res = subprocess.run([_hipcc(), *host_flags, "-c", src, "-o", obj], capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"host ASan compile failed for {os.path.basename(src)}:\n{res.stderr}")
+
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs or min(len(srcs), 8)) as ex:
+        for f in [ex.submit(one, s, o) for s, o in zip(srcs, objs)]:
+            f.result()
+    lib = os.path.join(out_dir, "libtriton_llm_hip_asan.so")
+    res = subprocess.run([_hipcc(), "--offload-host-only", "-shared", "-fPIC", "-Xarch_host", "-fsanitize=address",
+                          *objs, "-o", lib, *LINK_LIBS], capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"host ASan link failed:\n{res.stderr}")
+    return lib
+
+
+def asan_runtime() -> str | None:
+    """Path of the compiler's shared ASan runtime, or None."""
+    clang = os.path.join(os.path.dirname(os.path.realpath(_hipcc())), "..", "llvm", "bin", "clang")
+    for c in (clang, "/opt/rocm/llvm/bin/clang"):
+        if os.path.exists(c):
+            res = subprocess.run([c, "-print-file-name=libclang_rt.asan-x86_64.so"], capture_output=True, text=True)
+            path = res.stdout.strip()
+            if res.returncode == 0 and os.path.isabs(path) and os.path.exists(path):
+                return path
+    return None
+
+
 if __name__ == "__main__":
     build()
