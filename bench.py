@@ -176,7 +176,7 @@ def bench_decode(cfg, steps, warmup, replicas=1, cpu=True, split=0, cpu_budget_s
     from oracle import inputs as oi
     from oracle import numerics as on
     from triton_llm import gpu
-    from triton_llm.kernels import attention_decode, rope_kv_append
+    from triton_llm.kernels import attention_decode, decode_step
     from triton_llm.kernels.decode import decode_workspace, decode_workspace_bytes
 
     dt = cfg.dtype
@@ -207,9 +207,10 @@ def bench_decode(cfg, steps, warmup, replicas=1, cpu=True, split=0, cpu_budget_s
                          workspace=ws, split=split)
 
     def step(i):
+        # RoPE + append + attention: one tl_attention_decode_append call
         kc, vc = caches[i % replicas]
-        rope_kv_append(q, kn, vn, kc, vc, lens_d, cos_d, sin_d)
-        attend(i)
+        decode_step(q, kn, vn, kc, vc, lens_d, Hq, Hkv, cos_d, sin_d, sm_scale=cfg.scale, out=out,
+                    workspace=ws, split=split)
 
     # One eager step per replica fills the workspace and block caches.  Each
     # replica's step (RoPE + append + attention) and its attention call alone

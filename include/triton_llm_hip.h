@@ -172,6 +172,32 @@ int tl_attention_decode(const void* q, const void* k_cache, const void* v_cache,
                         float sm_scale, int split_size, int dtype,
                         void* stream);
 
+/* One decode step's token and attention in one call:
+ *   tl_rope_kv_append(q, k_new, v_new, ..., n_new = 1)  then
+ *   tl_attention_decode(q, k_cache, v_cache, cache_lens, len_add = 1, ...)
+ * with the same results (rotated q in place, cache row cache_lens[b]
+ * written bit for bit as tl_rope_kv_append writes it, the same output).
+ * No reference counterpart as one function: it fuses the model's decode
+ * sequence (smollm2_triton/model.py:296-314; gpt2_triton/model.py:332-349
+ * without RoPE).  In the small-cache mode the workgroup of each (sequence,
+ * KV head) rotates and writes its token before streaming the cache, so the
+ * step is one launch; otherwise the append is its own launch first.
+ * q: (batch, n_head, d_k) {batch, head} strides, rotated in place;
+ * k_new / v_new: (batch, n_kv_head, d_k) {batch, head} strides, read only;
+ * caches, o, workspace, split_size and the support rules as for
+ * tl_attention_decode; cos/sin (rope_rows rows of d_k / 2) as for
+ * tl_rope_kv_append (NULL: no RoPE).  cache_lens must not be NULL. */
+int tl_attention_decode_append(void* q, const void* k_new, const void* v_new,
+                               void* k_cache, void* v_cache, const int32_t* cache_lens,
+                               const float* cos_table, const float* sin_table,
+                               int rope_rows, void* o, void* workspace,
+                               size_t workspace_bytes, int batch, int n_head,
+                               int n_kv_head, int max_ctx, int d_k,
+                               const int64_t* q_strides, const int64_t* k_new_strides,
+                               const int64_t* v_new_strides, const int64_t* k_strides,
+                               const int64_t* v_strides, const int64_t* o_strides,
+                               float sm_scale, int split_size, int dtype, void* stream);
+
 /* The same decode with no workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference.  The

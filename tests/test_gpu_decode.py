@@ -12,7 +12,7 @@ from oracle import numerics as on
 from oracle import rope as orope
 from tests import _helpers as H
 from triton_llm import gpu
-from triton_llm.kernels import attention_decode, decode_step, precompute_cos_sin
+from triton_llm.kernels import attention_decode, decode_step, precompute_cos_sin, rope_kv_append
 
 pytestmark = pytest.mark.gpu
 
@@ -61,6 +61,8 @@ def run_decode_step(cfg, data, batches=None, split=0):
             kc[b, :, p] = data["k_new"][b]
         vc[b, :, p] = data["v_new"][b]
     exp = oa.decode_ref(q, kc, vc, lens + 1, sm_scale=cfg.scale, dtype=dt, batches=batches)
+    # q is rotated in place, bit for bit as the oracle rotates it
+    np.testing.assert_array_equal(H.download(q_d).view(np.uint8), q.view(np.uint8))
     return got, exp, kc_d, vc_d
 
 
@@ -201,3 +203,42 @@ def test_decode_all_sequences_empty_over_64(monkeypatch, mode):
                            gpu.to_device(lens), 6, 2, sm_scale=0.125, len_add=0)
     got = on.from_storage(H.download(out), dt)
     assert np.all(got == 0)
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("dtype,group,d_k,rope", [("float16", 1, 64, False), ("bfloat16", 3, 64, True),
+                                                  ("bfloat16", 12, 128, True), ("float32", 2, 128, True)])
+def test_decode_step_fused_equals_append_then_decode(monkeypatch, mode, dtype, group, d_k, rope):
+    """decode_step (one tl_attention_decode_append call: in the small-cache
+    mode the append runs inside the decode kernel) against rope_kv_append
+    followed by attention_decode on copies of the same inputs: q, both
+    caches and the output agree bit for bit.  Lengths include 0, max_ctx - 1
+    (the token fills the cache), max_ctx (no room: nothing is written) and,
+    with RoPE, positions past the table (not rotated, not written)."""
+    set_mode(monkeypatch, mode)
+    Hkv, max_ctx = 2, 300
+    cfg = oi.Config("decode-fused", "decode", dtype, 7, Hkv * group, Hkv, d_k, 23, 0.2,
+                    max_ctx=max_ctx, lo=0, hi=max_ctx - 1, rope_theta=1e4 if rope else None)
+    lens = oi.draw_lens(cfg)
+    lens[:4] = [0, max_ctx - 1, max_ctx, 250]
+    data = oi.make_decode(cfg, fill="nan", lens=lens)
+    cos, sin = oi.rope_tables(cfg)
+    cos_d = sin_d = None
+    if rope:
+        rows = 200  # sequences at positions >= 200 are past the table
+        cos_d, sin_d = gpu.to_device(np.ascontiguousarray(cos[:rows])), gpu.to_device(np.ascontiguousarray(sin[:rows]))
+    lens_d = gpu.to_device(lens)
+    outs = {}
+    for path in ("fused", "separate"):
+        q_d = H.upload(data["q"], dtype)
+        kn_d, vn_d = H.upload(data["k_new"], dtype), H.upload(data["v_new"], dtype)
+        kc_d, vc_d = H.upload(data["k_cache"], dtype), H.upload(data["v_cache"], dtype)
+        print(f"[case] decode fused-vs-separate {mode} {dtype} g{group} d{d_k} rope={rope} {path}", flush=True)
+        if path == "fused":
+            o = decode_step(q_d, kn_d, vn_d, kc_d, vc_d, lens_d, cfg.n_head, Hkv, cos_d, sin_d, sm_scale=cfg.scale)
+        else:
+            rope_kv_append(q_d, kn_d, vn_d, kc_d, vc_d, lens_d, cos_d, sin_d)
+            o = attention_decode(q_d, kc_d, vc_d, lens_d, cfg.n_head, Hkv, sm_scale=cfg.scale, len_add=1)
+        outs[path] = [H.download(x).view(np.uint8) for x in (o, q_d, kc_d, vc_d)]
+    for name, a, b in zip(("out", "q", "k_cache", "v_cache"), outs["fused"], outs["separate"]):
+        np.testing.assert_array_equal(a, b, err_msg=name)

@@ -88,6 +88,16 @@ __device__ __forceinline__ uint16_t from_f32<F16>(float f) { return (uint16_t)f3
 template <>
 __device__ __forceinline__ uint16_t from_f32<BF16>(float f) { return (uint16_t)f32_to_bf16_bits_rne(f); }
 
+// RoPE of one half-split pair (x_i, x_{i+d/2}) at one position: each product
+// and the sum / difference rounded separately in fp32, as NumPy evaluates
+// the same expression (hipcc would otherwise contract a*b - c*d into an FMA).
+__device__ __forceinline__ void rope_rotate_pair(float xe, float xo, float c, float s, float& oe, float& oo) {
+#pragma clang fp contract(off)
+  const float a = xe * c, b = xo * s, d = xe * s, e = xo * c;
+  oe = a - b;
+  oo = d + e;
+}
+
 // Unpack a 32-bit word holding two 16-bit values (low half first).
 template <typename T>
 __device__ __forceinline__ void unpack2(uint32_t w, float& lo, float& hi);

@@ -160,6 +160,18 @@ struct DecodeParams {
   uint32_t k_region_bytes, v_region_bytes;  // bytes addressable from one (b, head) base
   int64_t o_sb, o_sh;
   float scale_log2;  // sm_scale * log2(e)
+  // Fused RoPE + KV append (tl_attention_decode_append, small-cache mode
+  // only): before streaming, the workgroup of each (sequence, pair) rotates
+  // its query heads in place and writes the new token's rotated k and its v
+  // to cache row lens[b] (every chunk of a KV head writes the same bytes).
+  int append;
+  const void* kn;
+  const void* vn;
+  const float* cos_t;  // NULL: no rotation
+  const float* sin_t;
+  int rope_rows;
+  int64_t kn_sb, kn_sh, vn_sb, vn_sh;
+  int64_t k_ss, v_ss;  // cache seq strides in elements
 };
 
 __device__ __forceinline__ int ctx_len(const DecodeParams& p, int b) {
@@ -290,6 +302,58 @@ __device__ __forceinline__ void set_progress_priority(int64_t done, int64_t shar
   else if (q == 1) __builtin_amdgcn_s_setprio(2);
   else if (q == 2) __builtin_amdgcn_s_setprio(1);
   else __builtin_amdgcn_s_setprio(0);
+}
+
+// The fused append of tl_attention_decode_append for the pair of one
+// workgroup: the same arithmetic and rounding as rope_kv_append_kernel
+// (tl_rope.hip), so the cache bytes and rotated q are identical to a
+// tl_rope_kv_append call followed by tl_attention_decode.
+template <typename T, int D>
+__device__ void append_token(const DecodeParams& p, int b, int pair) {
+  using B = typename T::bits;
+  constexpr int H = D / 2;
+  const int n_chunks = p.n_pairs / p.n_kv;
+  const int hkv = pair / n_chunks;
+  const int hq0 = hkv * p.group + (pair - hkv * n_chunks) * p.heads_per_pair;
+  const int n_g = min(p.heads_per_pair, hkv * p.group + p.group - hq0);
+  const int pos = p.lens[b];
+  const bool rope = p.cos_t != nullptr;
+  if (pos < 0 || pos >= p.max_ctx || (rope && pos >= p.rope_rows)) return;
+  // jobs: n_g query rows (RoPE only), then the k row, then the v row; job j
+  // is element pair (i, i + D/2) of row j / H
+  for (int j = threadIdx.x; j < (n_g + 2) * H; j += blockDim.x) {
+    const int r = j / H, i = j - r * H;
+    float c = 1.f, sn = 0.f;
+    if (rope) {
+      c = p.cos_t[(int64_t)pos * H + i];
+      sn = p.sin_t[(int64_t)pos * H + i];
+    }
+    if (r < n_g) {
+      if (!rope) continue;
+      B* qr = (B*)p.q + b * p.q_sb + (int64_t)(hq0 + r) * p.q_sh;
+      float oe, oo;
+      rope_rotate_pair(to_f32<T>(qr[i]), to_f32<T>(qr[i + H]), c, sn, oe, oo);
+      qr[i] = from_f32<T>(oe);
+      qr[i + H] = from_f32<T>(oo);
+    } else if (r == n_g) {
+      const B* kr = (const B*)p.kn + b * p.kn_sb + hkv * p.kn_sh;
+      B* dst = (B*)p.k + b * p.k_sb + hkv * p.k_sh + (int64_t)pos * p.k_ss;
+      if (rope) {
+        float oe, oo;
+        rope_rotate_pair(to_f32<T>(kr[i]), to_f32<T>(kr[i + H]), c, sn, oe, oo);
+        dst[i] = from_f32<T>(oe);
+        dst[i + H] = from_f32<T>(oo);
+      } else {
+        dst[i] = kr[i];
+        dst[i + H] = kr[i + H];
+      }
+    } else {
+      const B* vr = (const B*)p.vn + b * p.vn_sb + hkv * p.vn_sh;
+      B* dst = (B*)p.v + b * p.v_sb + hkv * p.v_sh + (int64_t)pos * p.v_ss;
+      dst[i] = vr[i];
+      dst[i + H] = vr[i + H];
+    }
+  }
 }
 
 // G: query heads of one (kv head, chunk) pair (<= group).  NW: waves per
@@ -502,6 +566,13 @@ __global__ __launch_bounds__(64 * NW) void decode_split_kernel(DecodeParams p) {
   if constexpr (PAIR) {
     const int b = (int)blockIdx.x / p.n_pairs;
     const int pair = (int)blockIdx.x - b * p.n_pairs;
+    if (p.append) {
+      // the new token first: rotated q rows and cache row lens[b], visible
+      // to every thread of the workgroup before any of them reads them
+      append_token<T, D>(p, b, pair);
+      __threadfence_block();
+      __syncthreads();
+    }
     const int ctx = uniform(ctx_len(p, b));
     segment(b, ctx, pair, 0, ctx, true, 0, 0, 0);
   } else {
@@ -688,12 +759,25 @@ int launch_decode_t(DecodeParams& p, int d_k, hipStream_t st) {
 
 size_t round256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// The new token of tl_attention_decode_append.
+struct AppendArgs {
+  const void* k_new;
+  const void* v_new;
+  const float* cos_t;
+  const float* sin_t;
+  int rope_rows;
+  const int64_t* k_new_strides;
+  const int64_t* v_new_strides;
+};
+
 int decode_entry(const void* q, const void* k_cache, const void* v_cache,
                  const int32_t* cache_lens, int len_add, void* o, void* workspace,
                  size_t workspace_bytes, int batch, int n_head, int n_kv_head, int max_ctx,
                  int d_k, const int64_t* q_strides, const int64_t* k_strides,
                  const int64_t* v_strides, const int64_t* o_strides, float sm_scale,
-                 int split_size, int dtype, void* stream, bool check_only = false);
+                 int split_size, int dtype, void* stream, bool check_only = false,
+                 const AppendArgs* ap = nullptr);
+
 
 }  // namespace
 
@@ -775,6 +859,24 @@ int tl_attention_decode(const void* q, const void* k_cache, const void* v_cache,
                       o_strides, sm_scale, split_size, dtype, stream);
 }
 
+int tl_attention_decode_append(void* q, const void* k_new, const void* v_new, void* k_cache,
+                               void* v_cache, const int32_t* cache_lens, const float* cos_table,
+                               const float* sin_table, int rope_rows, void* o, void* workspace,
+                               size_t workspace_bytes, int batch, int n_head, int n_kv_head, int max_ctx,
+                               int d_k, const int64_t* q_strides, const int64_t* k_new_strides,
+                               const int64_t* v_new_strides, const int64_t* k_strides,
+                               const int64_t* v_strides, const int64_t* o_strides, float sm_scale,
+                               int split_size, int dtype, void* stream) {
+  if (batch == 0 || n_head == 0) return 0;
+  if (!k_new || !v_new || !cache_lens || !k_new_strides || !v_new_strides) return TL_ERR_INVALID;
+  if ((cos_table == nullptr) != (sin_table == nullptr)) return TL_ERR_INVALID;
+  if (cos_table && rope_rows < 0) return TL_ERR_INVALID;
+  const AppendArgs ap{k_new, v_new, cos_table, sin_table, rope_rows, k_new_strides, v_new_strides};
+  return decode_entry(q, k_cache, v_cache, cache_lens, 1, o, workspace, workspace_bytes, batch, n_head, n_kv_head,
+                      max_ctx, d_k, q_strides, k_strides, v_strides, o_strides, sm_scale, split_size, dtype, stream,
+                      false, &ap);
+}
+
 int tl_attention_decode_noalloc(const void* q, const void* k_cache, const void* v_cache,
                                 const int32_t* cache_lens, int len_add, void* o, int batch,
                                 int n_head, int n_kv_head, int max_ctx, int d_k,
@@ -816,7 +918,7 @@ int decode_entry(const void* q, const void* k_cache, const void* v_cache,
                  size_t workspace_bytes, int batch, int n_head, int n_kv_head, int max_ctx,
                  int d_k, const int64_t* q_strides, const int64_t* k_strides,
                  const int64_t* v_strides, const int64_t* o_strides, float sm_scale,
-                 int split_size, int dtype, void* stream, bool check_only) {
+                 int split_size, int dtype, void* stream, bool check_only, const AppendArgs* ap) {
   if (batch == 0 || n_head == 0) return 0;
   if (!q || !k_cache || !v_cache || !o || !workspace || batch < 0 ||
       n_head < 0 || n_kv_head < 1 || n_head % n_kv_head != 0 || max_ctx < 1 ||
@@ -881,6 +983,33 @@ int decode_entry(const void* q, const void* k_cache, const void* v_cache,
   p.k_region_bytes = (uint32_t)k_region;
   p.v_region_bytes = (uint32_t)v_region;
   if (check_only) return 0;  // every argument check passed; nothing launched
+  if (ap) {
+    if (pair_mode(p, d_k, esize)) {
+      // small caches: each workgroup appends its pair's token itself
+      p.append = 1;
+      p.kn = ap->k_new;
+      p.vn = ap->v_new;
+      p.cos_t = ap->cos_t;
+      p.sin_t = ap->sin_t;
+      p.rope_rows = ap->rope_rows;
+      p.kn_sb = ap->k_new_strides[0];
+      p.kn_sh = ap->k_new_strides[1];
+      p.vn_sb = ap->v_new_strides[0];
+      p.vn_sh = ap->v_new_strides[1];
+      p.k_ss = k_strides[2];
+      p.v_ss = v_strides[2];
+    } else {
+      // shared positions: the token goes in first, by its own launch
+      const int64_t qs[3] = {q_strides[0], 0, q_strides[1]};
+      const int64_t ks[3] = {ap->k_new_strides[0], 0, ap->k_new_strides[1]};
+      const int64_t vs[3] = {ap->v_new_strides[0], 0, ap->v_new_strides[1]};
+      const int st = tl_rope_kv_append(const_cast<void*>(q), ap->k_new, ap->v_new, const_cast<void*>(k_cache),
+                                       const_cast<void*>(v_cache), cache_lens, ap->cos_t, ap->sin_t, ap->rope_rows,
+                                       batch, 1, n_head, n_kv_head, max_ctx, d_k, qs, ks, vs, k_strides, v_strides,
+                                       dtype, stream);
+      if (st != 0) return st;
+    }
+  }
   hipStream_t st = tl_resolve_stream(stream);
   switch (dtype) {
     case TL_DTYPE_F32: return launch_decode_t<F32>(p, d_k, st);

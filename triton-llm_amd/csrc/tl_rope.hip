@@ -16,10 +16,7 @@ namespace {
 
 __device__ __forceinline__ void rotate_pair(float xe, float xo, float c, float s,
                                             float& oe, float& oo) {
-#pragma clang fp contract(off)
-  const float a = xe * c, b = xo * s, d = xe * s, e = xo * c;
-  oe = a - b;
-  oo = d + e;
+  rope_rotate_pair(xe, xo, c, s, oe, oo);
 }
 
 // VEC consecutive table entries (fp32) from row offset `at`: 16-byte loads.

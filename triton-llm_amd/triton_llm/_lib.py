@@ -68,6 +68,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _i64p, _i64p, _i64p, _i64p,
          _c_float, _c_int, _c_int, _vp],
     ),
+    "tl_attention_decode_append": (
+        _c_int,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _c_size,
+         _c_int, _c_int, _c_int, _c_int, _c_int,
+         _i64p, _i64p, _i64p, _i64p, _i64p, _i64p,
+         _c_float, _c_int, _c_int, _vp],
+    ),
     "tl_attention_decode_noalloc": (
         _c_int,
         [_vp, _vp, _vp, _vp, _c_int, _vp,

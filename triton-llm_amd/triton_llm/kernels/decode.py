@@ -166,8 +166,52 @@ def attention_decode(q_dev, k_cache, v_cache, cache_lens, n_head: int, n_kv_head
 def decode_step(q_dev, k_new, v_new, k_cache, v_cache, cache_lens, n_head: int, n_kv_head: int,
                 cos_dev=None, sin_dev=None, sm_scale: float | None = None, out=None,
                 workspace=None, split: int = 0):
-    """RoPE + append of the new token, then attention over ``cache_lens[b] + 1`` positions."""
-    rope_kv_append(q_dev, k_new, v_new, k_cache, v_cache, cache_lens, cos_dev, sin_dev)
-    return attention_decode(q_dev, k_cache, v_cache, cache_lens, n_head, n_kv_head,
-                            sm_scale=sm_scale, len_add=1, out=out, workspace=workspace,
-                            split=split)
+    """RoPE + append of the new token, then attention over ``cache_lens[b] + 1`` positions.
+
+    The same results as ``rope_kv_append`` followed by ``attention_decode``
+    with ``len_add=1`` (q rotated in place, cache row ``cache_lens[b]``
+    written, the output returned), in one library call
+    (``tl_attention_decode_append``): with a small cache the workgroups that
+    stream each (sequence, KV head) write its token first, so the step is a
+    single launch.  q_dev: ``(batch, n_head, d_k)``; k_new / v_new:
+    ``(batch, n_kv_head, d_k)``.
+    """
+    batch, n_kv, max_ctx, d_k = _check_cache(k_cache, v_cache)
+    if n_kv != n_kv_head:
+        raise ValueError(f"cache has {n_kv} KV heads, n_kv_head={n_kv_head}")
+    if n_head <= 0 or n_head % n_kv_head:
+        raise ValueError(f"n_head ({n_head}) must be a positive multiple of n_kv_head ({n_kv_head})")
+    if int(np.prod(q_dev.shape)) != batch * n_head * d_k or q_dev.shape[0] != batch or q_dev.shape[-1] != d_k:
+        raise ValueError(f"q shape {q_dev.shape} is not (batch={batch}, n_head={n_head}, d_k={d_k})")
+    for name, t in (("k_new", k_new), ("v_new", v_new)):
+        if int(np.prod(t.shape)) != batch * n_kv * d_k or t.shape[0] != batch or t.shape[-1] != d_k:
+            raise ValueError(f"{name} shape {t.shape} is not (batch={batch}, n_kv_head={n_kv}, d_k={d_k})")
+    if d_k not in (64, 128):
+        raise ValueError(f"decode supports d_k in (64, 128), got {d_k}")
+    _check_lens(cache_lens, batch)
+    code = same_dtype(q_dev, k_new, v_new, k_cache, v_cache)
+    rope_rows = 0
+    if (cos_dev is None) != (sin_dev is None):
+        raise ValueError("cos_dev and sin_dev must both be given or both be None")
+    if cos_dev is not None:
+        if cos_dev.shape != sin_dev.shape or len(cos_dev.shape) != 2 or cos_dev.shape[1] != d_k // 2:
+            raise ValueError(f"cos/sin tables must be (rows, {d_k // 2}), got {cos_dev.shape}")
+        rope_rows = cos_dev.shape[0]
+    if sm_scale is None:
+        sm_scale = default_scale(d_k)
+    if out is None:
+        out = gpu.allocate((batch, n_head, d_k), q_dev.dtype)
+    elif int(np.prod(out.shape)) != batch * n_head * d_k or gpu.dtype_name(out.dtype) != gpu.dtype_name(q_dev.dtype):
+        raise ValueError(f"out must hold (batch, n_head, d_k) of the input dtype, got {out.shape}")
+    ws_bytes, split = decode_workspace_bytes(batch, n_head, n_kv_head, max_ctx, d_k, split)
+    ws = scratch(ws_bytes, workspace, key="decode")
+    qo = _lib.strides(n_head * d_k, d_k)
+    kv = _lib.strides(n_kv * d_k, d_k)
+    c_str = _lib.strides(n_kv * max_ctx * d_k, max_ctx * d_k, d_k)
+    launch(gpu.runtime().tl_attention_decode_append, vp(q_dev), vp(k_new), vp(v_new), vp(k_cache), vp(v_cache),
+           vp(cache_lens), vp(cos_dev), vp(sin_dev), rope_rows, vp(out), vp(ws),
+           ws.nbytes if ws is not None else 0,
+           batch, n_head, n_kv_head, max_ctx, d_k, qo, kv, kv, c_str, c_str, qo,
+           float(sm_scale), split, code, None,
+           what="decode_step")
+    return out
