@@ -93,6 +93,22 @@ rec("dec noalloc too big", lib.tl_attention_decode_noalloc(fake, fake, fake, Non
                                                            128, s3(64 * 128, 128, 1), s3(8 << 27, 1 << 27, 128),
                                                            s3(8 << 27, 1 << 27, 128), s3(64 * 128, 128, 1), 0.125,
                                                            256, BF16, None))
+kvn = s3(2 * 64, 64, 1)
+rec("dec_append null k_new", lib.tl_attention_decode_append(fake, null, fake, fake, fake, fake, None, None, 0, fake,
+                                                            fake, 1 << 30, 2, 3, 1, 64, 64, q_st, kvn, kvn, kv, kv,
+                                                            q_st, 0.125, 16, BF16, None))
+rec("dec_append null lens", lib.tl_attention_decode_append(fake, fake, fake, fake, fake, null, None, None, 0, fake,
+                                                           fake, 1 << 30, 2, 3, 1, 64, 64, q_st, kvn, kvn, kv, kv,
+                                                           q_st, 0.125, 16, BF16, None))
+rec("dec_append cos only", lib.tl_attention_decode_append(fake, fake, fake, fake, fake, fake, fake, None, 8, fake,
+                                                          fake, 1 << 30, 2, 3, 1, 64, 64, q_st, kvn, kvn, kv, kv,
+                                                          q_st, 0.125, 16, BF16, None))
+rec("dec_append group", lib.tl_attention_decode_append(fake, fake, fake, fake, fake, fake, None, None, 0, fake,
+                                                       fake, 1 << 30, 2, 3, 2, 64, 64, q_st, kvn, kvn, kv, kv,
+                                                       q_st, 0.125, 16, BF16, None))
+rec("dec_append empty", lib.tl_attention_decode_append(null, null, null, null, null, null, None, None, 0, null,
+                                                       null, 0, 0, 3, 1, 64, 64, z, z, z, z, z, z, 0.125, 16, BF16,
+                                                       None))
 rec("rope empty", lib.tl_rope_inplace(null, null, null, 0, 64, 64, 1, 0, F32, None))
 rec("rope odd d", lib.tl_rope_inplace(null, null, null, 4, 64, 63, 1, 0, F32, None))
 rec("rope null", lib.tl_rope_inplace(null, null, null, 4, 64, 64, 1, 0, F32, None))
