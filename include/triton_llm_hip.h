@@ -145,8 +145,9 @@ int tl_attention_fwd(const void* q, const void* k, const void* v, void* o,
  * Launches the split pass, then a combine pass that merges the partials of
  * heads whose positions were shared by several workgroups and writes zeros
  * for empty sequences.  The workspace holds the partials and may be reused
- * by consecutive calls on one stream.  Small caches (max_ctx <= 2048 and at
- * most 64 MiB of K and V) instead run one workgroup per (sequence, KV head)
+ * by consecutive calls on one stream.  Small caches (max_ctx <= 2048, at
+ * most 384 KiB of K and V per (sequence, KV head) at max_ctx and 64 MiB in
+ * all) instead run one workgroup per (sequence, KV head)
  * that finishes its heads itself: one launch, no partials, and the kernels
  * read neither split_size nor the workspace.  The workspace arguments are
  * checked in every mode all the same (non-NULL, 16-byte aligned, at least

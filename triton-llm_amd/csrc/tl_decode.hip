@@ -19,7 +19,8 @@
 // reach 6.5 TB/s.)  A share may end inside one pair and continue into the
 // next; each piece is a segment with its own softmax state.
 //
-// Small caches (max_ctx <= 2048 and at most 64 MiB of K/V, e.g. GPT-2's
+// Small caches (max_ctx <= 2048, at most 384 KiB of K/V per (sequence, KV
+// head) and 64 MiB in all, e.g. GPT-2's
 // 1024-position cache) are latency-bound instead: a few MB spread over a
 // thousand shares cost a combine launch and dependent loads for little
 // streaming.  There one 16-wave workgroup (64 key streams -- 128 for
@@ -78,6 +79,12 @@ template <typename T, int D, int G, bool PAIR>
 constexpr int lanes_per_row() { return PAIR && D * T::size == 128 && G <= 4 ? 8 : 16; }
 constexpr int kPairMaxCtx = 2048;                  // pair mode: max_ctx at most
 constexpr int64_t kPairMaxBytes = 64ll << 20;      // pair mode: K/V cache bytes at most
+// pair mode: K/V bytes of one (sequence, KV head) at max_ctx at most.  One
+// workgroup streams a whole pair at about one CU's load rate (60 GB/s), so a
+// long pair outlasts the shares' extra combine launch: at batch 1, 256 KiB
+// per pair took 6.7 us in pair mode against 8.6 with shares, 512 KiB 16.3
+// against 10.6, 1 MiB 23.4 against 12.4.
+constexpr int64_t kPairMaxPairBytes = 384ll << 10;
 constexpr int kUnroll = 4;    // keys in flight per stream
 constexpr float kRescaleLog2 = 8.f;
 constexpr int kAuxNontemporal = 2;  // buffer-load cache policy: nt
@@ -697,7 +704,9 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
 // paths on the same small inputs.)
 bool pair_mode(const DecodeParams& p, int d_k, int esize) {
   const int64_t cache_bytes = (int64_t)p.batch * p.n_pairs * p.max_ctx * 2 * d_k * esize;
-  return !tl_overrides.decode_shares && p.max_ctx <= kPairMaxCtx && cache_bytes <= kPairMaxBytes;
+  const int64_t pair_bytes = (int64_t)p.max_ctx * 2 * d_k * esize;
+  return !tl_overrides.decode_shares && p.max_ctx <= kPairMaxCtx && cache_bytes <= kPairMaxBytes &&
+         pair_bytes <= kPairMaxPairBytes;
 }
 
 template <typename T, int D, int G>
