@@ -80,8 +80,6 @@ static_assert(W_LDS == 160 * 1024, "the whole LDS of a CU");
 __device__ __forceinline__ int vswz(int r) { return (r >> 1) & 7; }
 
 // O^T += V^T . P^T with the accumulator in AGPRs.
-template <typename T>
-struct PvMfma;
 // zero(c) sets c = 0 . 0 + 0 with the same instruction, so that every
 // definition of an accumulator is an AGPR output of an asm statement: were
 // it set to zero by ordinary code, its live range would not be tied to the
