@@ -230,6 +230,9 @@ def test_prefill_reads_cache_layout_and_seq_major_rows():
     (16, 1280, 1280, 8, 8, False),   # 5 tiles on 2 workgroups: partial last round
     (24, 1536, 256, 16, 8, True),    # bottom-right causal: tiles with no visible key between others
     (8, 768, 768, 6, 2, True),       # 2 (batch, kv) units: one list, 3 workgroups
+    (16, 2048, 2048, 6, 2, True),    # 6 heads in 8 lists: 4 parts per head (qt % 4), 3 parts per list
+    (16, 1024, 1024, 12, 4, True),   # 12 heads: 2 parts per head, lists cut inside a (batch, kv) unit
+    (8, 2048, 2048, 9, 3, False),    # 9 heads, 8 parts per head of one tile each, one workgroup per list
 ])
 @pytest.mark.parametrize("d_k", [64, 128])
 def test_prefill_persistent_schedules(monkeypatch, d128_kernel, cus, seq_q, seq_k, n_head, n_kv, causal, d_k):

@@ -170,6 +170,7 @@ struct TlOverrides {
   int max_cus;
   int decode_shares;
   int prefill_w64;
+  int prefill_one_list;
 };
 extern TlOverrides tl_overrides;
 

@@ -21,8 +21,9 @@ struct FlashParams {
   float scale_log2;
   // Static tile schedule of the persistent 16-bit kernel (see flash_fwd_16).
   int n_queues;    // 8 (one tile list per XCD) or 1
-  int q_units;     // (batch, kv head) units per list
-  int q_tiles;     // tiles per list: q_units * n_qt * group
+  int q_split;     // parts per query head: part j holds its tiles with qt % q_split == j
+  int q_parts;     // parts per list
+  int q_tiles;     // tiles per list: q_parts * n_qt / q_split
   int q_machines;  // workgroups per list
   int q_triple;    // first three rounds use the balanced-triple order
 };
@@ -64,18 +65,23 @@ __device__ __forceinline__ int fresh_lane() {
   return l;
 }
 
-// Tile i of list `queue` of the persistent schedule: lists hold the (batch,
-// kv head) units' query tiles ordered by qt descending (causal cost), the
-// group's query heads of one qt adjacent.
+// Tile i of list `queue` of the persistent schedule.  The query heads of the
+// call, (batch, kv head) unit by unit, are cut into q_split parts each (part
+// j: the head's query tiles with qt % q_split == j), and list x holds parts
+// [x q_parts, (x + 1) q_parts): a few consecutive heads, hence few (batch,
+// kv head) units, whose K / V then stay in one XCD's L2.  A list is ordered
+// by qt descending (causal cost): the lvl-th costliest tile of every part,
+// parts in order, then the next level.
 __device__ __forceinline__ void decode_tile(const FlashParams& p, int queue, int i, int& b, int& hq, int& qt) {
-  const int per_qt = p.q_units * p.group;  // tiles per qt step in a list
-  const int qt_rev = i / per_qt;
-  const int rem = i - qt_rev * per_qt;
-  const int u = queue * p.q_units + rem / p.group;  // (batch, kv head) unit
+  const int lvl = i / p.q_parts;
+  const int part = queue * p.q_parts + (i - lvl * p.q_parts);
+  const int hs = part / p.q_split;  // query head (b, hkv, g) as (b * n_kv + hkv) * group + g
+  const int j = part - hs * p.q_split;
+  const int u = hs / p.group;
   const int hkv = u % p.n_kv;
   b = u / p.n_kv;
-  qt = p.n_qt - 1 - qt_rev;
-  hq = hkv * p.group + rem % p.group;
+  hq = hkv * p.group + (hs - u * p.group);
+  qt = j + p.q_split * (p.n_qt / p.q_split - 1 - lvl);
 }
 
 // Rank (position in its list) of workgroup j's r-th tile; >= q_tiles: none.

@@ -114,9 +114,10 @@ __device__ __forceinline__ void decode_block(const FlashParams& p, int& b, int& 
 // ---------------------------------------------------------------------------
 // Persistence: one workgroup per CU walks a static list of query tiles.
 //
-// Tiles (b, hq, qt) form n_queues lists -- one per XCD when the (batch, kv
-// head) units divide by 8, so that the K/V tiles a list reads stay in one
-// XCD's L2 (the dispatcher hands workgroups to XCDs round-robin, so
+// Tiles (b, hq, qt) form n_queues lists -- one per XCD when the query heads,
+// cut into q_split parts by qt % q_split, deal evenly into 8 lists, so that
+// a list covers a few consecutive heads and the K/V tiles it reads stay in
+// one XCD's L2 (the dispatcher hands workgroups to XCDs round-robin, so
 // workgroup L serves list L % n_queues) -- each ordered by qt descending,
 // i.e. by causal cost.  Workgroup j of a list takes ranks j, then by rounds
 // of q_machines in alternating direction (a round pair then sums to the same
@@ -1177,11 +1178,23 @@ int launch_flash_16(FlashParams& p, void* ws, bool causal, hipStream_t st) {
   const bool scale_s = std::is_same<T, F16>::value && fabsf(p.scale_log2) > 1.f;
   p.vt = ws;
   p.n_qt = (p.seq_q + K16_BM - 1) / K16_BM;
-  // Tile lists: one per XCD when the (batch, kv head) units split evenly.
-  const int units = p.batch * p.n_kv;
-  p.n_queues = units % 8 == 0 ? 8 : 1;
-  p.q_units = units / p.n_queues;
-  p.q_tiles = p.q_units * p.n_qt * p.group;
+  // Tile lists: one per XCD when the query heads' tiles deal evenly into 8
+  // lists of whole parts (q_split parts per head, each n_qt / q_split tiles);
+  // otherwise one list.
+  const int heads = p.batch * p.n_head;
+  p.n_queues = 1;
+  p.q_split = 1;
+  if (!tl_overrides.prefill_one_list) {
+    for (int s = 1; s <= 8; s *= 2) {
+      if ((int64_t)heads * s % 8 == 0 && p.n_qt % s == 0) {
+        p.n_queues = 8;
+        p.q_split = s;
+        break;
+      }
+    }
+  }
+  p.q_parts = (int)((int64_t)heads * p.q_split / p.n_queues);
+  p.q_tiles = p.q_parts * (p.n_qt / p.q_split);
   p.q_machines = min((tl_device_cus() + p.n_queues - 1) / p.n_queues, p.q_tiles);
   const int rounds = p.q_tiles / p.q_machines;
   p.q_triple = (p.q_tiles % p.q_machines == 0 && rounds % 2 == 1 && rounds >= 3 && p.q_machines % 2 == 0) ? 1 : 0;
