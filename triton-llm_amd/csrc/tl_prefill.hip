@@ -434,7 +434,14 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
           kfr[g] = *(const u32x4*)(smem + (kb_lane ^ (ks << 5)) + 32 * mb * ROWB);
         }
       };
-      __builtin_amdgcn_s_setprio(1);
+      // G phases issue at raised priority, so a G phase's MFMAs win over the
+      // other group's softmax -- except group 1's G(0), which runs beside
+      // group 0's G(0): it yields, so group 0 finishes its first S sooner and
+      // its first softmax overlaps group 1's MFMAs.
+      if (group == 1 && t == 0)
+        __builtin_amdgcn_s_setprio(0);
+      else
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int g = 0; g < kPrefetch; ++g) fetch(g);
 #pragma unroll
@@ -550,6 +557,17 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
       __builtin_amdgcn_sched_barrier(0);
     };
 
+    // This wave's next Q rows out of LDS: group 0's in K buffer
+    // (tb + n_kt) & 1, group 1's in V^T buffer (tb + n_kt) & 1 (each group
+    // stages its output there too).
+    const int qbuf = (group == 0 ? 0 : 2 * TILEB) + ((tb + n_kt) & 1) * TILEB;
+    auto read_next_q = [&]() __attribute__((always_inline)) {
+      const int ql = qbuf + 32 * wq * ROWB + k_lane_of(fresh_lane());
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) qf[ks] = __builtin_bit_cast(frag, *(const u32x4*)(smem + (ql ^ (ks << 5))));
+      scale_q();
+    };
+
     // ---- group 0 runs G(t), A(t); group 1 runs A(t-1), G(t), for t = 0 .. n_kt.
     // One barrier per t, after group 0's A(t) (which waits for the loads it
     // issued in G(t)) and group 1's G(t): G(t+1) then finds K_{t+1} and
@@ -572,6 +590,9 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
           lds_barrier();
         }
         g_phase(n_kt, Y{}, Y{}, N{});  // PV of the last tile; no S
+        // Its next Q rows (loaded in G(n_kt - 1), published by the last
+        // barrier) while group 1 still runs its last softmax and G phase.
+        if (has_next) read_next_q();
         wait_vmcnt<0>();
         lds_barrier();
       } else {
@@ -589,29 +610,22 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
     }
 
     // ---- tile switch ---------------------------------------------------------------
-    // 1. Every wave copies its next Q rows out of LDS (or, after a tile that
-    //    ran no phase, loads them cold).  2. Barrier: the two Q buffers are now
-    //    free until phase 2 of the next tile.  3. Each wave stages its output
-    //    rows, normalised and rounded, in its own part of its group's Q buffer
-    //    and stores them row-contiguously (16 lanes per 256-byte row), so each
-    //    store instruction writes whole cache lines.  The stores are not
-    //    waited for here.
+    // 1. Every wave of group 1 copies its next Q rows out of LDS (group 0 did
+    //    in its last step; after a tile that ran no phase, every wave loads
+    //    them cold).  2. Each wave stages its output rows, normalised and
+    //    rounded, in the rows of its group's Q buffer it just read its Q from
+    //    (so no barrier is needed between the two) and stores them
+    //    row-contiguously (16 lanes per 256-byte row), so each store
+    //    instruction writes whole cache lines.  The stores are not waited
+    //    for here.
     const float inv = kMfmaRowSum ? 1.f / l_acc[0] : 1.f / sum_xor32((l4[0] + l4[1]) + (l4[2] + l4[3]));
     const int ntb = (tb + n_kt + 1) & 1;  // where the next K_0 went
-    // the next Q rows: group 0's in K buffer (tb + n_kt) & 1, group 1's in
-    // V^T buffer (tb + n_kt) & 1; each group stages its output there too
-    const int qbuf = (group == 0 ? 0 : 2 * TILEB) + ((tb + n_kt) & 1) * TILEB;
     if (has_next) {
-      if (n_kt > 0) {
-        const int ql = qbuf + 32 * wq * ROWB + k_lane_of(fresh_lane());
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) qf[ks] = __builtin_bit_cast(frag, *(const u32x4*)(smem + (ql ^ (ks << 5))));
-        scale_q();
-      } else {
+      if (n_kt == 0)
         cold_start(nxt, ntb);  // no phase ran to prefetch it
-      }
+      else if (group == 1)
+        read_next_q();
     }
-    lds_barrier();
     {
       const int ln = fresh_lane();
       const int lq = ln & 31, h = ln >> 5;
