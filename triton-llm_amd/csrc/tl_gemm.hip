@@ -718,6 +718,7 @@ PromptPlan prompt_plan(int m, int k, const GemmGroups& G, int esize) {
   const double rate = esize == 2 ? 9.0e14 : 1.3e14;
   const double t1 = 2.0 * m * (double)k * (double)ncols / rate;
   auto busiest = [&](int S) { return (double)((P.tiles * (int64_t)S + cus - 1) / cus) / S; };
+  auto reduce_t = [&](int S) { return ((double)S * 4 + esize) * m * (double)ncols / 5.0e12 + 3e-6; };
   double best = t1;
   P.ksplit = 1;
   // Few rows (a batch of decoded tokens): the product streams B, and a few
@@ -744,10 +745,47 @@ PromptPlan prompt_plan(int m, int k, const GemmGroups& G, int esize) {
   }
   for (int S = 2; S <= 4 && esize == 4; ++S) {
     if (n_kt < 4 * S) break;
-    const double t = t1 * busiest(S) / busiest(1) + ((double)S * 4 + esize) * m * (double)ncols / 5.0e12 + 3e-6;
+    const double t = t1 * busiest(S) / busiest(1) + reduce_t(S);
     if (t < 0.97 * best) {
       best = t;
       P.ksplit = S;
+    }
+  }
+  if (esize == 4 && !P.narrow) {
+    // fp32 with 64-row tiles instead, when a model of the busiest CU's items
+    // says they win by 3%.  A CU runs two items at once at the sustained
+    // rate; a lone item runs at about 0.7 of it (one 128 x 128 fp32
+    // workgroup alone on a CU reaches 58% of the CU's MFMA peak, two
+    // together 82%), and a 64-row tile does its FLOPs at about 0.865 of a
+    // 128-row tile's rate (Llama-3.2-3B o at 2048 rows, K split in 2 either
+    // way: 321 against 316 us).  More items of 64 rows fill the CUs that a
+    // few 128-row tiles leave with one item or none (SmolLM2-360M at 2048
+    // rows: grouped q/k/v 78 -> 73 us, gate/up 191 -> 166 us).
+    const double r2 = rate / cus, r1 = r2 * (0.58 / 0.82);
+    auto model = [&](int ctm, int S) {
+      int64_t ctiles = 0;
+      for (int g = 0; g < G.count; ++g) ctiles += (int64_t)((m + ctm - 1) / ctm) * ((G.n[g] + kGmTile - 1) / kGmTile);
+      const int64_t per_cu = (ctiles * S + cus - 1) / cus;
+      const double w = 2.0 * ctm * kGmTile * (double)k / S / (ctm < kGmTile ? 0.865 : 1.0);
+      return (double)(per_cu - per_cu % 2) * w / r2 + (double)(per_cu % 2) * w / r1 + (S > 1 ? reduce_t(S) : 0.0);
+    };
+    const double t_cur = model(kGmTile, P.ksplit);
+    double t_best = 0.97 * t_cur;
+    int best_s = 0;
+    for (int S = 1; S <= 4; ++S) {
+      if (S > 1 && n_kt < 4 * S) break;
+      const double t = model(kGmTile / 2, S);
+      if (t < t_best) {
+        t_best = t;
+        best_s = S;
+      }
+    }
+    if (best_s) {
+      P.narrow = true;
+      P.tiles_m = (m + kGmTile / 2 - 1) / (kGmTile / 2);
+      P.tiles = 0;
+      for (int g = 0; g < G.count; ++g) P.tiles += P.tiles_m * ((G.n[g] + kGmTile - 1) / kGmTile);
+      P.ksplit = best_s;
     }
   }
   P.kt_per = (n_kt + P.ksplit - 1) / P.ksplit;
