@@ -202,6 +202,28 @@ def test_gemm_prompt_split_k(dtype, M, K, Ns):
             np.testing.assert_allclose(got, exp, rtol=8e-3, atol=1e-2)
 
 
+@pytest.mark.parametrize("M,K,Ns", [(2048, 960, (960, 320, 320)), (2048, 960, (960,)), (2048, 960, (320,)),
+                                   (2000, 2560, (960,)), (1999, 964, (2560, 2560))])
+def test_gemm_prompt_fp32_64_row_plans(M, K, Ns):
+    """fp32 prompt products with few 128-row tiles per CU (SmolLM2-360M's
+    projections at a 2048-token prompt) run 64-row tiles, whole-K or with K
+    split in 2-4: the grouped q/k/v, o / down with their splits, ragged M and
+    a K tail inside a 16-k stage."""
+    print(f"[case] gemm fp32 64-row {M}x{K} -> {Ns}", flush=True)
+    rng = np.random.default_rng(M + 5 * K + sum(Ns))
+    a = rng.standard_normal((M, K), dtype=np.float32)
+    bs = [rng.standard_normal((K, n), dtype=np.float32) / np.float32(np.sqrt(K)) for n in Ns]
+    a_dev = gpu.to_device(a)
+    if len(Ns) == 1:
+        outs = [gemm(a_dev, gpu.to_device(bs[0]))]
+    else:
+        outs = gemm_grouped(a_dev, [gpu.to_device(b) for b in bs])
+    for b, o in zip(bs, outs):
+        err = H.max_abs(H.download(o), gemm_ref(a, b))
+        H.report(f"fp32 64-row {M}x{K}@{K}x{b.shape[1]}", err, 2e-3)
+        assert err <= 2e-3
+
+
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
 @pytest.mark.parametrize("M,K,Ns", [(9, 3072, (3072,)), (33, 3072, (3072, 1024, 1024)), (64, 8192, (3072,)),
                                     (130, 3072, (3072, 1024)), (17, 3000, (3000,))])
