@@ -32,6 +32,14 @@ constexpr int kMaxSmallSplit = 32; // K-slices at most for few-row MFMA products
 constexpr int kNarrowMaxM = 64;
 constexpr int kNarrowBkb16 = 128;
 constexpr int kNarrowNst16 = 2;
+// fp32 MFMA kernels, k per LDS stage: 16, except 32 for the 64-row tiles a
+// prompt takes by the occupancy model below (72 KiB in three stages, still
+// two workgroups per CU; SmolLM2-360M's fp32 prompt layer 387 -> 380 us).
+// Few rows keep 16 (a Llama-3.2-3B layer at 64 rows: 183 against 194 us
+// with 32), and so do 128-row tiles (32 would need 96 KiB: one workgroup
+// per CU).
+constexpr int kF32Bk = 16;
+constexpr int kF32BkDeep = 32;
 constexpr int kSkThreads = 256;    // 4 waves
 constexpr int kSkUnroll = 16;      // row loads in flight per lane
 constexpr int kSkMaxTk = 1024;     // rows per K-slice at most (A's slice is staged in LDS)
@@ -672,6 +680,7 @@ __global__ __launch_bounds__(256) void gemm_simple_kernel(GemmParams p) {
 struct PromptPlan {
   bool huge;      // 16-bit 256 x 256 tiles (eight waves)
   bool narrow;    // 64 x 128 tiles (few rows: half the padding of 128-row tiles)
+  bool f32_deep;  // fp32 64-row tiles with 32-k stages (prompts)
   int tiles_m, tiles;
   int ksplit, kt_per;
   size_t ws_bytes;  // fp32 partials when split
@@ -711,8 +720,8 @@ PromptPlan prompt_plan(int m, int k, const GemmGroups& G, int esize) {
   const int tn = P.huge ? 2 * kGmTile : kGmTile;
   for (int g = 0; g < G.count; ++g) P.tiles += P.tiles_m * ((G.n[g] + tn - 1) / tn);
   // k per LDS stage of the kernel used
-  const int bk = esize == 2 ? (P.huge ? 32 : (P.narrow ? kNarrowBkb16 / 2 : 64)) : 16;
-  const int n_kt = (k + bk - 1) / bk;
+  const int bk = esize == 2 ? (P.huge ? 32 : (P.narrow ? kNarrowBkb16 / 2 : 64)) : kF32Bk;
+  int n_kt = (k + bk - 1) / bk;
   // modelled seconds: the product at a sustained rate, scaled by the busiest
   // CU's share of items; the reduce as HBM traffic plus a launch
   const double rate = esize == 2 ? 9.0e14 : 1.3e14;
@@ -772,8 +781,9 @@ PromptPlan prompt_plan(int m, int k, const GemmGroups& G, int esize) {
     const double t_cur = model(kGmTile, P.ksplit);
     double t_best = 0.97 * t_cur;
     int best_s = 0;
+    const int n_kt64 = (k + kF32BkDeep - 1) / kF32BkDeep;
     for (int S = 1; S <= 4; ++S) {
-      if (S > 1 && n_kt < 4 * S) break;
+      if (S > 1 && n_kt64 < 4 * S) break;
       const double t = model(kGmTile / 2, S);
       if (t < t_best) {
         t_best = t;
@@ -786,6 +796,8 @@ PromptPlan prompt_plan(int m, int k, const GemmGroups& G, int esize) {
       P.tiles = 0;
       for (int g = 0; g < G.count; ++g) P.tiles += P.tiles_m * ((G.n[g] + kGmTile - 1) / kGmTile);
       P.ksplit = best_s;
+      P.f32_deep = true;
+      n_kt = n_kt64;
     }
   }
   P.kt_per = (n_kt + P.ksplit - 1) / P.ksplit;
@@ -849,10 +861,12 @@ int launch_gemm(const void* a, const GemmGroups& G, int m, int k, int64_t lda, v
       else
         hipLaunchKernelGGL((gemm_mfma_kernel<T, 128, 2, 2>), grid, dim3(kGmThreads), 0, st, p);
     } else {
-      if (P.narrow)
-        hipLaunchKernelGGL((gemm_mfma_kernel<T, 64, 3, 1>), grid, dim3(kGmThreads), 0, st, p);
+      if (P.narrow && P.f32_deep)
+        hipLaunchKernelGGL((gemm_mfma_kernel<T, 4 * kF32BkDeep, 3, 1>), grid, dim3(kGmThreads), 0, st, p);
+      else if (P.narrow)
+        hipLaunchKernelGGL((gemm_mfma_kernel<T, 4 * kF32Bk, 3, 1>), grid, dim3(kGmThreads), 0, st, p);
       else
-        hipLaunchKernelGGL((gemm_mfma_kernel<T, 64, 3, 2>), grid, dim3(kGmThreads), 0, st, p);
+        hipLaunchKernelGGL((gemm_mfma_kernel<T, 4 * kF32Bk, 3, 2>), grid, dim3(kGmThreads), 0, st, p);
     }
     int e = tl_launch_status();
     if (e || p.ksplit == 1) return e;
