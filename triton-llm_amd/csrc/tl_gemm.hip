@@ -280,7 +280,8 @@ int launch_skinny(const void* a, GemmGroups G, int m, int k, int64_t lda, void* 
 //
 // Workgroup tile 128 x 128 of C, 4 waves in 2 x 2, each wave 64 x 64 (2 x 2
 // blocks of 32 x 32).  K is walked in LDS stages (16-bit: 64 k in two
-// stages; fp32: 16 k in three), every tile moved global -> LDS by LDS-DMA
+// stages; fp32: 16 k in three, 32 k for the 64-row prompt plans), every
+// tile moved global -> LDS by LDS-DMA
 // (buffer_load ... lds: no register round trip), every wave loading a
 // quarter.  Each wave computes the transposed block C^T = B^T . A^T with
 // the MFMA, so a lane ends up owning one row of C and 4 consecutive columns
@@ -851,7 +852,8 @@ int launch_gemm(const void* a, const GemmGroups& G, int m, int k, int64_t lda, v
     // Measured at the models' prompt shapes (2048 rows): 16-bit runs best
     // with 64 k per stage in two stages (729 against 645 TFLOP/s with 32 k
     // in three, 691 with 32 k in four, 507 with 64 k in three); fp32 is
-    // within 1% across those and keeps 16 k in three stages.
+    // within 1% across those and keeps 16 k in three stages, except the
+    // 64-row tiles a prompt takes by the occupancy model (kF32BkDeep).
     const dim3 grid((unsigned)(8 * p.per_xcd));
     if constexpr (T::size == 2) {
       if (P.huge)
