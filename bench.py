@@ -521,7 +521,7 @@ def bench_prefill(cfg, steps, warmup, replicas=1, cpu=True, cpu_budget_s=10.0, r
             apply_rope(gpu.view(q, (B * Hq * S, D)), cd, sd, seq_len=S)
             apply_rope(gpu.view(k, (B * Hkv * S, D)), cd, sd, seq_len=S)
         sets.append((q, k, v, gpu.allocate(q.shape, gdt)))
-    wsb = flash_workspace_bytes(B, Hkv, S, D, gdt)
+    wsb = flash_workspace_bytes(B, Hkv, S, D, gdt, n_head=Hq, seq_q=S)
     ws = gpu.allocate((max(wsb, 1),), np.uint8)
     lib = gpu.runtime()
 

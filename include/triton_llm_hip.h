@@ -116,9 +116,23 @@ int tl_rope_inplace(void* x, const float* cos_table, const float* sin_table,
  * Workspace: tl_attention_fwd_workspace_bytes
  * (the 16-bit MFMA path at d_k 128 stages a key-major copy of V there; 0
  * for d_k 64 and fp32, which read V in place; NULL is accepted when 0).
+ * A 16-byte-aligned workspace of tl_attention_fwd_workspace_bytes_split
+ * bytes (at least the above) also lets a causal 16-bit MFMA call with
+ * seq_k >= seq_q and few query tiles split the key range of its costliest
+ * tiles over two workgroups, which balances the persistent schedule; the
+ * two parts of a tile merge inside the kernel (no extra launch).  Given
+ * less, the call runs unsplit.  Split and unsplit outputs agree to rounding;
+ * either is deterministic for the same arguments and workspace size.  The
+ * workspace needs no initialisation and may be reused by later calls (on
+ * one stream, as the V copy requires).
  * ------------------------------------------------------------------------- */
 size_t tl_attention_fwd_workspace_bytes(int batch, int n_kv_head, int seq_k,
                                         int d_k, int dtype);
+/* No counterpart in the reference (its attention launches take no
+ * workspace); see above. */
+size_t tl_attention_fwd_workspace_bytes_split(int batch, int n_head, int n_kv_head,
+                                              int seq_q, int seq_k, int d_k,
+                                              int causal, int dtype);
 int tl_attention_fwd(const void* q, const void* k, const void* v, void* o,
                      void* workspace, size_t workspace_bytes, int batch,
                      int n_head, int n_kv_head, int seq_q, int seq_k, int d_k,

@@ -41,6 +41,24 @@ def test_workspace_queries():
     assert lib.tl_attention_fwd_workspace_bytes(2, 3, 100, 64, _lib.DTYPE_F16) == 0
     assert lib.tl_attention_fwd_workspace_bytes(2, 3, 100, 128, _lib.DTYPE_F16) == 2 * 3 * 128 * 128 * 2
     assert lib.tl_attention_fwd_workspace_bytes(1, 1, 100, 32, _lib.DTYPE_BF16) == 0  # generic path
+    # Key-split region: only causal 16-bit d_k 128 calls with seq_k >= seq_q and few
+    # tiles; otherwise the minimum.  (Planned for 256 CUs when no device is visible.)
+    fwd, split = lib.tl_attention_fwd_workspace_bytes, lib.tl_attention_fwd_workspace_bytes_split
+    BF, F16, F32 = _lib.DTYPE_BF16, _lib.DTYPE_F16, _lib.DTYPE_F32
+    base = fwd(1, 8, 2048, 128, BF)
+    ll = split(1, 24, 8, 2048, 2048, 128, 1, BF)  # Llama-3.2-3B heads, a 2048-token prompt
+    assert ll > base and split(1, 24, 8, 2048, 2048, 128, 1, F16) == ll
+    # after the V copy (256-aligned): 64 bytes of arrival words per split tile
+    # (256-aligned), then two partial slots of 8 waves x (64 KiB / 4 + 512) bytes
+    slot = 8 * (4 * 4 * 1024 + 512)
+    extra = ll - base
+    tiles = extra // (2 * slot)
+    assert tiles > 0 and extra == ((tiles * 64 + 255) // 256) * 256 + tiles * 2 * slot
+    assert split(1, 24, 8, 2048, 2048, 128, 0, BF) == base                # not causal
+    assert split(1, 24, 8, 2048, 2048, 128, 1, F32) == 0                  # fp32 kernel
+    assert split(1, 24, 8, 2048, 1024, 128, 1, BF) == fwd(1, 8, 1024, 128, BF)  # seq_q > seq_k
+    assert split(4, 9, 3, 2048, 2048, 64, 1, BF) == 0                     # d_k 64: never split
+    assert split(1, 24, 8, 8192, 8192, 128, 1, BF) == fwd(1, 8, 8192, 128, BF)  # balanced: 5a
     split = lib.tl_decode_split_size(64, 8, 16384)
     assert split % 16 == 0 and 64 <= split <= 4096
     assert lib.tl_decode_split_size(8, 12, 1024) == 64  # short caches: one-iteration floor

@@ -63,7 +63,8 @@ class RecordingRuntime:
     the real library."""
 
     HOST_ONLY = ("tl_decode_split_size", "tl_attention_decode_workspace_bytes",
-                 "tl_attention_fwd_workspace_bytes", "tl_error_string")
+                 "tl_attention_fwd_workspace_bytes", "tl_attention_fwd_workspace_bytes_split",
+                 "tl_error_string")
 
     def __init__(self):
         self.real = _lib.load()

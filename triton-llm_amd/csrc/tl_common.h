@@ -165,12 +165,19 @@ int tl_fill_bytes(void* dst, unsigned char value, size_t nbytes, hipStream_t st)
 //   prefill_w64    TRITON_LLM_HIP_PREFILL_W64 nonzero: 16-bit d_k 128
 //                  prefill runs flash_fwd_w64 (64 query rows per wave)
 //                  instead of flash_fwd_16, so tests and A/B timing can
-//                  run both.
+//                  run both;
+//   prefill_one_list  TRITON_LLM_HIP_PREFILL_ONE_LIST nonzero: flash_fwd_16
+//                  deals every tile from one list instead of one per XCD;
+//   prefill_no_split  TRITON_LLM_HIP_PREFILL_NO_SPLIT nonzero: flash_fwd_16
+//                  splits no tile's key range over two workgroups (and
+//                  tl_attention_fwd_workspace_bytes_split asks for no
+//                  split region).
 struct TlOverrides {
   int max_cus;
   int decode_shares;
   int prefill_w64;
   int prefill_one_list;
+  int prefill_no_split;
 };
 extern TlOverrides tl_overrides;
 

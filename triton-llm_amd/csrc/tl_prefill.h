@@ -7,6 +7,8 @@
 
 namespace tlp {
 
+constexpr int kMaxEntries = 64;  // list entries of a key-split schedule
+
 struct FlashParams {
   const void* q;
   const void* k;
@@ -26,6 +28,21 @@ struct FlashParams {
   int q_tiles;     // tiles per list: q_parts * n_qt / q_split
   int q_machines;  // workgroups per list
   int q_triple;    // first three rounds use the balanced-triple order
+  // Key split (causal flash_fwd_16 only; n_entries 0: none).  A list is a
+  // sequence of n_entries entries of q_parts items each: entry e holds level
+  // lvl = e_code[e] & 63's tiles whole (part e_code[e] >> 6 = 0) or the lower
+  // (1) or upper (2) part of their key tiles.  The split levels are the
+  // costliest, 0 .. n_split_levels - 1.  The parts of one tile merge through
+  // split_ws (see flash_fwd_16's tile switch).  The kernel reads e_code from
+  // the kernel-argument segment (entry_code): indexing the by-value argument
+  // would copy the array into registers.
+  int n_entries;
+  int n_split_levels;
+  int n_split_tiles;         // n_queues * n_split_levels * q_parts
+  uint32_t split_part_bytes; // partial region bytes (2 slots per split tile)
+  uint64_t split_token;      // this call's arrival tag (never 0)
+  void* split_ws;            // arrival words (8 per split tile), then the partial slots
+  uint8_t e_code[kMaxEntries];
 };
 
 // 16-bit kernels: query rows per tile (both flash_fwd_16 and flash_fwd_w64)
@@ -72,7 +89,7 @@ __device__ __forceinline__ int fresh_lane() {
 // kv head) units, whose K / V then stay in one XCD's L2.  A list is ordered
 // by qt descending (causal cost): the lvl-th costliest tile of every part,
 // parts in order, then the next level.
-__device__ __forceinline__ void decode_tile(const FlashParams& p, int queue, int i, int& b, int& hq, int& qt) {
+__host__ __device__ inline void decode_tile(const FlashParams& p, int queue, int i, int& b, int& hq, int& qt) {
   const int lvl = i / p.q_parts;
   const int part = queue * p.q_parts + (i - lvl * p.q_parts);
   const int hs = part / p.q_split;  // query head (b, hkv, g) as (b * n_kv + hkv) * group + g
@@ -84,8 +101,22 @@ __device__ __forceinline__ void decode_tile(const FlashParams& p, int queue, int
   qt = j + p.q_split * (p.n_qt / p.q_split - 1 - lvl);
 }
 
+// Item i of list `queue` of a key-split schedule (p.n_entries > 0) whose
+// entry e = i / q_parts has code `code`: the tile as decode_tile gives it
+// for the entry's level, its key part (0 whole, 1 lower, 2 upper) and, for a
+// part, the tile's split index (< n_split_tiles).
+__host__ __device__ inline void decode_item(const FlashParams& p, int queue, int i, int code, int& b, int& hq,
+                                            int& qt, int& kpart, int& sidx) {
+  const int e = i / p.q_parts;
+  const int within = i - e * p.q_parts;
+  const int lvl = code & 63;
+  decode_tile(p, queue, lvl * p.q_parts + within, b, hq, qt);
+  kpart = code >> 6;
+  sidx = (queue * p.n_split_levels + lvl) * p.q_parts + within;
+}
+
 // Rank (position in its list) of workgroup j's r-th tile; >= q_tiles: none.
-__device__ __forceinline__ int sched_rank(const FlashParams& p, int j, int r) {
+__host__ __device__ inline int sched_rank(const FlashParams& p, int j, int r) {
   const int m = p.q_machines;
   if (p.q_triple && r < 3) {
     const int hm = m / 2;

@@ -36,6 +36,11 @@
 #include <math.h>
 #include <stdlib.h>
 
+#include <algorithm>
+#include <stddef.h>
+#include <atomic>
+#include <mutex>
+#include <random>
 #include <type_traits>
 
 namespace {
@@ -220,21 +225,48 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
                                 : 16u * (uint32_t)p.sk_pad * 2u;     // bytes of 16 V^T rows
 
   // ---- tile state --------------------------------------------------------------
+  // Code of list entry e, read from the kernel-argument segment (p is the
+  // kernel's only argument, at offset 0) with a scalar load.
+  auto entry_code = [&](int e) __attribute__((always_inline)) {
+    typedef const __attribute__((address_space(4))) uint32_t kword;
+    kword* tab = (kword*)((const __attribute__((address_space(4))) char*)__builtin_amdgcn_kernarg_segment_ptr() +
+                          offsetof(FlashParams, e_code));
+    return (int)((tab[e >> 2] >> (8 * (e & 3))) & 0xffu);
+  };
+  // Key-split parts exist only for causal d_k 128 (the host plans no split
+  // otherwise); other instances carry none of their code.
+  constexpr bool kSplit = CAUSAL && D == 128;
+  // A key-split part covers K tiles [kt0, kt0 + n_kt) of its tile: the
+  // lower part [0, h), the upper [h, n_kt of the whole tile), h = min(half
+  // the tile's K tiles, (first query row + off) / BN), so every query row of
+  // the tile (first row >= BM, off >= 0: the host splits no other tile) has
+  // keys in both parts.
   struct Tile {
-    int b, hq, qt, n_kt, k_rows;
-    const char* kg;
-    const char* vg;  // natural V of the tile's (batch, kv head) (VNAT)
+    int b, hq, qt, n_kt, k_rows, kt0, kpart, sidx;
+    const char* kg;  // K rows from key kt0 * BN on
+    const char* vg;  // natural V rows from key kt0 * BN on (VNAT)
   };
   auto make_tile = [&](int rank) __attribute__((always_inline)) {
     Tile tl;
-    decode_tile(p, queue, rank, tl.b, tl.hq, tl.qt);
+    tl.kpart = 0;
+    tl.sidx = 0;
+    if (kSplit && p.n_entries)
+      decode_item(p, queue, rank, entry_code(rank / p.q_parts), tl.b, tl.hq, tl.qt, tl.kpart, tl.sidx);
+    else
+      decode_tile(p, queue, rank, tl.b, tl.hq, tl.qt);
     const int q_last = min(p.seq_q, tl.qt * K16_BM + K16_BM) - 1;
     int k_end = p.seq_k;
     if (CAUSAL) k_end = max(0, min(p.seq_k, q_last + off + 1));
-    tl.n_kt = (k_end + BN - 1) / BN;             // K tiles the workgroup loads
-    tl.k_rows = min(p.seq_k, tl.n_kt * BN);      // keys the workgroup reads
-    tl.kg = (const char*)((const Bits*)p.k + tl.b * p.k_sb + (tl.hq / p.group) * p.k_sh);
-    tl.vg = (const char*)((const Bits*)p.v + tl.b * p.v_sb + (tl.hq / p.group) * p.v_sh);
+    tl.n_kt = (k_end + BN - 1) / BN;  // K tiles the workgroup loads
+    tl.kt0 = 0;
+    if (kSplit && tl.kpart) {
+      const int h = min(tl.n_kt / 2, (tl.qt * K16_BM + off) / BN);
+      tl.kt0 = tl.kpart == 1 ? 0 : h;
+      tl.n_kt = tl.kpart == 1 ? h : tl.n_kt - h;
+    }
+    tl.k_rows = min(p.seq_k - tl.kt0 * BN, tl.n_kt * BN);  // keys the workgroup reads
+    tl.kg = (const char*)((const Bits*)p.k + tl.b * p.k_sb + (tl.hq / p.group) * p.k_sh + (int64_t)tl.kt0 * BN * p.k_ss);
+    tl.vg = (const char*)((const Bits*)p.v + tl.b * p.v_sb + (tl.hq / p.group) * p.v_sh + (int64_t)tl.kt0 * BN * p.v_ss);
     return tl;
   };
 
@@ -259,7 +291,7 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
       return rsrc_of(tl.vg + (int64_t)tv * BN * v_ss2, (uint32_t)rows * v_ss2);
     } else {
       const char* vg = (const char*)((const Bits*)p.vt + ((int64_t)tl.b * p.n_kv + tl.hq / p.group) * D * p.sk_pad);
-      return rsrc_of(vg + (int64_t)tv * BN * 2, tv < tl.n_kt ? (uint32_t)D * (uint32_t)p.sk_pad * 2u : 0u);
+      return rsrc_of(vg + (int64_t)(tl.kt0 + tv) * BN * 2, tv < tl.n_kt ? (uint32_t)D * (uint32_t)p.sk_pad * 2u : 0u);
     }
   };
   // Q rows [128 g, 128 g + 128) of a tile (rows past seq_q read as zeros).
@@ -342,6 +374,12 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
     int wave_k_end = p.seq_k;
     if (CAUSAL) wave_k_end = max(0, min(p.seq_k, min(q0 + 31, p.seq_q - 1) + off + 1));
     if (q0 >= p.seq_q) wave_k_end = 0;  // no rows: no compute
+    // Key positions relative to the part's first key (a key-split part
+    // starts at K tile kt0): the softmax compares t * BN with these.
+    const int kshift = kSplit ? cur.kt0 * BN : 0;
+    const int seq_k_rel = p.seq_k - kshift;
+    const int off_rel = off - kshift;
+    const int wave_k_end_rel = wave_k_end - kshift;
 
 #pragma unroll
     for (int i = 0; i < NDB; ++i)
@@ -477,8 +515,8 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
     // A(t): masked softmax of S_t -> P_t.  key = kb + 32 mb + 8 (r/4) + 4 h + r % 4;
     // a tile the wave does not use yields P = 0.
     auto a_phase = [&](int t) __attribute__((always_inline)) {
-      const int kb = t * BN;
-      if (t >= n_kt || kb >= wave_k_end) {
+      const int kb = t * BN;  // first key of the tile, relative to the part's first key
+      if (t >= n_kt || kb >= wave_k_end_rel) {
 #pragma unroll
         for (int tt = 0; tt < BN / 16; ++tt) pw[tt] = u32x4{0u, 0u, 0u, 0u};
         __builtin_amdgcn_sched_barrier(0);
@@ -491,12 +529,12 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
 #pragma unroll
           for (int rr = 0; rr < 16; ++rr) s[mb][rr] = fmaf(s[mb][rr], p.scale_log2, -m_run);
       }
-      const bool need_mask = (kb + BN > p.seq_k) || (CAUSAL && kb + BN - 1 > q0 + off);
+      const bool need_mask = (kb + BN > seq_k_rel) || (CAUSAL && kb + BN - 1 > q0 + off_rel);
       if (need_mask) {
         const int ln = fresh_lane();
         const int h = ln >> 5;
-        int lim = p.seq_k - 1 - kb - 4 * h;
-        if (CAUSAL) lim = min(lim, q0 + (ln & 31) + off - kb - 4 * h);
+        int lim = seq_k_rel - 1 - kb - 4 * h;
+        if (CAUSAL) lim = min(lim, q0 + (ln & 31) + off_rel - kb - 4 * h);
 #pragma unroll
         for (int mb = 0; mb < NMB; ++mb)
 #pragma unroll
@@ -618,7 +656,7 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
     //    row-contiguously (16 lanes per 256-byte row), so each store
     //    instruction writes whole cache lines.  The stores are not waited
     //    for here.
-    const float inv = kMfmaRowSum ? 1.f / l_acc[0] : 1.f / sum_xor32((l4[0] + l4[1]) + (l4[2] + l4[3]));
+    float l_row = kMfmaRowSum ? l_acc[0] : sum_xor32((l4[0] + l4[1]) + (l4[2] + l4[3]));
     const int ntb = (tb + n_kt + 1) & 1;  // where the next K_0 went
     if (has_next) {
       if (n_kt == 0)
@@ -626,7 +664,87 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
       else if (group == 1)
         read_next_q();
     }
-    {
+    // 3. A key-split part: each wave merges with the same wave of the tile's
+    //    other part, which holds the same 32 query rows.  The wave stores its
+    //    partial (O^T unnormalised, and per row m, l) in its part's slot,
+    //    waits until the stores have completed, then one lane swaps the
+    //    call's tag into the wave's arrival word.  The wave that finds the tag
+    //    already there arrived second: it loads the other partial, merges the
+    //    two in part order (so the result does not depend on which arrived
+    //    first), clears the word for the next call and writes the output;
+    //    the first wave writes nothing.  Nothing waits on another workgroup.
+    //    Stores and loads of partials and the word are device-coherent (sc1
+    //    stores and loads, a device-scope swap), which orders them across
+    //    XCDs without a cache write-back or invalidate.
+    bool write_out = true;
+    if constexpr (kSplit) {
+      if (cur.kpart) {
+        constexpr uint32_t kWaveBytes = NDB * 4 * 1024 + 512;  // O^T (NDB x 4 float4 per lane), then (m, l)
+        constexpr uint32_t kSlotBytes = 8 * kWaveBytes;
+        constexpr int kSc1 = 16;                               // cache-policy bit sc1
+        const int ln = fresh_lane();
+        char* ws = (char*)p.split_ws;
+        const uint32_t words = ((uint32_t)p.n_split_tiles * 64u + 255u) & ~255u;
+        const __amdgpu_buffer_rsrc_t rs =
+            __builtin_amdgcn_make_buffer_rsrc(ws + words, (short)0, (int)p.split_part_bytes, kBufRsrcWord3);
+        const uint32_t mine = ((uint32_t)cur.sidx * 2u + (uint32_t)(cur.kpart - 1)) * kSlotBytes + (uint32_t)wave * kWaveBytes;
+        const uint32_t theirs = ((uint32_t)cur.sidx * 2u + (uint32_t)(2 - cur.kpart)) * kSlotBytes + (uint32_t)wave * kWaveBytes;
+        const float m_row = fresh ? -INFINITY : m_run;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int rq = 0; rq < 4; ++rq) {
+            const f32x4 v = {o_acc[db][4 * rq], o_acc[db][4 * rq + 1], o_acc[db][4 * rq + 2], o_acc[db][4 * rq + 3]};
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rs,
+                                                   (int)(mine + (uint32_t)(((db * 4 + rq) * 64 + ln) * 16)), 0, kSc1);
+          }
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(m_row), __float_as_uint(l_row)}, rs,
+                                              (int)(mine + NDB * 4 * 1024u + (uint32_t)ln * 8u), 0, kSc1);
+        wait_vmcnt<0>();
+        unsigned long long* word = (unsigned long long*)ws + (int64_t)cur.sidx * 8 + wave;
+        unsigned long long old = 0;
+        if (ln == 0) old = __hip_atomic_exchange(word, (unsigned long long)p.split_token, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        old = ((unsigned long long)(uint32_t)__builtin_amdgcn_readfirstlane((int)(old >> 32)) << 32) |
+              (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)old);
+        write_out = old == p.split_token;
+        if (write_out) {
+          const u32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)(theirs + NDB * 4 * 1024u + (uint32_t)ln * 8u), 0, kSc1);
+          const float m_o = __uint_as_float(ml.x), l_o = __uint_as_float(ml.y);
+          const bool lower = cur.kpart == 1;
+          const float m_a = lower ? m_row : m_o, m_b = lower ? m_o : m_row;
+          const float m = fmaxf(m_a, m_b);
+          const float w_a = fast_exp2(m_a - m), w_b = fast_exp2(m_b - m);
+          // O = O_a w_a + O_b w_b, l likewise (a: the lower part), the same
+          // operations whichever part merges
+          const float l_a = lower ? l_row : l_o, l_b = lower ? l_o : l_row;
+          l_row = fmaf(l_a, w_a, l_b * w_b);
+          constexpr int kChunk = 2;  // d-blocks of the other partial in registers at once
+#pragma unroll
+          for (int d0 = 0; d0 < NDB; d0 += kChunk) {
+            u32x4 t[kChunk][4];
+#pragma unroll
+            for (int db = 0; db < kChunk; ++db)
+#pragma unroll
+              for (int rq = 0; rq < 4; ++rq)
+                t[db][rq] = __builtin_amdgcn_raw_buffer_load_b128(
+                    rs, (int)(theirs + (uint32_t)((((d0 + db) * 4 + rq) * 64 + ln) * 16)), 0, kSc1);
+#pragma unroll
+            for (int db = 0; db < kChunk; ++db)
+#pragma unroll
+              for (int rq = 0; rq < 4; ++rq)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                  const float x_m = o_acc[d0 + db][4 * rq + e], x_t = __uint_as_float(t[db][rq][e]);
+                  const float x_a = lower ? x_m : x_t, x_b = lower ? x_t : x_m;
+                  o_acc[d0 + db][4 * rq + e] = fmaf(x_a, w_a, x_b * w_b);
+                }
+          }
+          if (ln == 0) __hip_atomic_store(word, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
+    const float inv = 1.f / l_row;
+    if (write_out) {
       const int ln = fresh_lane();
       const int lq = ln & 31, h = ln >> 5;
       const int wbase = qbuf + 32 * wq * ROWB;  // this wave's 32 rows
@@ -1186,11 +1304,73 @@ size_t vt_bytes(int batch, int n_kv, int seq_k, int d_k) {
   return (size_t)batch * n_kv * d_k * (size_t)vt_row_keys(seq_k) * 2;
 }
 
-template <typename T, int D>
-int launch_flash_16(FlashParams& p, void* ws, bool causal, hipStream_t st) {
-  // fp16 Q pre-scaled by |sm_scale log2 e| > 1 could overflow: scale scores instead
-  const bool scale_s = std::is_same<T, F16>::value && fabsf(p.scale_log2) > 1.f;
-  p.vt = ws;
+// ---- schedule planning (host) ----------------------------------------------------
+// Partial slot of one key-split part: per wave, O^T unnormalised (D / 2
+// floats per lane) and (m, l) per lane.
+static size_t split_slot_bytes(int D) { return 8u * ((size_t)(D / 32) * 4 * 1024 + 512); }
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// K tiles a whole query tile qt reads (causal: up to its last row's diagonal).
+static int tile_k_tiles(const FlashParams& p, int qt, bool causal) {
+  int k_end = p.seq_k;
+  if (causal) {
+    const int q_last = min(p.seq_q, qt * K16_BM + K16_BM) - 1;
+    k_end = max(0, min(p.seq_k, q_last + (p.seq_k - p.seq_q) + 1));
+  }
+  return (k_end + K16_BN - 1) / K16_BN;
+}
+
+static void set_rounds(FlashParams& p, int cus) {
+  p.q_machines = min((cus + p.n_queues - 1) / p.n_queues, p.q_tiles);
+  const int rounds = p.q_tiles / p.q_machines;
+  p.q_triple = (p.q_tiles % p.q_machines == 0 && rounds % 2 == 1 && rounds >= 3 && p.q_machines % 2 == 0) ? 1 : 0;
+}
+
+// Modelled time of the busiest workgroup, in K steps: a whole tile of n K
+// tiles costs n + 1 (its steps and its tile switch, first G phase and first
+// softmax, which do not overlap), a key-split part its own K tiles + 1.5
+// (the same and the merge); items are dealt as the kernel deals them
+// (decode_item, sched_rank).
+static double busiest_cost(const FlashParams& p) {
+  const double ovh = 1.0;
+  const int off = p.seq_k - p.seq_q;
+  double worst = 0.0;
+  for (int queue = 0; queue < p.n_queues; ++queue)
+    for (int j = 0; j < p.q_machines; ++j) {
+      double sum = 0.0;
+      for (int r = 0;; ++r) {
+        const int i = sched_rank(p, j, r);
+        if (i >= p.q_tiles) break;
+        int b, hq, qt, kpart = 0;
+        if (p.n_entries) {
+          int sidx;
+          decode_item(p, queue, i, p.e_code[i / p.q_parts], b, hq, qt, kpart, sidx);
+        } else {
+          decode_tile(p, queue, i, b, hq, qt);
+        }
+        const int n = tile_k_tiles(p, qt, true);
+        if (kpart == 0) {
+          sum += n + ovh;
+        } else {
+          const int h = min(n / 2, (qt * K16_BM + off) / K16_BN);
+          sum += (kpart == 1 ? h : n - h) + ovh + 0.5;
+        }
+      }
+      worst = fmax(worst, sum);
+    }
+  return worst;
+}
+
+// Tile lists and rounds of flash_fwd_16, and its key split: causal d_k 128
+// calls (seq_k >= seq_q) with fewer tiles than a few rounds of the machine
+// may cut the key range of their s costliest levels in two (one list entry
+// per part), the s that minimises the modelled busiest workgroup, when that
+// beats no split by 5% and the split region (arrival words, then two
+// partial slots per split tile) fits in split_room bytes.  Returns the split
+// region's size (0: no split).  At d_k 64 a step is half the MFMA work while
+// a tile's switch costs about as much, and splits measured no faster
+// (SmolLM2-135M-shaped prompts at batch 2 and 4), so d_k 64 never splits.
+static size_t plan_flash_16_uncached(FlashParams& p, int D, bool causal, size_t split_room, int cus) {
   p.n_qt = (p.seq_q + K16_BM - 1) / K16_BM;
   // Tile lists: one per XCD when the query heads' tiles deal evenly into 8
   // lists of whole parts (q_split parts per head, each n_qt / q_split tiles);
@@ -1208,10 +1388,157 @@ int launch_flash_16(FlashParams& p, void* ws, bool causal, hipStream_t st) {
     }
   }
   p.q_parts = (int)((int64_t)heads * p.q_split / p.n_queues);
-  p.q_tiles = p.q_parts * (p.n_qt / p.q_split);
-  p.q_machines = min((tl_device_cus() + p.n_queues - 1) / p.n_queues, p.q_tiles);
-  const int rounds = p.q_tiles / p.q_machines;
-  p.q_triple = (p.q_tiles % p.q_machines == 0 && rounds % 2 == 1 && rounds >= 3 && p.q_machines % 2 == 0) ? 1 : 0;
+  const int levels = p.n_qt / p.q_split;
+  p.q_tiles = p.q_parts * levels;
+  p.n_entries = 0;
+  p.n_split_levels = 0;
+  p.n_split_tiles = 0;
+  p.split_part_bytes = 0;
+  set_rounds(p, cus);
+  if (!causal || D != 128 || p.seq_k < p.seq_q || tl_overrides.prefill_no_split || levels < 2 ||
+      levels > kMaxEntries / 2 || (int64_t)p.q_tiles * p.n_queues > 4 * (int64_t)cus)
+    return 0;
+  const double base = busiest_cost(p);
+  const double ovh = 1.0;
+  FlashParams best = p;
+  double best_cost = base;
+  size_t best_bytes = 0;
+  // level lvl holds qt = j + q_split (levels - 1 - lvl): every level but the
+  // last has qt >= 1, whose parts both reach every query row
+  for (int s = 1; s < levels; ++s) {
+    FlashParams c = p;
+    const int tiles = p.n_queues * s * p.q_parts;
+    const size_t part_bytes = (size_t)tiles * 2 * split_slot_bytes(D);
+    const size_t bytes = align256((size_t)tiles * 64) + part_bytes;
+    if (bytes > split_room || part_bytes >= ((size_t)1 << 31)) break;
+    // entries: (mean cost, level, part); ordered by cost descending
+    struct Ent { double cost; int lvl, kpart; };
+    Ent ent[kMaxEntries];
+    int n = 0;
+    for (int lvl = 0; lvl < levels; ++lvl) {
+      double whole = 0.0, lo = 0.0, hi = 0.0;
+      for (int j = 0; j < p.q_split; ++j) {
+        const int qt = j + p.q_split * (levels - 1 - lvl);
+        const int k = tile_k_tiles(p, qt, true);
+        const int h = min(k / 2, (qt * K16_BM + p.seq_k - p.seq_q) / K16_BN);
+        whole += k + ovh;
+        lo += h + ovh + 0.5;
+        hi += (k - h) + ovh + 0.5;
+      }
+      if (lvl < s) {
+        ent[n++] = {lo / p.q_split, lvl, 1};
+        ent[n++] = {hi / p.q_split, lvl, 2};
+      } else {
+        ent[n++] = {whole / p.q_split, lvl, 0};
+      }
+    }
+    std::stable_sort(ent, ent + n, [](const Ent& a, const Ent& b) { return a.cost > b.cost; });
+    for (int e = 0; e < n; ++e) c.e_code[e] = (uint8_t)(ent[e].lvl | ent[e].kpart << 6);  // lvl < 32
+    c.n_entries = n;
+    c.n_split_levels = s;
+    c.n_split_tiles = tiles;
+    c.split_part_bytes = (uint32_t)part_bytes;
+    c.q_tiles = p.q_parts * n;
+    set_rounds(c, cus);
+    const double cost = busiest_cost(c);
+    if (cost < best_cost) {
+      best = c;
+      best_cost = cost;
+      best_bytes = bytes;
+    }
+  }
+  if (best_cost > 0.95 * base) return 0;
+  p = best;
+  return best_bytes;
+}
+
+// plan_flash_16_uncached, memoised: a call's plan depends only on the key
+// below (the overrides included), and simulating the candidate
+// splits costs tens of microseconds of host time, more than a short launch.
+static size_t plan_flash_16(FlashParams& p, int D, bool causal, size_t split_room) {
+  struct Key {
+    int batch, n_head, seq_q, seq_k, D, causal, cus, one_list, no_split;
+    size_t room;
+    bool operator==(const Key& o) const {
+      return batch == o.batch && n_head == o.n_head && seq_q == o.seq_q && seq_k == o.seq_k && D == o.D &&
+             causal == o.causal && cus == o.cus && one_list == o.one_list && no_split == o.no_split &&
+             room == o.room;
+    }
+  };
+  struct Entry {
+    Key key;
+    FlashParams plan;
+    size_t bytes;
+  };
+  static std::mutex mu;
+  static Entry cache[16];
+  static int n_cached = 0, next_slot = 0;
+  const int cus = tl_device_cus();
+  const Key key{p.batch,  p.n_head, p.seq_q, p.seq_k, D, causal ? 1 : 0, cus, tl_overrides.prefill_one_list,
+                tl_overrides.prefill_no_split, split_room};
+  auto take = [&p](const FlashParams& c) {  // the schedule fields only
+    p.n_qt = c.n_qt;
+    p.n_queues = c.n_queues;
+    p.q_split = c.q_split;
+    p.q_parts = c.q_parts;
+    p.q_tiles = c.q_tiles;
+    p.q_machines = c.q_machines;
+    p.q_triple = c.q_triple;
+    p.n_entries = c.n_entries;
+    p.n_split_levels = c.n_split_levels;
+    p.n_split_tiles = c.n_split_tiles;
+    p.split_part_bytes = c.split_part_bytes;
+    for (int e = 0; e < kMaxEntries; ++e) p.e_code[e] = c.e_code[e];
+  };
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < n_cached; ++i)
+      if (cache[i].key == key) {
+        take(cache[i].plan);
+        return cache[i].bytes;
+      }
+  }
+  FlashParams c = p;
+  const size_t bytes = plan_flash_16_uncached(c, D, causal, split_room, cus);
+  take(c);
+  std::lock_guard<std::mutex> lock(mu);
+  cache[next_slot] = Entry{key, c, bytes};
+  next_slot = (next_slot + 1) % 16;
+  n_cached = min(n_cached + 1, 16);
+  return bytes;
+}
+
+// This call's arrival tag: a per-process random base plus a call count, so a
+// word left in a reused workspace by an earlier call (or holding unrelated
+// data) is not mistaken for it.  Never 0, the value a merge leaves behind.
+static uint64_t next_split_token() {
+  static const uint64_t base = [] {
+    std::random_device rd;
+    return ((uint64_t)rd() << 32) ^ (uint64_t)rd();
+  }();
+  static std::atomic<uint64_t> count{0};
+  const uint64_t t = base + 2 * (count.fetch_add(1, std::memory_order_relaxed) + 1);
+  return t ? t : 1;
+}
+
+template <typename T, int D>
+int launch_flash_16(FlashParams& p, void* ws, size_t ws_bytes, bool causal, hipStream_t st) {
+  // fp16 Q pre-scaled by |sm_scale log2 e| > 1 could overflow: scale scores instead
+  const bool scale_s = std::is_same<T, F16>::value && fabsf(p.scale_log2) > 1.f;
+  p.vt = ws;
+  // d_k 128 with 64 query rows per wave (tl_prefill_w64.hip): on request
+  // only (TRITON_LLM_HIP_PREFILL_W64); it measures about 8% slower than this
+  // kernel on config 5a.  Not when the scores must be scaled in fp32 (fp16,
+  // large scale); it addresses a wave's 64 output rows with 32-bit offsets.
+  const bool w64 = D == 128 && !scale_s && tl_overrides.prefill_w64 && (64 * p.o_ss + D) * 2 < ((int64_t)1 << 32);
+  const size_t vt_need = D == 64 ? 0 : vt_bytes(p.batch, p.n_kv, p.seq_k, D);
+  const size_t room = ws && aligned16(ws) && ws_bytes > align256(vt_need) ? ws_bytes - align256(vt_need) : 0;
+  p.split_ws = nullptr;
+  p.split_token = 0;
+  if (plan_flash_16(p, D, causal, w64 ? 0 : room)) {
+    p.split_ws = (char*)ws + align256(vt_need);
+    p.split_token = next_split_token();
+  }
   if constexpr (D != 64) {  // d_k 64 reads V in place
     const int vt_tiles = p.sk_pad / 64 * p.n_kv * p.batch;
     const int vt_grid = min(vt_tiles, 2 * tl_device_cus());
@@ -1220,14 +1547,7 @@ int launch_flash_16(FlashParams& p, void* ws, bool causal, hipStream_t st) {
     const int e = tl_launch_status();
     if (e) return e;
   }
-  // d_k 128 with 64 query rows per wave (tl_prefill_w64.hip): on request
-  // only (TRITON_LLM_HIP_PREFILL_W64); it measures about 8% slower than this
-  // kernel on config 5a.  Not when the scores must be scaled in fp32 (fp16,
-  // large scale); it addresses a wave's 64 output rows with 32-bit offsets.
-  if constexpr (D == 128) {
-    const bool w64_ok = (64 * p.o_ss + D) * 2 < ((int64_t)1 << 32);
-    if (!scale_s && tl_overrides.prefill_w64 && w64_ok) return launch_flash_w64(p, T::code, causal, st);
-  }
+  if (w64) return launch_flash_w64(p, T::code, causal, st);
   dim3 grid((unsigned)(p.q_machines * p.n_queues));
   if constexpr (std::is_same<T, F16>::value) {
     if (scale_s) {
@@ -1309,6 +1629,23 @@ size_t tl_attention_fwd_workspace_bytes(int batch, int n_kv_head, int seq_k, int
   return vt_bytes(batch, n_kv_head, seq_k, d_k);
 }
 
+size_t tl_attention_fwd_workspace_bytes_split(int batch, int n_head, int n_kv_head, int seq_q, int seq_k,
+                                              int d_k, int causal, int dtype) {
+  const size_t base = tl_attention_fwd_workspace_bytes(batch, n_kv_head, seq_k, d_k, dtype);
+  if ((dtype != TL_DTYPE_BF16 && dtype != TL_DTYPE_F16) || (d_k != 64 && d_k != 128) || !causal ||
+      batch <= 0 || n_head <= 0 || n_kv_head <= 0 || n_head % n_kv_head || seq_q <= 0 || seq_k <= 0)
+    return base;
+  FlashParams p{};
+  p.batch = batch;
+  p.n_head = n_head;
+  p.n_kv = n_kv_head;
+  p.group = n_head / n_kv_head;
+  p.seq_q = seq_q;
+  p.seq_k = seq_k;
+  const size_t split = plan_flash_16(p, d_k, true, SIZE_MAX);
+  return split ? align256(base) + split : base;
+}
+
 int tl_attention_fwd(const void* q, const void* k, const void* v, void* o, void* workspace,
                      size_t workspace_bytes, int batch, int n_head, int n_kv_head,
                      int seq_q, int seq_k, int d_k, const int64_t* q_strides,
@@ -1348,11 +1685,11 @@ int tl_attention_fwd(const void* q, const void* k, const void* v, void* o, void*
     const size_t need = tl_attention_fwd_workspace_bytes(batch, n_kv_head, seq_k, d_k, dtype);
     if (need && (!workspace || !aligned16(workspace) || workspace_bytes < need)) return TL_ERR_INVALID;
     if (dtype == TL_DTYPE_BF16)
-      return d_k == 64 ? launch_flash_16<BF16, 64>(p, workspace, cz, st)
-                       : launch_flash_16<BF16, 128>(p, workspace, cz, st);
+      return d_k == 64 ? launch_flash_16<BF16, 64>(p, workspace, workspace_bytes, cz, st)
+                       : launch_flash_16<BF16, 128>(p, workspace, workspace_bytes, cz, st);
     if (dtype == TL_DTYPE_F16)
-      return d_k == 64 ? launch_flash_16<F16, 64>(p, workspace, cz, st)
-                       : launch_flash_16<F16, 128>(p, workspace, cz, st);
+      return d_k == 64 ? launch_flash_16<F16, 64>(p, workspace, workspace_bytes, cz, st)
+                       : launch_flash_16<F16, 128>(p, workspace, workspace_bytes, cz, st);
     return TL_ERR_INVALID;
   }
   switch (dtype) {

@@ -59,7 +59,7 @@ int tl_device_cus() {
   return n;
 }
 
-TlOverrides tl_overrides = {0, 0, 0, 0};
+TlOverrides tl_overrides = {0, 0, 0, 0, 0};
 
 namespace {
 int env_int(const char* name) {
@@ -83,6 +83,7 @@ int tl_init(int device) {
   tl_overrides.decode_shares = env_int("TRITON_LLM_HIP_DECODE_SHARES") != 0;
   tl_overrides.prefill_w64 = env_int("TRITON_LLM_HIP_PREFILL_W64") != 0;
   tl_overrides.prefill_one_list = env_int("TRITON_LLM_HIP_PREFILL_ONE_LIST") != 0;
+  tl_overrides.prefill_no_split = env_int("TRITON_LLM_HIP_PREFILL_NO_SPLIT") != 0;
   if (g_stream && g_device == device) return 0;
   hipError_t e = hipSetDevice(device);
   if (e != hipSuccess) return (int)e;

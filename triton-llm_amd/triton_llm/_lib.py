@@ -52,6 +52,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _vp],
     ),
     "tl_attention_fwd_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
+    "tl_attention_fwd_workspace_bytes_split": (
+        _c_size, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
     "tl_attention_fwd": (
         _c_int,
         [_vp, _vp, _vp, _vp, _vp, _c_size,

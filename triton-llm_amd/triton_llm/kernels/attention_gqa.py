@@ -103,7 +103,8 @@ def attention_gqa(
         q_str = _lib.strides(n_head * seq_q * d_k, seq_q * d_k, d_k)
         kv_str = _lib.strides(n_kv_head * seq_k * d_k, seq_k * d_k, d_k)
         lib = gpu.runtime()
-        ws_bytes = lib.tl_attention_fwd_workspace_bytes(1, n_kv_head, seq_k, d_k, code)
+        ws_bytes = lib.tl_attention_fwd_workspace_bytes_split(1, n_head, n_kv_head, seq_q, seq_k, d_k,
+                                                              1 if causal else 0, code)
         ws = shared_workspace("attention_gqa.prefill", ws_bytes)
         launch(lib.tl_attention_fwd, vp(q_dev), vp(k_dev), vp(v_dev), vp(o_dev), vp(ws), ws_bytes,
             1, n_head, n_kv_head, seq_q, seq_k, d_k,

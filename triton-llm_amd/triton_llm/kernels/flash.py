@@ -24,9 +24,19 @@ from ._common import launch, check_status, contiguous_strides, default_scale, sa
 from .attention_gqa import MAX_D
 
 
-def flash_workspace_bytes(batch: int, n_kv_head: int, seq_k: int, d_k: int, dtype) -> int:
-    return gpu.runtime().tl_attention_fwd_workspace_bytes(batch, n_kv_head, seq_k, d_k,
-                                                         gpu.dtype_code(dtype))
+def flash_workspace_bytes(batch: int, n_kv_head: int, seq_k: int, d_k: int, dtype, *,
+                          n_head: int | None = None, seq_q: int | None = None,
+                          causal: bool = True) -> int:
+    """Workspace bytes of a flash call.  Given ``n_head`` and ``seq_q`` too,
+    the size that also lets a causal call split its costliest tiles' key
+    ranges over two workgroups (tl_attention_fwd_workspace_bytes_split);
+    otherwise the minimum."""
+    lib = gpu.runtime()
+    code = gpu.dtype_code(dtype)
+    if n_head is None or seq_q is None:
+        return lib.tl_attention_fwd_workspace_bytes(batch, n_kv_head, seq_k, d_k, code)
+    return lib.tl_attention_fwd_workspace_bytes_split(batch, n_head, n_kv_head, seq_q, seq_k, d_k,
+                                                      1 if causal else 0, code)
 
 
 def flash_attention_strided(q, k, v, out, *, batch, n_head, n_kv_head, seq_q, seq_k, d_k,
@@ -45,7 +55,11 @@ def flash_attention_strided(q, k, v, out, *, batch, n_head, n_kv_head, seq_q, se
     if sm_scale is None:
         sm_scale = default_scale(d_k)
     lib = gpu.runtime()
-    ws_bytes = lib.tl_attention_fwd_workspace_bytes(batch, n_kv_head, seq_k, d_k, code)
+    if workspace is None:  # the shared workspace, large enough to split
+        ws_bytes = lib.tl_attention_fwd_workspace_bytes_split(batch, n_head, n_kv_head, seq_q, seq_k,
+                                                              d_k, 1 if causal else 0, code)
+    else:  # a caller's workspace must hold the minimum; the call splits if it holds more
+        ws_bytes = lib.tl_attention_fwd_workspace_bytes(batch, n_kv_head, seq_k, d_k, code)
     ws = scratch(ws_bytes, workspace, key="flash")
     launch(lib.tl_attention_fwd, vp(q), vp(k), vp(v), vp(out), vp(ws), ws.nbytes if ws is not None else 0,
         batch, n_head, n_kv_head, seq_q, seq_k, d_k,

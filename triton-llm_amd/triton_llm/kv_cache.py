@@ -93,7 +93,10 @@ class GpuKVCache:
         # from here (a stream-ordered device copy, no host synchronisation)
         self._len_table = gpu.to_device(np.arange(self.max_seq + 1, dtype=np.int32))
         self._decode_ws = decode_workspace(1, n_head, n_kv_head, self.max_seq, d_k)
-        wsb = flash_workspace_bytes(1, n_kv_head, self.max_seq, d_k, dtype)
+        # room to split a full-length prompt's costliest tiles (shorter
+        # prompts split as far as it allows)
+        wsb = flash_workspace_bytes(1, n_kv_head, self.max_seq, d_k, dtype, n_head=n_head,
+                                    seq_q=self.max_seq)
         self._prefill_ws = gpu.allocate((wsb,), np.uint8) if wsb else None
 
     @property
