@@ -39,6 +39,7 @@
 #include <algorithm>
 #include <stddef.h>
 #include <atomic>
+#include <chrono>
 #include <mutex>
 #include <random>
 #include <type_traits>
@@ -1513,8 +1514,14 @@ static size_t plan_flash_16(FlashParams& p, int D, bool causal, size_t split_roo
 // data) is not mistaken for it.  Never 0, the value a merge leaves behind.
 static uint64_t next_split_token() {
   static const uint64_t base = [] {
-    std::random_device rd;
-    return ((uint64_t)rd() << 32) ^ (uint64_t)rd();
+    uint64_t b = (uint64_t)std::chrono::steady_clock::now().time_since_epoch().count() * 0x9e3779b97f4a7c15ull ^
+                 (uint64_t)(uintptr_t)&b;
+    try {  // no exception may leave the C ABI
+      std::random_device rd;
+      b ^= ((uint64_t)rd() << 32) ^ (uint64_t)rd();
+    } catch (...) {
+    }
+    return b;
   }();
   static std::atomic<uint64_t> count{0};
   const uint64_t t = base + 2 * (count.fetch_add(1, std::memory_order_relaxed) + 1);
