@@ -25,7 +25,20 @@ TOL = {"float32": 2e-3, "bfloat16": 2e-2}
 @pytest.mark.parametrize("dtype,d_k,n_head,n_kv", [("float32", 64, 9, 3), ("bfloat16", 64, 9, 3),
                                                    ("bfloat16", 128, 24, 8), ("float32", 128, 8, 8)])
 def test_cached_attention_block_prefill_then_decode(dtype, d_k, n_head, n_kv):
-    n_layer, max_seq, prompt, steps = 2, 96, 41, 5
+    run_block(dtype, d_k, n_head, n_kv, n_layer=2, max_seq=96, prompt=41, steps=5)
+
+
+def test_cached_attention_long_prompt_splits_its_tiles():
+    """A 1536-token prompt with Llama-3.2-3B heads: the flash call splits
+    its longest tiles' keys over two workgroups (the cache's workspace has
+    room for a full-length prompt's split), then two decoded tokens."""
+    from triton_llm.kernels.flash import flash_workspace_bytes
+    assert (flash_workspace_bytes(1, 8, 1536, 128, gpu.bfloat16, n_head=24, seq_q=1536)
+            > flash_workspace_bytes(1, 8, 1536, 128, gpu.bfloat16))
+    run_block("bfloat16", 128, 24, 8, n_layer=1, max_seq=2048, prompt=1536, steps=2)
+
+
+def run_block(dtype, d_k, n_head, n_kv, n_layer, max_seq, prompt, steps):
     D = d_k
     cos, sin = orope.precompute_cos_sin(max_seq, D, 1e4)
     cos_d, sin_d = gpu.to_device(cos), gpu.to_device(sin)
