@@ -31,7 +31,7 @@ def pytest_runtest_logstart(nodeid, location):
 def _library_overrides_follow_env():
     """The HIP library reads its test overrides (TRITON_LLM_HIP_MAX_CUS,
     TRITON_LLM_HIP_DECODE_SHARES, TRITON_LLM_HIP_PREFILL_W64,
-    TRITON_LLM_HIP_PREFILL_ONE_LIST) in tl_init,
+    TRITON_LLM_HIP_PREFILL_ONE_LIST, TRITON_LLM_HIP_PREFILL_NO_SPLIT) in tl_init,
     not per launch.  Tests set them
     with tests._helpers.set_override; this fixture is set up before
     monkeypatch and so torn down after it, and re-reads the restored

@@ -106,7 +106,8 @@ def _initialize():
 def reload_overrides():
     """Make the library re-read its test-only environment overrides
     (TRITON_LLM_HIP_MAX_CUS, TRITON_LLM_HIP_DECODE_SHARES,
-    TRITON_LLM_HIP_PREFILL_W64, TRITON_LLM_HIP_PREFILL_ONE_LIST), which it reads
+    TRITON_LLM_HIP_PREFILL_W64, TRITON_LLM_HIP_PREFILL_ONE_LIST,
+    TRITON_LLM_HIP_PREFILL_NO_SPLIT), which it reads
     in tl_init, never per launch.  Does nothing before the first GPU use."""
     if _initialized:
         check_error(_rt.tl_init(int(os.environ.get("TRITON_LLM_DEVICE", "0"))))
