@@ -1328,12 +1328,18 @@ static void set_rounds(FlashParams& p, int cus) {
 }
 
 // Modelled time of the busiest workgroup, in K steps: a whole tile of n K
-// tiles costs n + 1 (its steps and its tile switch, first G phase and first
-// softmax, which do not overlap), a key-split part its own K tiles + 1.5
-// (the same and the merge); items are dealt as the kernel deals them
-// (decode_item, sched_rank).
+// tiles costs n + kTileOvh (its steps and its tile switch, first G phase and
+// first softmax, which do not overlap), a key-split part its own K tiles +
+// kTileOvh + kMergeOvh (the same and the merge); items are dealt as the
+// kernel deals them (decode_item, sched_rank).  The two constants were
+// fitted by timing Llama-3.2-3B-shaped prompts (1024-4096 tokens, 16, 24
+// and 32 query heads) under five settings: (2, 1.5) was best or tied on
+// every shape, e.g. 40.9 against 43.4 us at 2048 tokens with (1, 0.5).
+constexpr double kTileOvh = 2.0;
+constexpr double kMergeOvh = 1.5;
+
 static double busiest_cost(const FlashParams& p) {
-  const double ovh = 1.0;
+  const double ovh = kTileOvh;
   const int off = p.seq_k - p.seq_q;
   double worst = 0.0;
   for (int queue = 0; queue < p.n_queues; ++queue)
@@ -1354,7 +1360,7 @@ static double busiest_cost(const FlashParams& p) {
           sum += n + ovh;
         } else {
           const int h = min(n / 2, (qt * K16_BM + off) / K16_BN);
-          sum += (kpart == 1 ? h : n - h) + ovh + 0.5;
+          sum += (kpart == 1 ? h : n - h) + ovh + kMergeOvh;
         }
       }
       worst = fmax(worst, sum);
@@ -1400,7 +1406,7 @@ static size_t plan_flash_16_uncached(FlashParams& p, int D, bool causal, size_t 
       levels > kMaxEntries / 2 || (int64_t)p.q_tiles * p.n_queues > 4 * (int64_t)cus)
     return 0;
   const double base = busiest_cost(p);
-  const double ovh = 1.0;
+  const double ovh = kTileOvh;
   FlashParams best = p;
   double best_cost = base;
   size_t best_bytes = 0;
@@ -1423,8 +1429,8 @@ static size_t plan_flash_16_uncached(FlashParams& p, int D, bool causal, size_t 
         const int k = tile_k_tiles(p, qt, true);
         const int h = min(k / 2, (qt * K16_BM + p.seq_k - p.seq_q) / K16_BN);
         whole += k + ovh;
-        lo += h + ovh + 0.5;
-        hi += (k - h) + ovh + 0.5;
+        lo += h + ovh + kMergeOvh;
+        hi += (k - h) + ovh + kMergeOvh;
       }
       if (lvl < s) {
         ent[n++] = {lo / p.q_split, lvl, 1};
