@@ -41,7 +41,7 @@ def test_workspace_queries():
     assert lib.tl_attention_fwd_workspace_bytes(2, 3, 100, 64, _lib.DTYPE_F16) == 0
     assert lib.tl_attention_fwd_workspace_bytes(2, 3, 100, 128, _lib.DTYPE_F16) == 2 * 3 * 128 * 128 * 2
     assert lib.tl_attention_fwd_workspace_bytes(1, 1, 100, 32, _lib.DTYPE_BF16) == 0  # generic path
-    # Key-split region: only causal 16-bit d_k 128 calls with seq_k >= seq_q and few
+    # Key-split region: only causal 16-bit MFMA calls with seq_k >= seq_q and few
     # tiles; otherwise the minimum.  (Planned for 256 CUs when no device is visible.)
     fwd, split = lib.tl_attention_fwd_workspace_bytes, lib.tl_attention_fwd_workspace_bytes_split
     BF, F16, F32 = _lib.DTYPE_BF16, _lib.DTYPE_F16, _lib.DTYPE_F32
@@ -57,7 +57,8 @@ def test_workspace_queries():
     assert split(1, 24, 8, 2048, 2048, 128, 0, BF) == base                # not causal
     assert split(1, 24, 8, 2048, 2048, 128, 1, F32) == 0                  # fp32 kernel
     assert split(1, 24, 8, 2048, 1024, 128, 1, BF) == fwd(1, 8, 1024, 128, BF)  # seq_q > seq_k
-    assert split(4, 9, 3, 2048, 2048, 64, 1, BF) == 0                     # d_k 64: never split
+    assert split(2, 9, 3, 2048, 2048, 64, 1, BF) > 0                      # d_k 64, batch 2: split
+    assert split(4, 9, 3, 2048, 2048, 64, 1, BF) == 0                     # config 3: not worth it
     assert split(1, 24, 8, 8192, 8192, 128, 1, BF) == fwd(1, 8, 8192, 128, BF)  # balanced: 5a
     split = lib.tl_decode_split_size(64, 8, 16384)
     assert split % 16 == 0 and 64 <= split <= 4096

@@ -1,5 +1,5 @@
-"""Key-split prefill: causal 16-bit d_k 128 calls with few query tiles split
-the key range of their costliest tiles over two workgroups, which merge in
+"""Key-split prefill: causal 16-bit calls with few query tiles split the key
+range of their costliest tiles over two workgroups, which merge in
 the kernel (tl_attention_fwd_workspace_bytes_split sizes the workspace that
 allows it).  Each case first checks that the call does split (the size query
 asks for more than the minimum), then compares with the oracle (2e-2
@@ -50,6 +50,11 @@ def run(q_d, k_d, v_d, sm_scale, ws, dtype):
     (2, 6, 2, 1000, 1000, 128),    # ragged last query tile, one list
     (1, 8, 4, 700, 1500, 128),     # seq_k > seq_q: bottom-right causal offset
     (1, 12, 4, 1536, 1536, 128),   # GQA group 3, 6 levels
+    (2, 9, 3, 2048, 2048, 64),     # SmolLM2-135M heads at batch 2: d_k 64, V read in place
+    (1, 16, 4, 2048, 2048, 64),
+    (4, 9, 3, 1000, 1000, 64),     # ragged, d_k 64
+    (1, 9, 3, 2048, 2048, 64),     # SmolLM2-135M at batch 1: one list of whole heads, then split
+    (1, 15, 5, 1536, 1536, 64),    # SmolLM2-360M heads at batch 1
 ])
 def test_split_matches_oracle_and_unsplit(monkeypatch, cus, dtype, sm_scale, B, Hq, Hkv, sq, sk, d_k):
     H.set_override(monkeypatch, "TRITON_LLM_HIP_MAX_CUS", cus)

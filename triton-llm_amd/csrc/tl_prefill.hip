@@ -234,9 +234,9 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
                           offsetof(FlashParams, e_code));
     return (int)((tab[e >> 2] >> (8 * (e & 3))) & 0xffu);
   };
-  // Key-split parts exist only for causal d_k 128 (the host plans no split
-  // otherwise); other instances carry none of their code.
-  constexpr bool kSplit = CAUSAL && D == 128;
+  // Key-split parts exist only for causal calls (the host plans no split
+  // otherwise); non-causal instances carry none of their code.
+  constexpr bool kSplit = CAUSAL;
   // A key-split part covers K tiles [kt0, kt0 + n_kt) of its tile: the
   // lower part [0, h), the upper [h, n_kt of the whole tile), h = min(half
   // the tile's K tiles, (first query row + off) / BN), so every query row of
@@ -719,7 +719,7 @@ __global__ __launch_bounds__(K16_THREADS, 2) void flash_fwd_16(FlashParams p) {
           // operations whichever part merges
           const float l_a = lower ? l_row : l_o, l_b = lower ? l_o : l_row;
           l_row = fmaf(l_a, w_a, l_b * w_b);
-          constexpr int kChunk = 2;  // d-blocks of the other partial in registers at once
+          constexpr int kChunk = NDB < 2 ? NDB : 2;  // d-blocks of the other partial in registers at once
 #pragma unroll
           for (int d0 = 0; d0 < NDB; d0 += kChunk) {
             u32x4 t[kChunk][4];
@@ -1368,15 +1368,13 @@ static double busiest_cost(const FlashParams& p) {
   return worst;
 }
 
-// Tile lists and rounds of flash_fwd_16, and its key split: causal d_k 128
-// calls (seq_k >= seq_q) with fewer tiles than a few rounds of the machine
-// may cut the key range of their s costliest levels in two (one list entry
-// per part), the s that minimises the modelled busiest workgroup, when that
+// Tile lists and rounds of flash_fwd_16, and its key split: causal calls
+// (seq_k >= seq_q) with fewer tiles than a few rounds of the machine may cut
+// the key range of their s costliest levels in two (one list entry per
+// part), the s that minimises the modelled busiest workgroup, when that
 // beats no split by 5% and the split region (arrival words, then two
 // partial slots per split tile) fits in split_room bytes.  Returns the split
-// region's size (0: no split).  At d_k 64 a step is half the MFMA work while
-// a tile's switch costs about as much, and splits measured no faster
-// (SmolLM2-135M-shaped prompts at batch 2 and 4), so d_k 64 never splits.
+// region's size (0: no split).
 static size_t plan_flash_16_uncached(FlashParams& p, int D, bool causal, size_t split_room, int cus) {
   p.n_qt = (p.seq_q + K16_BM - 1) / K16_BM;
   // Tile lists: one per XCD when the query heads' tiles deal evenly into 8
@@ -1395,16 +1393,31 @@ static size_t plan_flash_16_uncached(FlashParams& p, int D, bool causal, size_t 
     }
   }
   p.q_parts = (int)((int64_t)heads * p.q_split / p.n_queues);
-  const int levels = p.n_qt / p.q_split;
+  int levels = p.n_qt / p.q_split;
   p.q_tiles = p.q_parts * levels;
   p.n_entries = 0;
   p.n_split_levels = 0;
   p.n_split_tiles = 0;
   p.split_part_bytes = 0;
   set_rounds(p, cus);
-  if (!causal || D != 128 || p.seq_k < p.seq_q || tl_overrides.prefill_no_split || levels < 2 ||
-      levels > kMaxEntries / 2 || (int64_t)p.q_tiles * p.n_queues > 4 * (int64_t)cus)
+  if (!causal || p.seq_k < p.seq_q || tl_overrides.prefill_no_split) return 0;
+  // Per-XCD lists that cut each head into as many parts as it has tiles
+  // leave one cost level, nothing to split (SmolLM2-135M at batch 1: 9
+  // heads, 8 parts each).  Such a call tries one list of whole heads
+  // instead, kept only if a split is worth it.
+  const FlashParams lists = p;
+  if (levels < 2 && p.n_queues > 1 && p.n_qt >= 2) {
+    p.n_queues = 1;
+    p.q_split = 1;
+    p.q_parts = heads;
+    levels = p.n_qt;
+    p.q_tiles = p.q_parts * levels;
+    set_rounds(p, cus);
+  }
+  if (levels < 2 || levels > kMaxEntries / 2 || (int64_t)p.q_tiles * p.n_queues > 4 * (int64_t)cus) {
+    p = lists;
     return 0;
+  }
   const double base = busiest_cost(p);
   const double ovh = kTileOvh;
   FlashParams best = p;
@@ -1454,7 +1467,10 @@ static size_t plan_flash_16_uncached(FlashParams& p, int D, bool causal, size_t 
       best_bytes = bytes;
     }
   }
-  if (best_cost > 0.95 * base) return 0;
+  if (best_cost > 0.95 * base) {
+    p = lists;
+    return 0;
+  }
   p = best;
   return best_bytes;
 }

@@ -58,9 +58,14 @@ def flash_attention_strided(q, k, v, out, *, batch, n_head, n_kv_head, seq_q, se
     if workspace is None:  # the shared workspace, large enough to split
         ws_bytes = lib.tl_attention_fwd_workspace_bytes_split(batch, n_head, n_kv_head, seq_q, seq_k,
                                                               d_k, 1 if causal else 0, code)
-    else:  # a caller's workspace must hold the minimum; the call splits if it holds more
-        ws_bytes = lib.tl_attention_fwd_workspace_bytes(batch, n_kv_head, seq_k, d_k, code)
-    ws = scratch(ws_bytes, workspace, key="flash")
+        ws = scratch(ws_bytes, None, key="flash")
+    else:
+        # a caller's workspace must hold the minimum (which may be 0) and is
+        # always passed on: the call splits if it holds more
+        need = lib.tl_attention_fwd_workspace_bytes(batch, n_kv_head, seq_k, d_k, code)
+        if workspace.nbytes < need:
+            raise ValueError(f"workspace holds {workspace.nbytes} bytes, {need} required")
+        ws = workspace
     launch(lib.tl_attention_fwd, vp(q), vp(k), vp(v), vp(out), vp(ws), ws.nbytes if ws is not None else 0,
         batch, n_head, n_kv_head, seq_q, seq_k, d_k,
         _lib.strides(*q_strides), _lib.strides(*k_strides), _lib.strides(*v_strides),
