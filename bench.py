@@ -18,11 +18,12 @@ passes on this host's cores).
 ``append-5a`` and ``append-3`` time the fused RoPE + KV append at those
 prefill configs' full prompts (what the GPU-resident cache runs before
 prefill attention), HBM-bound, with the oracle's NumPy append as the CPU
-baseline.  ``5a-2048`` times 5a's attention at a 2048-token prompt, where
-the flash kernel splits its longest tiles' key ranges over two workgroups.
+baseline.  ``5a-2048`` (5a's attention at a 2048-token prompt) and ``3-b1``
+(config 3 at batch 1) time shapes on which the flash kernel splits its
+longest tiles' key ranges over two workgroups.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-                       [--config all|5|append|1|2|3|4|5a|5b|append-5a|append-3|5a-2048]
+                       [--config all|5|append|1|2|3|4|5a|5b|append-5a|append-3|5a-2048|3-b1]
 """
 
 from __future__ import annotations
@@ -618,17 +619,19 @@ def append_bytes(cfg):
     return 2 * B * S * (Hq + 2 * Hkv) * D * e + S * D * 4
 
 
-# Extra prefill lines beside the six configs: 5a's heads at a 2048-token
-# prompt, the shape on which flash_fwd_16 splits its longest tiles' keys
-# over two workgroups (192 query tiles for 256 CUs).
-PREFILL_EXTRA = {"5a-2048": ("5a", 2048, "llama3.2-3b-prefill-2048-bf16")}
+# Extra prefill lines beside the six configs, shapes on which flash_fwd_16
+# splits its longest tiles' keys over two workgroups: 5a's heads at a
+# 2048-token prompt (192 query tiles for 256 CUs) and config 3's prompt at
+# batch 1 (72 tiles).
+PREFILL_EXTRA = {"5a-2048": ("5a", {"seq": 2048}, "llama3.2-3b-prefill-2048-bf16"),
+                 "3-b1": ("3", {"batch": 1}, "smollm2-135m-prefill-b1-bf16")}
 
 
 def prefill_extra(name):
     from oracle import inputs as oi
 
-    base, seq, workload = PREFILL_EXTRA[name]
-    return oi.scaled(oi.CONFIGS[base], seq=seq, name=workload)
+    base, fields, workload = PREFILL_EXTRA[name]
+    return oi.scaled(oi.CONFIGS[base], name=workload, **fields)
 
 
 def bench_append(name, steps, warmup, cpu=True, cpu_budget_s=4.0, ramp_ms=0.0):
@@ -856,8 +859,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="all",
                     help="all (default: every BASELINE config, headline 5b, plus the prompt-size RoPE + "
-                         "KV append of 5a and 3 and 5a's attention at 2048 tokens), 5 (5a + 5b), append "
-                         "(both appends), or one of 1 2 3 4 5a 5b append-5a append-3 5a-2048")
+                         "KV append of 5a and 3, 5a at 2048 tokens and 3 at batch 1), 5 (5a + 5b), append "
+                         "(both appends), or one of 1 2 3 4 5a 5b append-5a append-3 5a-2048 3-b1")
     # The GPU's shader clock climbs over the first tens of milliseconds of
     # sustained load: each config first runs its own step untimed for this long
     # (measured: 5 warm-up steps alone left 5a ~10% slow).
@@ -914,7 +917,7 @@ def main():
         print(json.dumps(bench_gemm(min(args.steps, 20), min(args.warmup, 5), cpu=cpu,
                                     vs_rocblas=args.gemm_rocblas)))
         return
-    sel = {"5": ["5a", "5b"], "all": ["1", "2", "3", "4", "5a", "5b", "append-5a", "append-3", "5a-2048"],
+    sel = {"5": ["5a", "5b"], "all": ["1", "2", "3", "4", "5a", "5b", "append-5a", "append-3", "5a-2048", "3-b1"],
            "append": ["append-5a", "append-3"]}.get(args.config, [args.config])
     results = {}
     for name in sel:
