@@ -58,7 +58,8 @@ def test_workspace_queries():
     assert split(1, 24, 8, 2048, 2048, 128, 1, F32) == 0                  # fp32 kernel
     assert split(1, 24, 8, 2048, 1024, 128, 1, BF) == fwd(1, 8, 1024, 128, BF)  # seq_q > seq_k
     assert split(2, 9, 3, 2048, 2048, 64, 1, BF) > 0                      # d_k 64, batch 2: split
-    assert split(4, 9, 3, 2048, 2048, 64, 1, BF) == 0                     # config 3: not worth it
+    assert split(4, 9, 3, 2048, 2048, 64, 1, BF) > 0                      # config 3: one list, split
+    assert split(32, 15, 5, 512, 512, 64, 1, BF) == 0                     # many tiles: balanced
     assert split(1, 24, 8, 8192, 8192, 128, 1, BF) == fwd(1, 8, 8192, 128, BF)  # balanced: 5a
     split = lib.tl_decode_split_size(64, 8, 16384)
     assert split % 16 == 0 and 64 <= split <= 4096

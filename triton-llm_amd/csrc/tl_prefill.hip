@@ -1401,12 +1401,16 @@ static size_t plan_flash_16_uncached(FlashParams& p, int D, bool causal, size_t 
   p.split_part_bytes = 0;
   set_rounds(p, cus);
   if (!causal || p.seq_k < p.seq_q || tl_overrides.prefill_no_split) return 0;
-  // Per-XCD lists that cut each head into as many parts as it has tiles
-  // leave one cost level, nothing to split (SmolLM2-135M at batch 1: 9
-  // heads, 8 parts each).  Such a call tries one list of whole heads
-  // instead, kept only if a split is worth it.
+  // Splits are planned on one list of whole heads (kept only if a split is
+  // worth it) at d_k 64, and wherever the per-XCD lists cut each head into
+  // as many parts as it has tiles, which leaves one cost level and nothing
+  // to split (SmolLM2-135M at batch 1: 9 heads, 8 parts each).  Measured
+  // against splits planned on the per-XCD lists: config 3 33.1 against 34.9
+  // us (unsplit there), SmolLM2-360M heads at batch 2 29.4 against 33.3 us;
+  // at d_k 128 the per-XCD lists were as fast or faster (Llama-3.2-3B at
+  // 1024 and 2048 tokens: 25.8 / 40.6 against 26.5 / 41.2 us).
   const FlashParams lists = p;
-  if (levels < 2 && p.n_queues > 1 && p.n_qt >= 2) {
+  if ((levels < 2 || D == 64) && p.n_queues > 1 && p.n_qt >= 2) {
     p.n_queues = 1;
     p.q_split = 1;
     p.q_parts = heads;
